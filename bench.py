@@ -1,0 +1,273 @@
+"""Benchmark of the four mHC operators on one MI355X.
+
+Workload: the full mHC layer chain at DeepSeek-V3 width,
+N=4, D=7168, T=65536 tokens (B=8, S=8192), bf16 activations, fp32 gates.
+One step = one pass of the hot path over the batch, inputs resident in HBM:
+
+    mhc_pre_clamp_sinkhorn (need_backward)  ->  mhc_post
+    ->  mhc_post_backward  ->  mhc_pre_clamp_sinkhorn_backward
+
+with the chain's data dependencies (post uses this step's Sinkhorn matrix and
+post gates; the pre backward consumes the post backward's grad_h_out,
+grad_h_post and grad_h_res, as for an identity sublayer h_out = y + noise).
+The sublayer add h_out = y + noise and autograd's accumulation of the two
+grad_x contributions are torch glue, not mHC kernels: h_out is formed once
+before timing (it is identical every step), and both glue ops are timed and
+reported separately under "glue".
+
+value = T / (time of one step), tokens/s on one GPU.  The roofline object
+describes the dominant operator, timed with HIP events on the stream it runs
+on; algorithmic bytes follow each operator's compulsory I/O (every input read
+once, every output written once).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "flagos-mhc_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0
+
+
+def algorithmic_bytes(T, N, D, b=2):
+    """Compulsory bytes per operator (each input read once, output written once)."""
+    M = 2 * N + N * N
+    ND = N * D
+    return {
+        "pre_fwd": T * (ND * b + D * b + 4 * (2 * N + 2 * N * N + 1 + M)) + M * ND * b,
+        "post_fwd": T * (2 * ND * b + D * b + 4 * (N * N + N)),
+        "post_bwd": T * (3 * ND * b + 2 * D * b + 8 * (N * N + N)),
+        "pre_bwd": T * (2 * ND * b + D * b + 4 * (1 + M + 2 * N + N * N)) + M * ND * (b + 4),
+    }
+
+
+def make_inputs(T, N, D, dev, seed=0):
+    import torch
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    M = 2 * N + N * N
+    bf = torch.bfloat16
+    x = torch.randn(T, N, D, device=dev, generator=g).to(bf)
+    phi = (torch.randn(M, N * D, device=dev, generator=g) / (N * D) ** 0.5).to(bf)
+    alpha = torch.tensor([0.5, 0.5, 1.0], device=dev)
+    base = torch.randn(M, device=dev, generator=g) * 0.1
+    noise = (torch.randn(T, D, device=dev, generator=g) * 0.1).to(bf)
+    gup = torch.randn(T, N, D, device=dev, generator=g).to(bf)
+    return x, phi, alpha, base, noise, gup
+
+
+def run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
+    out = _pre_forward(x, phi, alpha, base, need_backward=True, want_x_scaled=False, **kw)
+    yp = m.mhc_post(x, out["comb_frag"], h_out, out["post_out"])
+    gx1, g_hres, g_hout, g_hpost = m.mhc_post_backward(gup, x, out["comb_frag"], h_out,
+                                                       out["post_out"])
+    gx2, gphi, ga, gb = m.mhc_pre_clamp_sinkhorn_backward(
+        x, phi, alpha, base, out["inv_rms"], None, out["mixes"], None, out["pre"], g_hout,
+        g_hpost, g_hres, **kw)
+    return out, yp, (gx1, g_hres, g_hout, g_hpost), (gx2, gphi, ga, gb)
+
+
+def time_events(fn, reps, stream):
+    import torch
+
+    ts = []
+    for _ in range(reps):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        fn()
+        e.record(stream)
+        e.synchronize()
+        ts.append(s.elapsed_time(e))
+    return statistics.median(ts), sum(ts) / len(ts)
+
+
+def cpu_baselines(N, D, sample_tokens, ref_tokens):
+    """Oracle chain (numpy float64, one thread) and the package's torch *_ref
+    chain (fp32, all host threads) on bounded token samples of the workload."""
+    import numpy as np
+    import torch
+
+    from oracle import mhc_oracle as orc
+
+    M = 2 * N + N * N
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-10.0, clamp_max=10.0, iter_times=20)
+    r = np.random.default_rng(0)
+
+    def bf(a):
+        return torch.tensor(a, dtype=torch.float32).to(torch.bfloat16).double().numpy()
+
+    Ts = sample_tokens
+    x = bf(r.standard_normal((Ts, N, D), dtype=np.float32))
+    phi = bf(r.standard_normal((M, N * D), dtype=np.float32) / np.sqrt(N * D))
+    alpha = np.array([0.5, 0.5, 1.0])
+    base = r.standard_normal(M) * 0.1
+    noise = bf(r.standard_normal((Ts, D), dtype=np.float32) * 0.1)
+    gup = bf(r.standard_normal((Ts, N, D), dtype=np.float32))
+
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(limits=1)
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        limiter = None
+    t0 = time.perf_counter()
+    out = orc.pre_fwd(x, phi, alpha, base, **kw)
+    h_out = out["y"] + noise
+    orc.post_fwd(x, out["comb_frag"], h_out, out["post_out"])
+    _, g_hres, g_hout, g_hpost = orc.post_bwd(gup, x, out["comb_frag"], h_out, out["post_out"])
+    orc.pre_bwd(x, phi, alpha, base, g_hout, g_hpost, g_hres, **kw)
+    oracle_s = time.perf_counter() - t0
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+
+    import FlagOS_mhc as m
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    Tr = ref_tokens
+    xt = torch.randn(Tr, N, D).to(torch.bfloat16)
+    phit = (torch.randn(M, N * D) / (N * D) ** 0.5).to(torch.bfloat16)
+    at, bt = torch.tensor([0.5, 0.5, 1.0]), torch.randn(M) * 0.1
+    nt = (torch.randn(Tr, D) * 0.1).to(torch.bfloat16)
+    gt = torch.randn(Tr, N, D).to(torch.bfloat16)
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        ro = m.mhc_pre_clamp_sinkhorn_ref(xt, phit, at, bt, **kw)
+        h = ro["y"] + nt
+        m.mhc_post_ref(xt, ro["comb_frag"], h, ro["post_out"])
+        _, ghr, gho, ghp = m.mhc_post_backward_ref(gt, xt, ro["comb_frag"], h, ro["post_out"])
+        m.mhc_pre_clamp_sinkhorn_backward_ref(xt, phit, at, bt, gho, ghp, ghr, **kw)
+        times.append(time.perf_counter() - t0)
+    ref_s = min(times)
+    return (
+        {"value": Ts / oracle_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+         "sample": f"oracle/mhc_oracle.py float64 chain (pre fwd, post fwd, post bwd, pre bwd) "
+                   f"on {Ts} tokens of the N={N} D={D} workload, one thread, {oracle_s:.1f} s"},
+        {"value": Tr / ref_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+         "sample": f"FlagOS_mhc *_ref torch fp32 chain on {Tr} tokens, {threads} threads, "
+                   f"best of 2: {ref_s:.2f} s"},
+    )
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=65536)
+    ap.add_argument("--cpu-sample", type=int, default=3072, help="oracle tokens for cpu_baseline")
+    ap.add_argument("--ref-sample", type=int, default=8192, help="torch *_ref tokens on CPU")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the mHC operators are per-token and this build "
+              f"runs on a single MI355X (asked for --gpus {args.gpus}, WORLD_SIZE={world}). "
+              f"A token-sharded multi-GPU run would only add one all-reduce of "
+              f"grad_phi/alpha/base; it is not measured here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import FlagOS_mhc as m
+    from FlagOS_mhc.mhc_pre_clamp_sinkhorn import _pre_forward
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    N, D, T = 4, 7168, args.tokens
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-10.0, clamp_max=10.0, iter_times=20)
+    x, phi, alpha, base, noise, gup = make_inputs(T, N, D, dev)
+    out = _pre_forward(x, phi, alpha, base, need_backward=True, want_x_scaled=False, **kw)
+    h_out = out["y"] + noise
+    stream = torch.cuda.current_stream(dev)
+
+    step = lambda: run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    # per-operator timing (HIP events on the launch stream)
+    res = run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)
+    o, _, pb, _ = res
+    reps = max(args.steps, 5)
+    ops = {
+        "pre_fwd": lambda: _pre_forward(x, phi, alpha, base, need_backward=True,
+                                        want_x_scaled=False, **kw),
+        "post_fwd": lambda: m.mhc_post(x, o["comb_frag"], h_out, o["post_out"]),
+        "post_bwd": lambda: m.mhc_post_backward(gup, x, o["comb_frag"], h_out, o["post_out"]),
+        "pre_bwd": lambda: m.mhc_pre_clamp_sinkhorn_backward(
+            x, phi, alpha, base, o["inv_rms"], None, o["mixes"], None, o["pre"], pb[2], pb[3],
+            pb[1], **kw),
+    }
+    algo = algorithmic_bytes(T, N, D)
+    op_stats = {}
+    for name, fn in ops.items():
+        fn()
+        med, mean = time_events(fn, reps, stream)
+        gbs = algo[name] / (mean * 1e-3) / 1e9
+        op_stats[name] = {"ms": round(mean, 4), "ms_median": round(med, 4),
+                          "algo_GB": round(algo[name] / 1e9, 4), "GBps": round(gbs, 1),
+                          "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    glue = {
+        "h_out_add_ms": round(time_events(lambda: out["y"] + noise, reps, stream)[1], 4),
+        "grad_x_accumulate_ms": round(time_events(lambda: pb[0] + res[3][0], reps, stream)[1], 4),
+    }
+    dominant = max(op_stats, key=lambda k: op_stats[k]["ms"])
+    dom = op_stats[dominant]
+    mhc_ms = sum(v["ms"] for v in op_stats.values())
+    chain_bytes = sum(algo.values())
+
+    result = {
+        "metric": "fwd+bwd tokens/s and % of 8 TB/s HBM peak, N=4 D=7168 T=65536 bf16, 1 GPU",
+        "value": round(T / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, BASELINE config-5 recipe)",
+        "config": {"workload": "mHC layer chain fwd+bwd (pre, post, post_bwd, pre_bwd)",
+                   "N": N, "D": D, "T": T, "B": 8, "S": T // 8, "clamp": [-10.0, 10.0],
+                   "iter_times": 20, "phi": [2 * N + N * N, N * D]},
+        "hbm_frac_chain": round(chain_bytes / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": dom["GBps"],
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": dom["frac_hbm"],
+                     "traffic": None},
+        "ops": op_stats,
+        "mhc_ops_ms": round(mhc_ms, 4),
+        "glue": glue,
+        "device": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu:
+        cb, rb = cpu_baselines(N, D, args.cpu_sample, args.ref_sample)
+        result["cpu_baseline"] = cb
+        result["ref_cpu_baseline"] = rb
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

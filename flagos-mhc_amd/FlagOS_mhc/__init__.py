@@ -1,0 +1,46 @@
+"""MI355X (gfx950) implementation of the four mHC operators.
+
+Drop-in for the reference package's public API (src/__init__.py:34-47): the
+same twelve names, signatures and return conventions.  The operators run
+hand-written HIP kernels from ``libmhc_amd.so`` (built by
+``flagos-mhc_amd/build.py``) on the current HIP stream; the ``*_ref``
+functions are the pure-PyTorch references of the same semantics.
+
+    mhc_post                       (forward)
+    mhc_post_backward
+    mhc_pre_clamp_sinkhorn         (forward, returns dict)
+    mhc_pre_clamp_sinkhorn_backward
+    mhc_post_fn, mhc_pre_clamp_sinkhorn_fn   (autograd wrappers)
+"""
+
+from .mhc_post import mhc_post, mhc_post_ref
+from .mhc_post_backward import mhc_post_backward, mhc_post_backward_ref
+from .mhc_pre_clamp_sinkhorn import (
+    mhc_pre_clamp_sinkhorn,
+    mhc_pre_clamp_sinkhorn_ref,
+)
+from .mhc_pre_clamp_sinkhorn_backward import (
+    mhc_pre_clamp_sinkhorn_backward,
+    mhc_pre_clamp_sinkhorn_backward_ref,
+)
+from .autograd import (
+    MhcPostFn,
+    MhcPreClampSinkhornFn,
+    mhc_post_fn,
+    mhc_pre_clamp_sinkhorn_fn,
+)
+
+__all__ = [
+    "mhc_post",
+    "mhc_post_ref",
+    "mhc_post_backward",
+    "mhc_post_backward_ref",
+    "mhc_pre_clamp_sinkhorn",
+    "mhc_pre_clamp_sinkhorn_ref",
+    "mhc_pre_clamp_sinkhorn_backward",
+    "mhc_pre_clamp_sinkhorn_backward_ref",
+    "MhcPostFn",
+    "MhcPreClampSinkhornFn",
+    "mhc_post_fn",
+    "mhc_pre_clamp_sinkhorn_fn",
+]

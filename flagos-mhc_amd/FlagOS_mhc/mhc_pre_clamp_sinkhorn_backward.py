@@ -1,0 +1,138 @@
+"""mhc_pre_clamp_sinkhorn_backward: gradients of the pre operator with respect
+to x, phi, alpha and base, for upstream grad_y (of y), grad_post_out and
+grad_comb_frag.
+
+Semantics: torch autograd through the fp32 forward, as the reference's
+mhc_pre_clamp_sinkhorn_backward_ref (src/mhc_pre_clamp_sinkhorn_backward.py:
+1397-1453): clamp gradient passes where clamp_min <= logit <= clamp_max.
+
+The gfx950 path (``mhc_pre_bwd``) takes the forward's saved inv_rms, mixes
+and pre, recomputes the Sinkhorn states per token in registers, and writes
+grad_x once:
+    grad_x = grad_y * pre[n] + inv * (grad_mixes @ phi) + scale * x,
+    scale  = -inv^2 * <grad_mixes, mixes> / (N*D).
+grad_phi = (grad_mixes * inv)^T @ x runs on MFMA split over token ranges and
+is reduced in a fixed order, as are grad_alpha and grad_base, so the result
+is deterministic.  The reference's x_scaled and h_res_logits arguments are
+accepted and not needed (x * inv_rms and the logits are recomputed), so
+passing None is fine.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .mhc_pre_clamp_sinkhorn import SUPPORTED_N, _flatten
+
+
+def mhc_pre_clamp_sinkhorn_backward(
+    x: torch.Tensor,
+    phi: torch.Tensor,
+    alpha: torch.Tensor,
+    base: torch.Tensor,
+    inv_rms: torch.Tensor,
+    x_scaled,
+    mixes: torch.Tensor,
+    h_res_logits,
+    pre: torch.Tensor,
+    grad_y: torch.Tensor,
+    grad_post_out: torch.Tensor,
+    grad_comb_frag: torch.Tensor,
+    norm_eps: float = 1e-6,
+    hc_eps: float = 1e-6,
+    clamp_min: float = 0.0,
+    clamp_max: float = 0.0,
+    iter_times: int = 20,
+):
+    """Returns (grad_x shaped like x in x's dtype, grad_phi (M, N*D) fp32,
+    grad_alpha (3,) fp32, grad_base (M,) fp32)
+    (src/mhc_pre_clamp_sinkhorn_backward.py:1292-1391)."""
+    del x_scaled, h_res_logits, norm_eps  # recomputed / folded into inv_rms
+    _lib.require_device("mhc_pre_clamp_sinkhorn_backward", x, phi, alpha, base, inv_rms, mixes,
+                        pre, grad_y, grad_post_out, grad_comb_frag)
+    if x.dim() not in (3, 4):
+        raise ValueError(f"unsupported x.dim()={x.dim()}")
+    shape = tuple(x.shape)
+    xf, _ = _flatten(x)
+    T, N, D = xf.shape
+    if grad_y.dim() == 3:
+        _B, _S, _D = grad_y.shape
+        assert _B * _S == T and _D == D
+    elif grad_y.dim() == 2:
+        assert tuple(grad_y.shape) == (T, D)
+    else:
+        raise ValueError(f"unsupported grad_y.dim()={grad_y.dim()}")
+    assert N in SUPPORTED_N, f"hc_mult={N} not supported (supported: {SUPPORTED_N})"
+    M = N * (N + 2)
+    assert tuple(phi.shape) == (M, N * D), f"phi shape {tuple(phi.shape)} != {(M, N * D)}"
+    xcode = _lib.dtype_code("mhc_pre_clamp_sinkhorn_backward", xf.dtype)
+    phi_c = phi.contiguous()
+    pcode = _lib.dtype_code("mhc_pre_clamp_sinkhorn_backward (phi)", phi_c.dtype)
+    dev = xf.device
+    f32 = dict(dtype=torch.float32, device=dev)
+
+    gy = grad_y.reshape(T, D).to(xf.dtype).contiguous()
+    gpost = grad_post_out.reshape(T, N).to(torch.float32).contiguous()
+    gcomb = grad_comb_frag.reshape(T, N, N).to(torch.float32).contiguous()
+    inv_c = inv_rms.reshape(T).to(torch.float32).contiguous()
+    mixes_c = mixes.reshape(T, M).to(torch.float32).contiguous()
+    pre_c = pre.reshape(T, N).to(torch.float32).contiguous()
+    alpha_c = alpha.reshape(3).to(torch.float32).contiguous()
+    base_c = base.reshape(M).to(torch.float32).contiguous()
+
+    grad_x = torch.empty((T, N * D), dtype=xf.dtype, device=dev)
+    grad_phi = torch.empty((M, N * D), **f32)
+    grad_alpha = torch.empty((3,), **f32)
+    grad_base = torch.empty((M,), **f32)
+    lib = _lib.load()
+    ws_bytes = int(lib.mhc_pre_bwd_workspace_size(T, N, D, pcode, int(iter_times)))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.mhc_pre_bwd(
+            xf.data_ptr(), xcode, phi_c.data_ptr(), pcode, alpha_c.data_ptr(), base_c.data_ptr(),
+            inv_c.data_ptr(), mixes_c.data_ptr(), pre_c.data_ptr(), gy.data_ptr(),
+            gpost.data_ptr(), gcomb.data_ptr(), float(hc_eps), float(clamp_min),
+            float(clamp_max), int(iter_times), grad_x.data_ptr(), grad_phi.data_ptr(),
+            grad_alpha.data_ptr(), grad_base.data_ptr(), ws.data_ptr(), ws_bytes, T, N, D,
+            _lib.stream_of(xf))
+    _lib.check(rc, "mhc_pre_clamp_sinkhorn_backward")
+    return grad_x.view(*shape), grad_phi.reshape(phi.shape), grad_alpha, grad_base
+
+
+def mhc_pre_clamp_sinkhorn_backward_ref(
+    x, phi, alpha, base,
+    grad_y, grad_post_out, grad_comb_frag,
+    norm_eps=1e-6, hc_eps=1e-6,
+    clamp_min=0.0, clamp_max=0.0,
+    iter_times=20,
+):
+    """Pure-PyTorch reference: autograd through an fp32 restatement of the
+    forward for the loss <grad_y, y> + <grad_post_out, post_out> +
+    <grad_comb_frag, comb_frag> (src/mhc_pre_clamp_sinkhorn_backward.py:
+    1397-1453).  Returns (grad_x in x's dtype, grad_phi, grad_alpha,
+    grad_base) fp32."""
+    orig_dtype = x.dtype
+    leaves = [t.detach().to(torch.float32).requires_grad_(True) for t in (x, phi, alpha, base)]
+    x_, phi_, a, b = leaves
+    xf = x_.reshape(-1, x_.shape[-2], x_.shape[-1])
+    T, N, D = xf.shape
+    x32 = xf.reshape(T, N * D)
+    inv = torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + norm_eps)
+    mixes = (x32 * inv) @ phi_.t()
+    pre = torch.sigmoid(mixes[:, :N] * a[0] + b[:N]) + hc_eps
+    post_out = 2.0 * torch.sigmoid(mixes[:, N:2 * N] * a[1] + b[N:2 * N])
+    logits = (mixes[:, 2 * N:] * a[2] + b[2 * N:]).reshape(T, N, N)
+    lc = torch.clamp(logits, clamp_min, clamp_max) if (clamp_min != 0.0 or clamp_max != 0.0) else logits
+    e = (lc - lc.max(dim=-1, keepdim=True).values).exp()
+    comb = e / e.sum(dim=-1, keepdim=True) + hc_eps
+    comb = comb / (comb.sum(dim=-2, keepdim=True) + hc_eps)
+    for _ in range(iter_times - 1):
+        comb = comb / (comb.sum(dim=-1, keepdim=True) + hc_eps)
+        comb = comb / (comb.sum(dim=-2, keepdim=True) + hc_eps)
+    y = (xf * pre.unsqueeze(-1)).sum(dim=-2)
+    loss = ((y * grad_y.to(torch.float32).reshape(T, D)).sum()
+            + (post_out * grad_post_out.to(torch.float32).reshape(T, N)).sum()
+            + (comb * grad_comb_frag.to(torch.float32).reshape(T, N, N)).sum())
+    dx, dphi, da, db = torch.autograd.grad(loss, leaves)
+    return dx.to(orig_dtype), dphi, da, db

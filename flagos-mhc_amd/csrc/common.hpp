@@ -1,0 +1,169 @@
+// Shared device helpers for the mHC kernels (gfx950 / CDNA4, wave64).
+//
+// * storage-type traits: 16-byte vector loads/stores of bf16 / fp16 / fp32
+//   rows, converted to and from fp32 registers (round-to-nearest-even on store)
+// * wave64 cross-lane reductions
+// * bf16 "plane" splitting of fp32 values for exact-enough MFMA contractions
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mhc {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// scalar conversions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  _Float16 v = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, v);
+}
+
+// ---------------------------------------------------------------------------
+// storage traits.  VEC = elements per 16-byte access.
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+template <typename S> struct Store;
+
+template <> struct Store<bf16_t> {
+  static constexpr int VEC = 8;
+  static constexpr int PLANES = 1;  // bf16 planes needed to hold a value exactly
+  __device__ static float to_f32(uint16_t b) { return bf16_bits_to_f32(b); }
+  __device__ static uint16_t from_f32(float f) { return (uint16_t)f32_to_bf16_bits(f); }
+  // 16-byte vector <-> 8 floats
+  __device__ static void unpack(const u32x4& v, float* o) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(v[i] << 16);
+      o[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+    }
+  }
+  __device__ static u32x4 pack(const float* o) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = f32_to_bf16_bits(o[2 * i]) | (f32_to_bf16_bits(o[2 * i + 1]) << 16);
+    return v;
+  }
+};
+
+template <> struct Store<f16_t> {
+  static constexpr int VEC = 8;
+  static constexpr int PLANES = 2;
+  __device__ static float to_f32(uint16_t b) { return f16_bits_to_f32(b); }
+  __device__ static uint16_t from_f32(float f) { return (uint16_t)f32_to_f16_bits(f); }
+  __device__ static void unpack(const u32x4& v, float* o) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = f16_bits_to_f32(v[i] & 0xffffu);
+      o[2 * i + 1] = f16_bits_to_f32(v[i] >> 16);
+    }
+  }
+  __device__ static u32x4 pack(const float* o) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = f32_to_f16_bits(o[2 * i]) | (f32_to_f16_bits(o[2 * i + 1]) << 16);
+    return v;
+  }
+};
+
+template <> struct Store<float> {
+  static constexpr int VEC = 4;
+  static constexpr int PLANES = 2;
+  __device__ static void unpack(const u32x4& v, float* o) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __uint_as_float(v[i]);
+  }
+  __device__ static u32x4 pack(const float* o) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(o[i]);
+    return v;
+  }
+};
+
+// Element access used by the unaligned (scalar) paths.
+template <typename S> __device__ __forceinline__ float load_elem(const S* p, int64_t i) {
+  return Store<S>::to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+template <> __device__ __forceinline__ float load_elem<float>(const float* p, int64_t i) {
+  return p[i];
+}
+template <typename S> __device__ __forceinline__ void store_elem(S* p, int64_t i, float v) {
+  reinterpret_cast<uint16_t*>(p)[i] = Store<S>::from_f32(v);
+}
+template <> __device__ __forceinline__ void store_elem<float>(float* p, int64_t i, float v) {
+  p[i] = v;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, const u32x4& v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Sum over lanes whose indices differ only in the bits of `mask`
+// (mask is a compile-time set of xor offsets, e.g. 0b0011 -> offsets 1 and 2).
+template <int MASK>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1)
+    if (MASK & o) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+template <int MASK>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1)
+    if (MASK & o) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 planes: v ~= p0 + p1 (+ p2), each a bf16 (returned as raw bits).
+// Two planes leave a relative residual below 2^-17; fp16 inputs are exact.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void split2_bf16(float v, uint32_t& hi, uint32_t& lo) {
+  hi = f32_to_bf16_bits(v);
+  float r = v - bf16_bits_to_f32(hi);
+  lo = f32_to_bf16_bits(r);
+}
+
+}  // namespace mhc

@@ -1,0 +1,625 @@
+// mhc_pre_clamp_sinkhorn backward.
+//
+// Semantics: torch autograd of mhc_pre_clamp_sinkhorn_ref, as the reference's
+// mhc_pre_clamp_sinkhorn_backward_ref does
+// (src/mhc_pre_clamp_sinkhorn_backward.py:1397-1453), for the loss
+// <grad_y, y> + <grad_post_out, post_out> + <grad_comb_frag, comb_frag>.
+//
+// Kernel A (pre_bwd_small_kernel), a block per 16 tokens:
+//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token)
+//   Sinkhorn / softmax / clamp / sigmoid-head VJP, lane per matrix element
+//   -> grad_mixes (T,M) and scale[t] = -inv^2 * <grad_mixes, mixes> / (N*D)
+//   (because <x, grad_mixes @ phi> = <grad_mixes, mixes> / inv), plus a
+//   per-block partial of grad_alpha / grad_base (fixed summation order).
+// Kernel B (pre_bwd_main_kernel), a block per (256 k-columns, token split):
+//   gs = grad_mixes @ phi on MFMA (A = phi^T rows kept in registers,
+//   B = grad_mixes rows from LDS), then
+//   grad_x = grad_y * pre[n] + inv * gs + scale * x, written once;
+//   grad_phi partial += (grad_mixes * inv)^T @ x on MFMA over 32-token
+//   sub-tiles staged in LDS.
+// Kernels C: deterministic reductions of the grad_phi split partials and of
+// the grad_alpha / grad_base block partials (no atomics anywhere).
+#include "mhc_launch.hpp"
+#include "pre_common.hpp"
+#include "pre_host.hpp"
+#include "sinkhorn.hpp"
+
+namespace mhc {
+
+constexpr int kBwdTile = 16;
+constexpr int kBwdThreads = 256;
+constexpr int kMainKC = 256;  // k columns per main-kernel block (all N streams x KC/N widths)
+constexpr int kMainTS = 32;   // tokens per main-kernel sub-tile
+constexpr int kMaxSplits = 16;
+
+// ---------------------------------------------------------------------------
+// Kernel A
+// ---------------------------------------------------------------------------
+struct PreBwdSmallArgs {
+  const void* x;
+  const void* gy;
+  const float* mixes;
+  const float* inv_rms;
+  const float* alpha;
+  const float* base;
+  const float* gpost;
+  const float* gcomb;
+  float hc_eps, cmin, cmax;
+  int apply_clamp;
+  int iters;
+  float* gm;       // (T, M)
+  float* scale;    // (T,)
+  float* partial;  // (gridDim.x, 3 + M)
+  float* sink_scratch;
+  int64_t sink_stride;
+  int64_t T;
+  int D;
+};
+
+template <int N, typename S, bool VEC>
+__global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallArgs a) {
+  using PD = PreDims<N>;
+  constexpr int M = PD::M, L = N * N, C = 3 + M;
+  __shared__ float gp_sh[kBwdTile][N];
+  __shared__ float contrib[kBwdTile][C + 1];
+
+  const S* __restrict__ x = static_cast<const S*>(a.x);
+  const S* __restrict__ gy = static_cast<const S*>(a.gy);
+  const int D = a.D;
+  const int64_t K = (int64_t)N * D;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t t0 = (int64_t)blockIdx.x * kBwdTile;
+
+  // ---- grad_pre: a wave per token ---------------------------------------
+  for (int q = 0; q < kBwdTile / 4; ++q) {
+    const int tt = wave + 4 * q;
+    const int64_t tok = t0 + tt;
+    float acc[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) acc[n] = 0.f;
+    if (tok < a.T) {
+      for (int64_t d = (int64_t)lane * 8; d < D; d += kWave * 8) {
+        float g8[8];
+        load8f<S, VEC>(gy + tok * D, d, D, true, g8);
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+          float x8[8];
+          load8f<S, VEC>(x + (tok * N + n) * D, d, D, true, x8);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
+        }
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
+    if (lane == 0) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) gp_sh[tt][n] = acc[n];
+    }
+  }
+  __syncthreads();
+
+  // ---- small stage, lane per N x N element --------------------------------
+  constexpr int TPP = kBwdThreads / L, PASSES = kBwdTile / TPP;
+  const float a0 = a.alpha[0], a1 = a.alpha[1], a2 = a.alpha[2];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int tt = ps * TPP + tid / L;
+    const int e = tid % L;
+    const int64_t tok = t0 + tt;
+    const bool ok = tok < a.T;
+    const float* mrow = a.mixes + (ok ? tok * M : 0);
+    const float ml = ok ? mrow[2 * N + e] : 0.f;
+    const float logit = ml * a2 + a.base[2 * N + e];
+    const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
+    const float g = ok ? a.gcomb[tok * L + e] : 0.f;
+    float dlc;
+    if (a.iters <= kSinkRegIters)
+      dlc = sinkhorn_vjp_regs<N>(lc, g, a.hc_eps, a.iters);
+    else
+      dlc = sinkhorn_vjp_scratch<N>(lc, g, a.hc_eps, a.iters,
+                                    a.sink_scratch + ((int64_t)blockIdx.x * kBwdTile + tt) * L + e,
+                                    a.sink_stride);
+    // torch.clamp passes the gradient where lo <= logit <= hi (inclusive)
+    if (a.apply_clamp && !(logit >= a.cmin && logit <= a.cmax)) dlc = 0.f;
+    const float gml = dlc * a2;
+
+    float gmh = 0.f, mh = 0.f, dz = 0.f;
+    if (e < 2 * N) {
+      mh = ok ? mrow[e] : 0.f;
+      if (e < N) {
+        const float sp = sigmoidf_(mh * a0 + a.base[e]);
+        dz = gp_sh[tt][e] * sp * (1.0f - sp);
+        gmh = dz * a0;
+      } else {
+        const float so = sigmoidf_(mh * a1 + a.base[e]);
+        const float gpo = ok ? a.gpost[tok * N + (e - N)] : 0.f;
+        dz = gpo * 2.0f * so * (1.0f - so);
+        gmh = dz * a1;
+      }
+    }
+    if (ok) {
+      a.gm[tok * M + 2 * N + e] = gml;
+      if (e < 2 * N) a.gm[tok * M + e] = gmh;
+    }
+    const float sdot = group_sum<L - 1>(gml * ml + gmh * mh);
+    const float c0 = group_sum<L - 1>(e < N ? dz * mh : 0.f);
+    const float c1 = group_sum<L - 1>((e >= N && e < 2 * N) ? dz * mh : 0.f);
+    const float c2 = group_sum<L - 1>(dlc * ml);
+    if (e == 0) {
+      if (ok) {
+        const float inv = a.inv_rms[tok];
+        a.scale[tok] = -inv * inv * sdot / (float)K;
+      }
+      contrib[tt][0] = c0;
+      contrib[tt][1] = c1;
+      contrib[tt][2] = c2;
+    }
+    contrib[tt][3 + 2 * N + e] = dlc;
+    if (e < 2 * N) contrib[tt][3 + e] = dz;
+  }
+  __syncthreads();
+
+  for (int c = tid; c < C; c += kBwdThreads) {
+    float s = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < kBwdTile; ++tt) s += contrib[tt][c];
+    a.partial[(int64_t)blockIdx.x * C + c] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel B
+// ---------------------------------------------------------------------------
+struct PreBwdMainArgs {
+  const void* x;
+  const void* gy;
+  const uint16_t* phiT;  // [P][K][MP32]
+  int64_t phiT_plane_stride;
+  int phi_planes;
+  const float* gm;
+  const float* inv_rms;
+  const float* pre;
+  const float* scale;
+  void* gx;
+  float* gphi_part;  // [nsplit][M][K]
+  int64_t T;
+  int D;
+  int64_t tok_per_split;
+};
+
+template <typename S> struct Raw { typedef uint16_t type; };
+template <> struct Raw<float> { typedef float type; };
+
+template <typename S> __device__ __forceinline__ float raw_to_f32(typename Raw<S>::type v) {
+  return Store<S>::to_f32(v);
+}
+template <> __device__ __forceinline__ float raw_to_f32<float>(float v) { return v; }
+
+// 8 raw elements of a row (element-wise with bound `lim` unless VEC)
+template <typename S, bool VEC>
+__device__ __forceinline__ void copy8_to_lds(const S* src, int64_t lim, bool ok,
+                                             typename Raw<S>::type* dst) {
+  typedef typename Raw<S>::type R;
+  if constexpr (VEC) {
+    if constexpr (sizeof(S) == 2) {
+      const u32x4 v = (ok && lim >= 8) ? ld16(src) : zero4();
+      st16(dst, v);
+    } else {
+      u32x4 v0 = zero4(), v1 = zero4();
+      if (ok && lim >= 8) {
+        v0 = ld16(src);
+        v1 = ld16(src + 4);
+      }
+      st16(dst, v0);
+      st16(dst + 4, v1);
+    }
+  } else {
+    const R* s = reinterpret_cast<const R*>(src);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = (ok && i < lim) ? s[i] : (R)0;
+  }
+}
+
+template <int N, typename S, bool VEC>
+__global__ __launch_bounds__(256) void pre_bwd_main_kernel(PreBwdMainArgs a) {
+  using PD = PreDims<N>;
+  typedef typename Raw<S>::type R;
+  constexpr int M = PD::M, MT = PD::MT, MP = PD::MP, MK = PD::MK, MP32 = PD::MP32;
+  constexpr int KC = kMainKC, DC = KC / N, TS = kMainTS;
+  constexpr int XP = XGroup<S>::PLANES;
+  constexpr int XPITCH = KC + 8, GPITCH = DC + 8, MPITCH = MP32 + 8, TPITCH = TS + 8;
+
+  __shared__ __attribute__((aligned(16))) R xs[TS][XPITCH];
+  __shared__ __attribute__((aligned(16))) R gys[TS][GPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t gmS[2][TS][MPITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t gT[2][MP][TPITCH];
+  __shared__ float pre_sh[TS][N];
+  __shared__ float inv_sh[TS], scale_sh[TS];
+
+  const S* __restrict__ x = static_cast<const S*>(a.x);
+  const S* __restrict__ gy = static_cast<const S*>(a.gy);
+  S* __restrict__ gx = static_cast<S*>(a.gx);
+  const int D = a.D;
+  const int64_t K = (int64_t)N * D;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  const int d0 = blockIdx.x * DC;
+  const int64_t tbeg = (int64_t)blockIdx.y * a.tok_per_split;
+  const int64_t tend = (tbeg + a.tok_per_split < a.T) ? tbeg + a.tok_per_split : a.T;
+  const int P = a.phi_planes;
+
+  // padding rows/columns of the operand tiles stay zero
+  for (int i = tid; i < 2 * TS * MPITCH; i += 256) (&gmS[0][0][0])[i] = 0;
+  for (int i = tid; i < 2 * MP * TPITCH; i += 256) (&gT[0][0][0])[i] = 0;
+
+  // A operands of gs^T = phi^T-rows x grad_mixes^T: MFMA row rr of k-tile q maps to
+  // wave column 16*(rr/4) + 4*q + rr%4, so each lane's outputs cover 16
+  // consecutive columns.
+  u32x4 aphi[4][MK][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int col = wave * 64 + 16 * (r >> 2) + 4 * q + (r & 3);
+    const int n = col / DC, dd = col - (col / DC) * DC;
+    const bool ok = d0 + dd < D;
+    const int64_t kg = (int64_t)n * D + d0 + dd;
+#pragma unroll
+    for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        aphi[q][mk][p] = (ok && p < P)
+                             ? ld16(a.phiT + p * a.phiT_plane_stride + kg * MP32 + 32 * mk + 8 * kq)
+                             : zero4();
+  }
+
+  floatx4 ph[4][MT];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) ph[q][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t tb = tbeg; tb < tend; tb += TS) {
+    __syncthreads();  // previous sub-tile fully consumed
+    // ---- stage the sub-tile -------------------------------------------------
+    constexpr int UPT = N * (DC / 8);  // 8-element units per token row chunk
+    for (int u = tid; u < TS * UPT; u += 256) {
+      const int tt = u / UPT, rem = u - (u / UPT) * UPT;
+      const int n = rem / (DC / 8), dd = (rem - (rem / (DC / 8)) * (DC / 8)) * 8;
+      const int64_t tok = tb + tt;
+      copy8_to_lds<S, VEC>(x + (tok * N + n) * D + d0 + dd, (int64_t)D - d0 - dd, tok < tend,
+                           &xs[tt][n * DC + dd]);
+    }
+    for (int u = tid; u < TS * (DC / 8); u += 256) {
+      const int tt = u / (DC / 8), dd = (u - (u / (DC / 8)) * (DC / 8)) * 8;
+      const int64_t tok = tb + tt;
+      copy8_to_lds<S, VEC>(gy + tok * D + d0 + dd, (int64_t)D - d0 - dd, tok < tend, &gys[tt][dd]);
+    }
+    for (int u = tid; u < TS * M; u += 256) {
+      const int tt = u / M, m = u - (u / M) * M;
+      const int64_t tok = tb + tt;
+      const bool ok = tok < tend;
+      const float v = ok ? a.gm[tok * M + m] : 0.f;
+      const float inv = ok ? a.inv_rms[tok] : 0.f;
+      uint32_t hi, lo;
+      split2_bf16(v, hi, lo);
+      gmS[0][tt][m] = (uint16_t)hi;
+      gmS[1][tt][m] = (uint16_t)lo;
+      split2_bf16(v * inv, hi, lo);
+      gT[0][m][tt] = (uint16_t)hi;
+      gT[1][m][tt] = (uint16_t)lo;
+    }
+    for (int u = tid; u < TS * N; u += 256) {
+      const int tt = u / N, n = u - (u / N) * N;
+      const int64_t tok = tb + tt;
+      pre_sh[tt][n] = tok < tend ? a.pre[tok * N + n] : 0.f;
+    }
+    if (tid < TS) {
+      const int64_t tok = tb + tid;
+      inv_sh[tid] = tok < tend ? a.inv_rms[tok] : 0.f;
+      scale_sh[tid] = tok < tend ? a.scale[tok] : 0.f;
+    }
+    __syncthreads();
+
+    // ---- gs and grad_x ---------------------------------------------------------
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int tt = 16 * h + r;
+      floatx4 gs[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) gs[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mk = 0; mk < MK; ++mk) {
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(&gmS[0][tt][32 * mk + 8 * kq]);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(&gmS[1][tt][32 * mk + 8 * kq]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          gs[q] = mfma16x16x32(as_bf16x8(aphi[q][mk][0]), as_bf16x8(b0), gs[q]);
+          gs[q] = mfma16x16x32(as_bf16x8(aphi[q][mk][0]), as_bf16x8(b1), gs[q]);
+          if (P > 1) gs[q] = mfma16x16x32(as_bf16x8(aphi[q][mk][1]), as_bf16x8(b0), gs[q]);
+        }
+      }
+      const int col0 = wave * 64 + 16 * kq;
+      const int n = col0 / DC, dd0 = col0 - (col0 / DC) * DC;
+      const float pn = pre_sh[tt][n], iv = inv_sh[tt], sc = scale_sh[tt];
+      float o[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float xv = raw_to_f32<S>(xs[tt][col0 + c]);
+        const float gv = raw_to_f32<S>(gys[tt][dd0 + c]);
+        o[c] = fmaf(sc, xv, fmaf(iv, gs[c >> 2][c & 3], gv * pn));
+      }
+      const int64_t tok = tb + tt;
+      if (tok < tend) {
+        S* dst = gx + (tok * N + n) * D + d0;
+        store8<S, VEC>(dst, dd0, (int64_t)D - d0, o);
+        store8<S, VEC>(dst, dd0 + 8, (int64_t)D - d0, o + 8);
+      }
+    }
+
+    // ---- grad_phi partial += (grad_mixes*inv)^T @ x -------------------------
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = wave * 64 + 16 * q + r;
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = raw_to_f32<S>(xs[8 * kq + e][col]);
+      u32x4 bx[2];
+      if constexpr (XP == 1) {
+        // bf16: rebuild the operand from raw bits (exact)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          bx[0][i] = (uint32_t)xs[8 * kq + 2 * i][col] | ((uint32_t)xs[8 * kq + 2 * i + 1][col] << 16);
+        bx[1] = zero4();
+      } else {
+        split8(f, bx[0], bx[1]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 g0 = *reinterpret_cast<const u32x4*>(&gT[0][16 * mt + r][8 * kq]);
+        const u32x4 g1 = *reinterpret_cast<const u32x4*>(&gT[1][16 * mt + r][8 * kq]);
+        ph[q][mt] = mfma16x16x32(as_bf16x8(g0), as_bf16x8(bx[0]), ph[q][mt]);
+        ph[q][mt] = mfma16x16x32(as_bf16x8(g1), as_bf16x8(bx[0]), ph[q][mt]);
+        if constexpr (XP > 1) ph[q][mt] = mfma16x16x32(as_bf16x8(g0), as_bf16x8(bx[1]), ph[q][mt]);
+      }
+    }
+  }
+
+  // ---- write this split's grad_phi partial ---------------------------------
+  float* part = a.gphi_part + (int64_t)blockIdx.y * M * K;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int col = wave * 64 + 16 * q + r;
+    const int n = col / DC, dd = col - (col / DC) * DC;
+    if (d0 + dd >= D) continue;
+    const int64_t kg = (int64_t)n * D + d0 + dd;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 16 * mt + 4 * kq + v;
+        if (m < M) part[(int64_t)m * K + kg] = ph[q][mt][v];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernels C: fixed-order reductions
+// ---------------------------------------------------------------------------
+__global__ void sum_splits_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                  int64_t n, int nsplit) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int j = 0; j < nsplit; ++j) s += part[(int64_t)j * n + i];
+    out[i] = s;
+  }
+}
+
+// One block per column c of partial (rows x C): out = sum over rows.
+__global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ partial,
+                                                       int64_t rows, int C,
+                                                       float* __restrict__ out_alpha,
+                                                       float* __restrict__ out_base) {
+  __shared__ float red[256];
+  const int c = blockIdx.x;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < rows; i += 256) s += partial[i * C + c];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (c < 3)
+      out_alpha[c] = red[0];
+    else
+      out_base[c - 3] = red[0];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct BwdLayout {
+  int M, L, C, P, MP32, nsplit, chunks, DC;
+  int64_t K, nblkA, tok_per_split;
+  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink, total;
+};
+
+static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iters) {
+  BwdLayout b{};
+  b.M = 2 * N + N * N;
+  b.L = N * N;
+  b.C = 3 + b.M;
+  b.P = phi_plane_count(phi_dtype);
+  b.MP32 = (int)round_up(b.M, 32);
+  b.K = (int64_t)N * D;
+  b.DC = kMainKC / N;
+  b.chunks = (int)((D + b.DC - 1) / b.DC);
+  b.nblkA = (T + kBwdTile - 1) / kBwdTile;
+  int ns = (1024 + b.chunks - 1) / b.chunks;
+  if (ns > kMaxSplits) ns = kMaxSplits;
+  const int64_t max_by_t = (T + kMainTS - 1) / kMainTS;
+  if (ns > max_by_t) ns = (int)max_by_t;
+  if (ns < 1) ns = 1;
+  b.tok_per_split = round_up((T + ns - 1) / ns, kMainTS);
+  if (b.tok_per_split < kMainTS) b.tok_per_split = kMainTS;
+  b.nsplit = (int)((T + b.tok_per_split - 1) / b.tok_per_split);
+  if (b.nsplit < 1) b.nsplit = 1;
+  size_t off = 0;
+  b.off_phiT = off;
+  off += align256(phiT_planes_bytes(phi_dtype, b.M, b.K));
+  b.off_gm = off;
+  off += align256((size_t)T * b.M * 4);
+  b.off_scale = off;
+  off += align256((size_t)T * 4);
+  b.off_partial = off;
+  off += align256((size_t)b.nblkA * b.C * 4);
+  b.off_gphi = off;
+  off += align256((size_t)b.nsplit * b.M * b.K * 4);
+  b.off_sink = off;
+  if (iters > kSinkRegIters) off += align256((size_t)(iters - 1) * b.nblkA * kBwdTile * b.L * 4);
+  b.total = off;
+  return b;
+}
+
+template <int N, typename S>
+static int launch_pre_bwd(const BwdLayout& lay, const PreBwdSmallArgs& sa,
+                          const PreBwdMainArgs& ma, float* grad_phi, float* grad_alpha,
+                          float* grad_base, bool vec, hipStream_t st) {
+  const dim3 gA((unsigned)lay.nblkA), bA(kBwdThreads);
+  if (vec)
+    hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, true>), gA, bA, 0, st, sa);
+  else
+    hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, false>), gA, bA, 0, st, sa);
+  int rc = check_launch("pre_bwd_small");
+  if (rc) return rc;
+  const dim3 gB((unsigned)lay.chunks, (unsigned)lay.nsplit), bB(256);
+  if (vec)
+    hipLaunchKernelGGL((pre_bwd_main_kernel<N, S, true>), gB, bB, 0, st, ma);
+  else
+    hipLaunchKernelGGL((pre_bwd_main_kernel<N, S, false>), gB, bB, 0, st, ma);
+  rc = check_launch("pre_bwd_main");
+  if (rc) return rc;
+  const int64_t n = (int64_t)lay.M * lay.K;
+  int64_t g = (n + 255) / 256;
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)g), dim3(256), 0, st, ma.gphi_part, grad_phi, n,
+                     lay.nsplit);
+  rc = check_launch("pre_bwd_sum_splits");
+  if (rc) return rc;
+  hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
+                     lay.nblkA, lay.C, grad_alpha, grad_base);
+  return check_launch("pre_bwd_sum_rows");
+}
+
+template <typename S>
+static int dispatch_pre_bwd(int N, const BwdLayout& lay, const PreBwdSmallArgs& sa,
+                            const PreBwdMainArgs& ma, float* gphi, float* galpha, float* gbase,
+                            bool vec, hipStream_t st) {
+  switch (N) {
+    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, gphi, galpha, gbase, vec, st);
+    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, gphi, galpha, gbase, vec, st);
+  }
+  return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
+}
+
+__global__ void zero_kernel(float* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0.f;
+}
+
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" size_t mhc_pre_bwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype,
+                                             int32_t iter_times) {
+  if (T < 0 || N <= 0 || D <= 0) return 0;
+  return bwd_layout(T, N, D, phi_dtype, iter_times).total;
+}
+
+extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                           const float* alpha, const float* base, const float* inv_rms,
+                           const float* mixes, const float* pre, const void* grad_y,
+                           const float* grad_post_out, const float* grad_comb_frag, float hc_eps,
+                           float clamp_min, float clamp_max, int32_t iter_times, void* grad_x,
+                           float* grad_phi, float* grad_alpha, float* grad_base, void* workspace,
+                           size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                           void* stream) {
+  clear_error();
+  if (T < 0 || D <= 0 || N <= 0)
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
+  if (N != 4 && N != 8) return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
+  if (!phi || !alpha || !base || !grad_phi || !grad_alpha || !grad_base)
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int M = 2 * N + N * N;
+  if (T == 0) {
+    // empty batch: the T-reductions are zero
+    hipLaunchKernelGGL(zero_kernel, dim3(64), dim3(256), 0, st, grad_phi, (int64_t)M * N * D);
+    hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, st, grad_alpha, (int64_t)3);
+    hipLaunchKernelGGL(zero_kernel, dim3(1), dim3(64), 0, st, grad_base, (int64_t)M);
+    return check_launch("pre_bwd_zero");
+  }
+  if (!x || !inv_rms || !mixes || !pre || !grad_y || !grad_post_out || !grad_comb_frag || !grad_x)
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: null pointer");
+  const BwdLayout lay = bwd_layout(T, N, D, phi_dtype, iter_times);
+  if (!workspace || workspace_bytes < lay.total)
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: workspace too small (%zu < %zu bytes)",
+                     workspace_bytes, lay.total);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* phiT = reinterpret_cast<uint16_t*>(ws + lay.off_phiT);
+  int rc = prepare_phiT_planes(phi, phi_dtype, M, lay.K, phiT, st);
+  if (rc) return rc;
+
+  PreBwdSmallArgs sa{};
+  sa.x = x;
+  sa.gy = grad_y;
+  sa.mixes = mixes;
+  sa.inv_rms = inv_rms;
+  sa.alpha = alpha;
+  sa.base = base;
+  sa.gpost = grad_post_out;
+  sa.gcomb = grad_comb_frag;
+  sa.hc_eps = hc_eps;
+  sa.cmin = clamp_min;
+  sa.cmax = clamp_max;
+  sa.apply_clamp = (clamp_min != 0.0f || clamp_max != 0.0f) ? 1 : 0;
+  sa.iters = iter_times;
+  sa.gm = reinterpret_cast<float*>(ws + lay.off_gm);
+  sa.scale = reinterpret_cast<float*>(ws + lay.off_scale);
+  sa.partial = reinterpret_cast<float*>(ws + lay.off_partial);
+  sa.sink_scratch = reinterpret_cast<float*>(ws + lay.off_sink);
+  sa.sink_stride = lay.nblkA * kBwdTile * lay.L;
+  sa.T = T;
+  sa.D = D;
+
+  PreBwdMainArgs ma{};
+  ma.x = x;
+  ma.gy = grad_y;
+  ma.phiT = phiT;
+  ma.phiT_plane_stride = lay.K * lay.MP32;
+  ma.phi_planes = lay.P;
+  ma.gm = sa.gm;
+  ma.inv_rms = inv_rms;
+  ma.pre = pre;
+  ma.scale = sa.scale;
+  ma.gx = grad_x;
+  ma.gphi_part = reinterpret_cast<float*>(ws + lay.off_gphi);
+  ma.T = T;
+  ma.D = D;
+  ma.tok_per_split = lay.tok_per_split;
+
+  const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(grad_y) && aligned16(grad_x);
+  switch (x_dtype) {
+    case MHC_DTYPE_BF16: return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, grad_phi, grad_alpha, grad_base, vec, st);
+    case MHC_DTYPE_F16: return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, grad_phi, grad_alpha, grad_base, vec, st);
+    case MHC_DTYPE_F32: return dispatch_pre_bwd<float>(N, lay, sa, ma, grad_phi, grad_alpha, grad_base, vec, st);
+  }
+  return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: x dtype %d not supported", x_dtype);
+}

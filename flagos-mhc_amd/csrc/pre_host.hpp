@@ -1,0 +1,38 @@
+// Host-side helpers of the pre-op entry points: workspace layout and the
+// preparation of phi as bf16 MFMA operand planes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mhc {
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// bf16 planes needed to carry phi of this dtype (1 for bf16, 2 otherwise).
+inline int phi_plane_count(int32_t phi_dtype) { return phi_dtype == 1 /*MHC_DTYPE_BF16*/ ? 1 : 2; }
+
+// Bytes of phi planes laid out [P][M][round_up(K, 8)].
+inline size_t phi_planes_bytes(int32_t phi_dtype, int M, int64_t K) {
+  return (size_t)phi_plane_count(phi_dtype) * (size_t)M * (size_t)round_up(K, 8) * 2;
+}
+
+// Bytes of transposed phi planes laid out [P][K][MP32], MP32 = M rounded up to 32.
+inline size_t phiT_planes_bytes(int32_t phi_dtype, int M, int64_t K) {
+  return (size_t)phi_plane_count(phi_dtype) * (size_t)K * (size_t)round_up(M, 32) * 2;
+}
+
+// Makes phi available as bf16 planes [P][M][ld].  bf16 phi with K % 8 == 0
+// and a 16-byte aligned base is used in place; anything else is converted
+// into `ws` (which must hold phi_planes_bytes).
+int prepare_phi_planes(const void* phi, int32_t phi_dtype, int M, int64_t K, void* ws,
+                       size_t ws_bytes, const uint16_t** planes, int64_t* ld,
+                       int64_t* plane_stride, int* nplanes, hipStream_t st);
+
+// Writes phi^T as bf16 planes [P][K][MP32] (zero for m >= M) into `dst`.
+int prepare_phiT_planes(const void* phi, int32_t phi_dtype, int M, int64_t K, uint16_t* dst,
+                        hipStream_t st);
+
+}  // namespace mhc

@@ -1,0 +1,120 @@
+/*
+ * mhc_amd.h -- C ABI of the MI355X (gfx950) mHC operator library
+ * (libmhc_amd.so).
+ *
+ * The reference (liuhycs/FlagOS-mhc) is a Python operator package with no
+ * FFI; its boundary is the Python API of src/__init__.py:34-47.  Each entry
+ * point below replaces the device work behind one of its four operators, and
+ * the Python package FlagOS_mhc binds them with ctypes exactly as a
+ * maintainer of the reference would (see FlagOS_mhc/_lib.py).
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers and sizes; the library never allocates or
+ *     frees memory: scratch space is passed in by the caller as `workspace`
+ *     (size from the matching *_workspace_size call);
+ *   - every tensor is contiguous, row-major, in the (T, N, D) token layout
+ *     (T = tokens = B*S, N = streams, D = width); gates and Sinkhorn
+ *     quantities are fp32;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = default stream)
+ *     and nothing synchronises with the host;
+ *   - return MHC_OK (0) or a negative MHC_ERR_* code; mhc_last_error()
+ *     then returns a message (thread-local, valid until the next call);
+ *   - T == 0 is accepted and does nothing.
+ */
+#ifndef MHC_AMD_H_
+#define MHC_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* storage dtypes of activations (x, h_out, y, grads) and of phi */
+#define MHC_DTYPE_F32 0
+#define MHC_DTYPE_BF16 1
+#define MHC_DTYPE_F16 2
+
+#define MHC_OK 0
+#define MHC_ERR_INVALID (-1)     /* bad argument: shape, null pointer, size */
+#define MHC_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. N) */
+#define MHC_ERR_HIP (-3)         /* HIP runtime error (launch failure) */
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* mhc_last_error(void);
+
+/* Library version, major*10000 + minor*100 + patch. */
+int32_t mhc_version(void);
+
+/*
+ * mhc_post forward.  Replaces the device work of mhc_post
+ * (src/mhc_post.py:296-341; semantics of mhc_post_ref, :344-352):
+ *   y[t,i,:] = sum_j h_res[t,j,i] * x[t,j,:] + h_post[t,i] * h_out[t,:]
+ * x, y: (T,N,D) `dtype`; h_out: (T,D) `dtype`; h_res: (T,N,N) fp32;
+ * h_post: (T,N) fp32.  N in {2,4,6,8}.
+ */
+int mhc_post_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                 void* y, int64_t T, int32_t N, int32_t D, int32_t dtype, void* stream);
+
+/*
+ * mhc_post backward.  Replaces the device work of mhc_post_backward
+ * (src/mhc_post_backward.py:593-621; semantics of mhc_post_backward_ref,
+ * :624-643).  grad_y, x, grad_x: (T,N,D) `dtype`; h_out, grad_h_out: (T,D)
+ * `dtype`; h_res, grad_h_res: (T,N,N) fp32; h_post, grad_h_post: (T,N) fp32.
+ */
+int mhc_post_bwd(const void* grad_y, const void* x, const float* h_res, const void* h_out,
+                 const float* h_post, void* grad_x, float* grad_h_res, void* grad_h_out,
+                 float* grad_h_post, int64_t T, int32_t N, int32_t D, int32_t dtype,
+                 void* stream);
+
+/*
+ * mhc_pre_clamp_sinkhorn forward.  Replaces the device work of
+ * mhc_pre_clamp_sinkhorn (src/mhc_pre_clamp_sinkhorn.py:857-971; semantics of
+ * mhc_pre_clamp_sinkhorn_ref, :974-1022): RMSNorm over N*D, the N*D -> M
+ * contraction with phi (M = 2N + N^2), sigmoid heads, optional clamp (on iff
+ * clamp_min != 0 or clamp_max != 0), row softmax and iter_times Sinkhorn
+ * normalisations, y = sum_n x[n] * pre[n].
+ * x: (T,N,D) `x_dtype`; phi: (M, N*D) `phi_dtype`; alpha (3,), base (M,) fp32.
+ * Outputs: y (T,D) `x_dtype`; post_out (T,N), comb_frag (T,N,N) fp32.
+ * Optional outputs (may be NULL): inv_rms (T,), mixes (T,M), h_res_logits
+ * (T,N,N) pre-clamp, pre (T,N), x_scaled (T,N*D) -- all fp32.
+ * N in {4, 8}.  Any D >= 1; D % 8 == 0 with 16-byte aligned rows takes the
+ * vectorised path.
+ */
+size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype);
+int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                const float* alpha, const float* base, float norm_eps, float hc_eps,
+                float clamp_min, float clamp_max, int32_t iter_times, void* y, float* post_out,
+                float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits, float* pre,
+                float* x_scaled, void* workspace, size_t workspace_bytes, int64_t T, int32_t N,
+                int32_t D, void* stream);
+
+/*
+ * mhc_pre_clamp_sinkhorn backward.  Replaces the device work of
+ * mhc_pre_clamp_sinkhorn_backward
+ * (src/mhc_pre_clamp_sinkhorn_backward.py:1292-1391; semantics of
+ * mhc_pre_clamp_sinkhorn_backward_ref, :1397-1453).  Takes the forward's
+ * saved inv_rms (T,), mixes (T,M) and pre (T,N); the reference's x_scaled and
+ * h_res_logits are not needed (x * inv_rms and the logits are recomputed).
+ * grad_y: (T,D) `x_dtype`; grad_post_out (T,N), grad_comb_frag (T,N,N) fp32.
+ * Outputs: grad_x (T,N,D) `x_dtype`; grad_phi (M,N*D), grad_alpha (3,),
+ * grad_base (M,) fp32.  The T-reductions are deterministic (fixed order).
+ * iter_times above 32 keeps the Sinkhorn states in workspace rather than in
+ * registers, which is why the workspace size depends on it.
+ */
+size_t mhc_pre_bwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype,
+                                  int32_t iter_times);
+int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                const float* alpha, const float* base, const float* inv_rms, const float* mixes,
+                const float* pre, const void* grad_y, const float* grad_post_out,
+                const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
+                int32_t iter_times, void* grad_x, float* grad_phi, float* grad_alpha,
+                float* grad_base, void* workspace, size_t workspace_bytes, int64_t T, int32_t N,
+                int32_t D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MHC_AMD_H_ */

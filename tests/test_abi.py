@@ -1,0 +1,108 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point declared in include/mhc_amd.h, rejects bad arguments with the right
+codes before touching the device, and the Python operators refuse CPU
+tensors instead of falling back."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import PKG_DIR, ROOT
+
+HEADER = os.path.join(ROOT, "include", "mhc_amd.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from FlagOS_mhc import _lib
+    if not os.path.exists(_lib.lib_path()):
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("mhc_build", os.path.join(PKG_DIR, "build.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _lib.load()
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mhc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_matches_binding():
+    from FlagOS_mhc import _lib
+    assert sorted(_lib.EXPORTED) == _declared()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    path = lib._name
+    raw = ctypes.CDLL(path)
+    for name in _declared():
+        assert ctypes.cast(getattr(raw, name), ctypes.c_void_p).value
+
+
+def test_version_and_error_string(lib):
+    assert lib.mhc_version() >= 100
+    assert isinstance(lib.mhc_last_error(), bytes)
+
+
+def test_workspace_sizes(lib):
+    assert lib.mhc_pre_fwd_workspace_size(65536, 4, 7168, 1) <= 256  # bf16 phi used in place
+    fp32 = lib.mhc_pre_fwd_workspace_size(65536, 4, 7168, 0)
+    assert fp32 >= 2 * 24 * 28672 * 2
+    ws20 = lib.mhc_pre_bwd_workspace_size(65536, 4, 7168, 1, 20)
+    ws40 = lib.mhc_pre_bwd_workspace_size(65536, 4, 7168, 1, 40)
+    assert ws20 >= 65536 * 24 * 4 and ws40 > ws20
+    assert lib.mhc_pre_bwd_workspace_size(0, 4, 7168, 1, 20) > 0
+
+
+def test_error_codes_without_device(lib):
+    dummy = ctypes.c_void_p(0x1000)
+    # unsupported N is rejected before any launch
+    rc = lib.mhc_post_fwd(dummy, dummy, dummy, dummy, dummy, 16, 3, 64, 1, None)
+    assert rc == -2 and b"N=3" in lib.mhc_last_error()
+    rc = lib.mhc_post_fwd(None, dummy, dummy, dummy, dummy, 16, 4, 64, 1, None)
+    assert rc == -1 and b"null" in lib.mhc_last_error()
+    rc = lib.mhc_post_fwd(dummy, dummy, dummy, dummy, dummy, 16, 4, 64, 7, None)
+    assert rc == -2
+    rc = lib.mhc_pre_fwd(dummy, 1, dummy, 1, dummy, dummy, 1e-6, 1e-6, 0.0, 0.0, 20,
+                         dummy, dummy, dummy, None, None, None, None, None, None, 0,
+                         16, 6, 64, None)
+    assert rc == -2
+    rc = lib.mhc_pre_bwd(dummy, 1, dummy, 1, dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                         dummy, 1e-6, 0.0, 0.0, 20, dummy, dummy, dummy, dummy, dummy, 16,
+                         16, 4, 64, None)
+    assert rc == -1 and b"workspace" in lib.mhc_last_error()
+    # T == 0 is a no-op for the forward ops
+    assert lib.mhc_post_fwd(dummy, dummy, dummy, dummy, dummy, 0, 4, 64, 1, None) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    import FlagOS_mhc as m
+    x = torch.zeros(16, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="HIP"):
+        m.mhc_post(x, torch.zeros(16, 4, 4), torch.zeros(16, 64, dtype=torch.bfloat16),
+                   torch.zeros(16, 4))
+    phi = torch.zeros(24, 256)
+    with pytest.raises(RuntimeError, match="HIP"):
+        m.mhc_pre_clamp_sinkhorn(x, phi, torch.zeros(3), torch.zeros(24))
+
+
+def test_public_api_names():
+    import FlagOS_mhc as m
+    assert m.__all__ == [
+        "mhc_post", "mhc_post_ref", "mhc_post_backward", "mhc_post_backward_ref",
+        "mhc_pre_clamp_sinkhorn", "mhc_pre_clamp_sinkhorn_ref",
+        "mhc_pre_clamp_sinkhorn_backward", "mhc_pre_clamp_sinkhorn_backward_ref",
+        "MhcPostFn", "MhcPreClampSinkhornFn", "mhc_post_fn", "mhc_pre_clamp_sinkhorn_fn",
+    ]
+    for name in m.__all__:
+        assert callable(getattr(m, name))

@@ -1,0 +1,186 @@
+"""GPU parity of mhc_pre_clamp_sinkhorn and its backward (HIP kernels via the
+C ABI) against the fp64 oracle on token subsets and at small sizes, against
+the package's fp32 ``*_ref`` functions run on the GPU at the BASELINE sizes,
+and end to end through the autograd wrappers.
+
+Tolerances (north star): fp32 Sinkhorn / mix outputs rtol 1e-4 (atol 1e-5
+for entries near zero); bf16 tensors rtol 2e-2 / atol 2e-2 of an fp32 or
+better reference; the fp32 T-reductions grad_phi / grad_alpha / grad_base
+rtol 1e-3 with atol 1e-4 * max|ref| (fp32 sums over up to 65536 tokens)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import FlagOS_mhc as m
+from oracle import mhc_oracle as orc
+from test_gpu_post import DEV, _gen, _np, _subset, assert_close
+
+pytestmark = pytest.mark.gpu
+
+FWD_KEYS = ("post_out", "comb_frag", "inv_rms", "mixes", "h_res_logits", "pre")
+
+
+def pre_inputs(T, N, D, dtype=torch.bfloat16, phi_dtype=torch.bfloat16, seed=0, recipe="baseline"):
+    g = _gen(seed)
+    M = 2 * N + N * N
+    if recipe == "baseline":
+        x = torch.randn(T, N, D, device=DEV, generator=g).to(dtype)
+        phi = (torch.randn(M, N * D, device=DEV, generator=g) / (N * D) ** 0.5).to(phi_dtype)
+        alpha = torch.tensor([0.5, 0.5, 1.0], device=DEV)
+        base = torch.randn(M, device=DEV, generator=g) * 0.1
+    else:                      # reference test recipe (tests/test_correctness.py:74-79)
+        x = (torch.randn(T, N, D, device=DEV, generator=g) * 0.1).to(dtype)
+        phi = (torch.randn(M, N * D, device=DEV, generator=g) * 0.1).to(phi_dtype)
+        alpha = torch.tensor([0.5, 0.5, 0.5], device=DEV)
+        base = torch.randn(M, device=DEV, generator=g) * 0.01
+    gy = torch.randn(T, D, device=DEV, generator=g).to(dtype)
+    gpost = torch.randn(T, N, device=DEV, generator=g)
+    gcomb = torch.randn(T, N, N, device=DEV, generator=g)
+    return x, phi, alpha, base, gy, gpost, gcomb
+
+
+def _oracle_fwd(idx, x, phi, alpha, base, kw):
+    return orc.pre_fwd(_np(x[idx]), _np(phi), _np(alpha), _np(base), **kw)
+
+
+def check_fwd(out, want, dtype, idx=None, what=""):
+    sel = (lambda t: t[idx]) if idx is not None else (lambda t: t)
+    assert_close(sel(out["y"].reshape(-1, out["y"].shape[-1])), want["y"], 2e-2, 2e-2, what + " y")
+    for k in FWD_KEYS:
+        w = want[k] if isinstance(want[k], np.ndarray) else _np(want[k])
+        assert_close(sel(out[k]), w, 1e-4, 1e-5, what + " " + k)
+
+
+FWD_CASES = [
+    # T, N, D, x dtype, phi dtype, recipe, clamp, iters
+    (16384, 4, 4096, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),   # config 3
+    (32768, 8, 2048, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),   # config 4
+    (16, 4, 64, torch.bfloat16, torch.float32, "reftest", 3.0, 20),           # reference test
+    (16, 4, 64, torch.bfloat16, torch.float32, "reftest", 0.0, 20),           # clamp disabled
+    (50, 4, 100, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),       # D % 8 != 0
+    (37, 4, 96, torch.float16, torch.float16, "baseline", 10.0, 7),
+    (29, 4, 64, torch.float32, torch.float32, "baseline", 2.0, 20),
+    (21, 8, 128, torch.bfloat16, torch.float32, "reftest", 3.0, 1),
+    (64, 4, 256, torch.bfloat16, torch.bfloat16, "baseline", 1.0, 0),
+    (48, 4, 128, torch.bfloat16, torch.bfloat16, "baseline", 0.5, 45),        # > 32 iterations
+]
+
+
+@pytest.mark.parametrize("T,N,D,dtype,phi_dtype,recipe,clamp,iters", FWD_CASES)
+def test_pre_fwd_parity(T, N, D, dtype, phi_dtype, recipe, clamp, iters):
+    print(f"[pre_fwd] T={T} N={N} D={D} {dtype} phi={phi_dtype} clamp={clamp} it={iters}", flush=True)
+    x, phi, alpha, base, *_ = pre_inputs(T, N, D, dtype, phi_dtype, recipe=recipe)
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-clamp, clamp_max=clamp, iter_times=iters)
+    out = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **kw)
+    torch.cuda.synchronize()
+    assert out["y"].dtype == dtype and out["y"].shape == (T, D)
+    idx = _subset(T)
+    want = _oracle_fwd(idx, x, phi, alpha, base, kw)
+    check_fwd(out, want, dtype, idx, "oracle:")
+    assert_close(out["x_scaled"][idx], want["x_scaled"], 1e-5, 1e-6, "x_scaled")
+    if T * N * D >= 1 << 24:   # whole output against the package's fp32 *_ref on the GPU
+        ref = m.mhc_pre_clamp_sinkhorn_ref(x, phi, alpha, base, **kw)
+        check_fwd(out, ref, dtype, None, "ref:")
+    # need_backward=False returns exactly the three outputs, same values
+    small = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=False, **kw)
+    assert set(small) == {"y", "post_out", "comb_frag"}
+    for k in small:
+        assert torch.equal(small[k], out[k])
+
+
+def test_pre_fwd_bsnd_shape():
+    B, S, N, D = 2, 8, 4, 64
+    x, phi, alpha, base, *_ = pre_inputs(B * S, N, D, recipe="reftest", phi_dtype=torch.float32)
+    out = m.mhc_pre_clamp_sinkhorn(x.reshape(B, S, N, D), phi, alpha, base, clamp_min=-3.0,
+                                   clamp_max=3.0)
+    assert out["y"].shape == (B, S, D)
+    assert out["post_out"].shape == (B * S, N) and out["comb_frag"].shape == (B * S, N, N)
+
+
+BWD_CASES = [
+    (16384, 4, 4096, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),   # config 3 sizes
+    (32768, 8, 2048, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),   # config 4
+    (16, 4, 64, torch.bfloat16, torch.float32, "reftest", 3.0, 20),           # reference test
+    (50, 4, 100, torch.bfloat16, torch.bfloat16, "baseline", 0.5, 20),        # D % 8 != 0, clamp active
+    (37, 4, 96, torch.float16, torch.float16, "baseline", 10.0, 7),
+    (29, 8, 64, torch.float32, torch.float32, "baseline", 2.0, 20),
+    (70, 4, 128, torch.bfloat16, torch.bfloat16, "baseline", 0.0, 40),        # scratch Sinkhorn path
+    (33, 8, 96, torch.bfloat16, torch.bfloat16, "reftest", 0.2, 1),
+]
+
+
+@pytest.mark.parametrize("T,N,D,dtype,phi_dtype,recipe,clamp,iters", BWD_CASES)
+def test_pre_bwd_parity(T, N, D, dtype, phi_dtype, recipe, clamp, iters):
+    print(f"[pre_bwd] T={T} N={N} D={D} {dtype} phi={phi_dtype} clamp={clamp} it={iters}", flush=True)
+    x, phi, alpha, base, gy, gpost, gcomb = pre_inputs(T, N, D, dtype, phi_dtype, recipe=recipe)
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-clamp, clamp_max=clamp, iter_times=iters)
+    out = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **kw)
+    gx, gphi, ga, gb = m.mhc_pre_clamp_sinkhorn_backward(
+        x, phi, alpha, base, out["inv_rms"], out["x_scaled"], out["mixes"], out["h_res_logits"],
+        out["pre"], gy, gpost, gcomb, **kw)
+    torch.cuda.synchronize()
+    assert gx.dtype == dtype and gx.shape == x.shape
+    assert gphi.dtype == torch.float32 and gphi.shape == phi.shape
+    if T <= 128:
+        want = orc.pre_bwd(_np(x), _np(phi), _np(alpha), _np(base), _np(gy), _np(gpost),
+                           _np(gcomb), **kw)
+    else:
+        ref = m.mhc_pre_clamp_sinkhorn_backward_ref(x, phi, alpha, base, gy, gpost, gcomb, **kw)
+        want = [_np(t) for t in ref]
+        idx = _subset(T)
+        # per-token grad_x also against the oracle on a subset (the T-reductions need all tokens)
+        sub = orc.pre_bwd(_np(x[idx]), _np(phi), _np(alpha), _np(base), _np(gy[idx]),
+                          _np(gpost[idx]), _np(gcomb[idx]), **kw)
+        assert_close(gx[idx], sub[0], 2e-2, 2e-2, "grad_x subset vs oracle")
+    assert_close(gx, want[0], 2e-2, 2e-2, "grad_x")
+    for got, w, name in ((gphi, want[1], "grad_phi"), (ga, want[2], "grad_alpha"), (gb, want[3], "grad_base")):
+        assert_close(got, w, 1e-3, 1e-4 * np.abs(w).max(), name)
+    # deterministic: no atomics anywhere
+    again = m.mhc_pre_clamp_sinkhorn_backward(
+        x, phi, alpha, base, out["inv_rms"], None, out["mixes"], None, out["pre"], gy, gpost,
+        gcomb, **kw)
+    for a, b in zip(again, (gx, gphi, ga, gb)):
+        assert torch.equal(a, b)
+
+
+def test_pre_bwd_empty_batch():
+    N, D = 4, 64
+    x, phi, alpha, base, *_ = pre_inputs(1, N, D)
+    e = lambda *s: torch.empty(*s, device=DEV)
+    gx, gphi, ga, gb = m.mhc_pre_clamp_sinkhorn_backward(
+        x[:0], phi, alpha, base, e(0), None, e(0, 24), None, e(0, N),
+        torch.empty(0, D, dtype=x.dtype, device=DEV), e(0, N), e(0, N, N))
+    torch.cuda.synchronize()
+    assert gx.shape == (0, N, D)
+    assert not gphi.any() and not ga.any() and not gb.any()
+
+
+@pytest.mark.parametrize("N", [4, 8])
+def test_autograd_chain(N):
+    """pre -> h_out = y + noise -> post -> loss, through the autograd wrappers,
+    against the same chain through the package's *_ref functions in fp32."""
+    T, D = 96, 128
+    x, phi, alpha, base, *_ = pre_inputs(T, N, D, recipe="baseline")
+    g = _gen(5)
+    noise = (torch.randn(T, D, device=DEV, generator=g) * 0.1).to(x.dtype)
+    upstream = torch.randn(T, N, D, device=DEV, generator=g).to(x.dtype)
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-10.0, clamp_max=10.0, iter_times=20)
+
+    leaves = [t.clone().requires_grad_(True) for t in (x, phi, alpha, base)]
+    y, post, comb = m.mhc_pre_clamp_sinkhorn_fn(*leaves, **kw)
+    out = m.mhc_post_fn(leaves[0], comb, y + noise, post)
+    (out.float() * upstream.float()).sum().backward()
+
+    rl = [t.detach().float().requires_grad_(True) for t in (x, phi, alpha, base)]
+    r = m.mhc_pre_clamp_sinkhorn_ref(*rl, **kw)
+    r_out = m.mhc_post_ref(rl[0], r["comb_frag"], r["y"] + noise.float(), r["post_out"])
+    (r_out * upstream.float()).sum().backward()
+
+    assert_close(out, r_out, 2e-2, 2e-2, "chain output")
+    assert_close(leaves[0].grad, rl[0].grad, 2e-2, 2e-2, "x.grad")
+    for a, b, name in ((leaves[1], rl[1], "phi"), (leaves[2], rl[2], "alpha"), (leaves[3], rl[3], "base")):
+        w = _np(b.grad)
+        assert_close(a.grad.float(), w, 2e-2, 2e-3 * np.abs(w).max(), name + ".grad")
