@@ -19,6 +19,8 @@
 //   sub-tiles staged in LDS.
 // Kernels C: deterministic reductions of the grad_phi split partials and of
 // the grad_alpha / grad_base block partials (no atomics anywhere).
+#include <type_traits>
+
 #include "mhc_launch.hpp"
 #include "pre_common.hpp"
 #include "pre_host.hpp"
@@ -47,8 +49,13 @@ struct PreBwdSmallArgs {
   float hc_eps, cmin, cmax;
   int apply_clamp;
   int iters;
-  float* gm;       // (T, M)
-  float* scale;    // (T,)
+  const float* pre;
+  float* gm;       // (T, M) fp32, or null
+  float* scale;    // (T,), or null
+  uint16_t* gmP;   // [2][T][MP32] bf16 planes of grad_mixes, or null
+  int64_t gmP_plane;
+  uint16_t* gTw;   // [ceil(T/16)][2][MP][16] bf16 planes of grad_mixes * inv
+  float4* coef;    // (T, N) {pre, inv, scale, 0}, or null
   float* partial;  // (gridDim.x, 3 + M)
   float* sink_scratch;
   int64_t sink_stride;
@@ -139,19 +146,50 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
         gmh = dz * a1;
       }
     }
-    if (ok) {
+    const float inv = ok ? a.inv_rms[tok] : 0.f;
+    if (ok && a.gm) {
       a.gm[tok * M + 2 * N + e] = gml;
       if (e < 2 * N) a.gm[tok * M + e] = gmh;
+    }
+    if (ok && a.gmP) {
+      // operand layouts of the streaming kernel: grad_mixes as bf16 planes
+      // [2][T][MP32] and g = grad_mixes * inv as token-transposed 16-token
+      // tiles [T/16][2][MP][16]; padding rows m >= M are zero
+      constexpr int MP32 = PD::MP32, MP = PD::MP;
+      uint16_t* gmP = a.gmP + tok * MP32;
+      uint16_t* gTw = a.gTw + (tok >> 4) * (2 * MP * 16) + (tok & 15);
+      uint32_t hi, lo;
+      split2_bf16(gml, hi, lo);
+      gmP[2 * N + e] = (uint16_t)hi;
+      gmP[a.gmP_plane + 2 * N + e] = (uint16_t)lo;
+      split2_bf16(gml * inv, hi, lo);
+      gTw[(2 * N + e) * 16] = (uint16_t)hi;
+      gTw[(MP + 2 * N + e) * 16] = (uint16_t)lo;
+      if (e < 2 * N) {
+        split2_bf16(gmh, hi, lo);
+        gmP[e] = (uint16_t)hi;
+        gmP[a.gmP_plane + e] = (uint16_t)lo;
+        split2_bf16(gmh * inv, hi, lo);
+        gTw[e * 16] = (uint16_t)hi;
+        gTw[(MP + e) * 16] = (uint16_t)lo;
+      }
+      if (e < MP32 - M) {
+        gmP[M + e] = 0;
+        gmP[a.gmP_plane + M + e] = 0;
+      }
+      if (e < MP - M) {
+        gTw[(M + e) * 16] = 0;
+        gTw[(MP + M + e) * 16] = 0;
+      }
     }
     const float sdot = group_sum<L - 1>(gml * ml + gmh * mh);
     const float c0 = group_sum<L - 1>(e < N ? dz * mh : 0.f);
     const float c1 = group_sum<L - 1>((e >= N && e < 2 * N) ? dz * mh : 0.f);
     const float c2 = group_sum<L - 1>(dlc * ml);
+    const float scale = -inv * inv * sdot / (float)K;
+    if (ok && a.coef && e < N) a.coef[tok * N + e] = float4{a.pre[tok * N + e], inv, scale, 0.f};
     if (e == 0) {
-      if (ok) {
-        const float inv = a.inv_rms[tok];
-        a.scale[tok] = -inv * inv * sdot / (float)K;
-      }
+      if (ok && a.scale) a.scale[tok] = scale;
       contrib[tt][0] = c0;
       contrib[tt][1] = c1;
       contrib[tt][2] = c2;
@@ -405,6 +443,194 @@ __global__ __launch_bounds__(256) void pre_bwd_main_kernel(PreBwdMainArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Kernel B, streaming form (bf16 activations, 16-byte aligned rows)
+//
+// A block has one wave per stream n and owns DW = 16*VC columns d of every
+// stream; it walks 16-token tiles t = split, split + nsplit, ... so every
+// block of the persistent grid gets the same work.  Lane (r = lane%16,
+// q = lane/16) loads, for the 4 tokens 4q..4q+3 of a tile, the VC columns
+// d0 + VC*r.. of x[t, n, :] and grad_y[t, :] (one coalesced load per row),
+// i.e. a 4 x VC bf16 block held in registers:
+//   * grad_phi (MFMA 16x16x16, reduction over the 16 tokens): the block is
+//     transposed in registers (16-bit shuffles inside the lane) so that its
+//     column c is a B operand (4 tokens of one column); A = (grad_mixes*inv)^T
+//     read from token-transposed 16-token tiles.  MFMA instance c covers the
+//     columns VC*r + c, r = 0..15.
+//   * gs = grad_mixes @ phi (MFMA 16x16x32, reduction over m): A = the 16
+//     tokens' grad_mixes rows, B = phi^T rows kept in registers for the whole
+//     kernel.  Output lane (r, q) holds tokens 4q..4q+3 of columns VC*r + c:
+//     exactly the rows of x and grad_y the lane loaded, so
+//     grad_x = grad_y*pre + inv*gs + scale*x is formed and stored in place.
+// No LDS and no barriers: each wave streams independently.
+// ---------------------------------------------------------------------------
+template <int N> struct StreamCfg {
+  static constexpr int VC = (N == 4) ? 8 : 4;  // columns per lane
+  static constexpr int DW = 16 * VC;           // columns per block and stream
+};
+
+constexpr int kStreamTile = 16;  // tokens per tile (MFMA K of the grad_phi product)
+
+struct PreBwdStreamArgs {
+  const bf16_t* x;
+  const bf16_t* gy;
+  const uint16_t* phiT;  // [P][K][MP32]
+  int64_t phiT_plane_stride;
+  int phi_planes;
+  const uint16_t* gmP;   // [2][T][MP32]
+  int64_t gmP_plane;
+  const uint16_t* gTw;   // [ceil(T/16)][2][MP][16]
+  const float4* coef;    // (T, N) {pre, inv, scale, 0}
+  bf16_t* gx;
+  float* gphi_part;      // [nsplit][M][K]
+  int64_t T;
+  int D;
+  int nsplit;
+};
+
+template <int VD> struct RowVec;
+template <> struct RowVec<4> { typedef u32x4 type; };
+template <> struct RowVec<2> { typedef u32x2 type; };
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma16x16x16(const u32x2& a, const u32x2& b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, a),
+                                                  __builtin_bit_cast(short4_t, b), c, 0, 0, 0);
+}
+
+template <int N, int P>
+__global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs a) {
+  using PD = PreDims<N>;
+  constexpr int M = PD::M, MT = PD::MT, MP = PD::MP, MK = PD::MK, MP32 = PD::MP32;
+  constexpr int VC = StreamCfg<N>::VC, DW = StreamCfg<N>::DW, VD = VC / 2;
+  constexpr int TT = kStreamTile;
+  typedef typename RowVec<VD>::type Row;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int D = a.D;
+  const int64_t K = (int64_t)N * D, T = a.T;
+  const int dl = blockIdx.x * DW + VC * r;  // first column d of this lane
+  const bool colok = dl < D;                // D % VC == 0 on this path
+  const int64_t kcol = (int64_t)n * D + dl;
+
+  u32x4 pb[VC][MK][P];
+#pragma unroll
+  for (int c = 0; c < VC; ++c)
+#pragma unroll
+    for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        pb[c][mk][p] = colok
+                           ? ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q)
+                           : zero4();
+
+  floatx4 ph[MT][VC];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t ntiles = (T + TT - 1) / TT;
+  for (int64_t tile = blockIdx.y; tile < ntiles; tile += a.nsplit) {
+    const int64_t tb = tile * TT, tg = tb + 4 * q;
+    Row xr[4], gr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t t = tg + e;
+      Row zx = {}, zg = {};
+      if (colok && t < T) {
+        zx = __builtin_nontemporal_load(reinterpret_cast<const Row*>(a.x + (t * N + n) * D + dl));
+        zg = *reinterpret_cast<const Row*>(a.gy + t * D + dl);
+      }
+      xr[e] = zx;
+      gr[e] = zg;
+    }
+    const int64_t ts = tb + r;  // token of MFMA row r in the gs product
+    u32x4 gA[MK][2];
+#pragma unroll
+    for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+        gA[mk][g] = ts < T ? ld16(a.gmP + g * a.gmP_plane + ts * MP32 + 32 * mk + 8 * q) : zero4();
+    int nv = (int)(T - tg);
+    nv = nv < 0 ? 0 : (nv > 4 ? 4 : nv);
+    u32x2 ga[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        u32x2 v = *reinterpret_cast<const u32x2*>(a.gTw + ((tile * 2 + g) * MP + 16 * mt + r) * TT + 4 * q);
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+          v[w] &= (2 * w < nv ? 0xffffu : 0u) | (2 * w + 1 < nv ? 0xffff0000u : 0u);
+        ga[mt][g] = v;
+      }
+
+    // ---- grad_phi partial += g^T @ x over this tile's 16 tokens -----------
+#pragma unroll
+    for (int c = 0; c < VC; ++c) {
+      // column c of the lane's 4 x VC block: tokens (2w, 2w+1) in dword w
+      u32x2 xt;
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const uint32_t lo = xr[2 * w][c >> 1], hi = xr[2 * w + 1][c >> 1];
+        xt[w] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        ph[mt][c] = mfma16x16x16(ga[mt][0], xt, ph[mt][c]);
+        ph[mt][c] = mfma16x16x16(ga[mt][1], xt, ph[mt][c]);
+      }
+    }
+
+    // ---- gs = grad_mixes @ phi and grad_x ----------------------------------
+    floatx4 gs[VC];
+#pragma unroll
+    for (int c = 0; c < VC; ++c) {
+      gs[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mk = 0; mk < MK; ++mk) {
+        gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][0]), gs[c]);
+        gs[c] = mfma16x16x32(as_bf16x8(gA[mk][1]), as_bf16x8(pb[c][mk][0]), gs[c]);
+        if constexpr (P > 1)
+          gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][P - 1]), gs[c]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t t = tg + e;
+      if (!(colok && t < T)) continue;
+      const float4 cf = a.coef[t * N + n];  // pre[t,n], inv[t], scale[t]
+      Row o;
+#pragma unroll
+      for (int w = 0; w < VD; ++w) {
+        const uint32_t xw = xr[e][w], gw = gr[e][w];
+        const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
+        const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
+        const float o0 = fmaf(cf.z, x0, fmaf(cf.y, gs[2 * w][e], g0 * cf.x));
+        const float o1 = fmaf(cf.z, x1, fmaf(cf.y, gs[2 * w + 1][e], g1 * cf.x));
+        o[w] = pack_bf16x2(o0, o1);
+      }
+      *reinterpret_cast<Row*>(a.gx + (t * N + n) * D + dl) = o;
+    }
+  }
+
+  if (!colok) return;
+  float* part = a.gphi_part + (int64_t)blockIdx.y * M * K;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 16 * mt + 4 * q + v;
+      if (m >= M) continue;
+#pragma unroll
+      for (int c = 0; c < VC; ++c) part[(int64_t)m * K + kcol + c] = ph[mt][c][v];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Kernels C: fixed-order reductions
 // ---------------------------------------------------------------------------
 __global__ void sum_splits_kernel(const float* __restrict__ part, float* __restrict__ out,
@@ -444,22 +670,28 @@ __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__
 // host side
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int M, L, C, P, MP32, nsplit, chunks, DC;
-  int64_t K, nblkA, tok_per_split;
-  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink, total;
+  int M, L, C, P, MP, MP32, nsplit, chunks, DC;
+  int64_t K, nblkA, tok_per_split, ntiles;
+  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink;
+  size_t off_gmP, off_gTw, off_coef, total;
 };
 
+// Workspace layout.  It covers both forms of kernel B (the streaming one for
+// bf16 activations and the LDS-staged one for the other dtypes / unaligned
+// rows), so the size depends only on (T, N, D, phi dtype, iterations).
 static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iters) {
   BwdLayout b{};
   b.M = 2 * N + N * N;
   b.L = N * N;
   b.C = 3 + b.M;
-  b.P = phi_plane_count(phi_dtype);
+  b.P = phi_bwd_planes(phi_dtype);
+  b.MP = (int)round_up(b.M, 16);
   b.MP32 = (int)round_up(b.M, 32);
   b.K = (int64_t)N * D;
   b.DC = kMainKC / N;
   b.chunks = (int)((D + b.DC - 1) / b.DC);
   b.nblkA = (T + kBwdTile - 1) / kBwdTile;
+  b.ntiles = (T + kStreamTile - 1) / kStreamTile;
   int ns = (1024 + b.chunks - 1) / b.chunks;
   if (ns > kMaxSplits) ns = kMaxSplits;
   const int64_t max_by_t = (T + kMainTS - 1) / kMainTS;
@@ -479,24 +711,99 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   b.off_partial = off;
   off += align256((size_t)b.nblkA * b.C * 4);
   b.off_gphi = off;
-  off += align256((size_t)b.nsplit * b.M * b.K * 4);
+  off += align256((size_t)kMaxSplits * b.M * b.K * 4);
+  b.off_gmP = off;
+  off += align256((size_t)2 * T * b.MP32 * 2);
+  b.off_gTw = off;
+  off += align256((size_t)b.ntiles * 2 * b.MP * kStreamTile * 2);
+  b.off_coef = off;
+  off += align256((size_t)T * N * 16);
   b.off_sink = off;
   if (iters > kSinkRegIters) off += align256((size_t)(iters - 1) * b.nblkA * kBwdTile * b.L * 4);
   b.total = off;
   return b;
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cache[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+template <int N, int P>
+static int stream_blocks_per_cu() {
+  static int cache = 0;
+  if (!cache) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pre_bwd_stream_kernel<N, P>, 64 * N, 0) != hipSuccess || nb <= 0)
+      nb = 1;
+    cache = nb;
+  }
+  return cache;
+}
+
+template <int N, int P>
+static int launch_stream(const BwdLayout& lay, PreBwdStreamArgs& sta, hipStream_t st) {
+  constexpr int DW = StreamCfg<N>::DW;
+  const int chunks = (int)((lay.K / N + DW - 1) / DW);
+  int64_t ns = (int64_t)device_cus() * stream_blocks_per_cu<N, P>() / chunks;
+  if (ns > kMaxSplits) ns = kMaxSplits;
+  if (ns > lay.ntiles) ns = lay.ntiles;
+  if (ns < 1) ns = 1;
+  sta.nsplit = (int)ns;
+  hipLaunchKernelGGL((pre_bwd_stream_kernel<N, P>), dim3((unsigned)chunks, (unsigned)ns),
+                     dim3(64 * N), 0, st, sta);
+  return check_launch("pre_bwd_stream");
+}
+
+static int reduce_tail(const BwdLayout& lay, const PreBwdSmallArgs& sa, const float* gphi_part,
+                       int nsplit, float* grad_phi, float* grad_alpha, float* grad_base,
+                       hipStream_t st) {
+  const int64_t n = (int64_t)lay.M * lay.K;
+  int64_t g = (n + 255) / 256;
+  if (g > 8192) g = 8192;
+  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)g), dim3(256), 0, st, gphi_part, grad_phi, n,
+                     nsplit);
+  int rc = check_launch("pre_bwd_sum_splits");
+  if (rc) return rc;
+  hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
+                     lay.nblkA, lay.C, grad_alpha, grad_base);
+  return check_launch("pre_bwd_sum_rows");
+}
+
 template <int N, typename S>
-static int launch_pre_bwd(const BwdLayout& lay, const PreBwdSmallArgs& sa,
-                          const PreBwdMainArgs& ma, float* grad_phi, float* grad_alpha,
+static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwdMainArgs& ma,
+                          PreBwdStreamArgs sta, float* grad_phi, float* grad_alpha,
                           float* grad_base, bool vec, hipStream_t st) {
   const dim3 gA((unsigned)lay.nblkA), bA(kBwdThreads);
+  const bool streaming = vec && std::is_same<S, bf16_t>::value;
+  if (streaming) {
+    sa.gm = nullptr;
+    sa.scale = nullptr;
+  } else {
+    sa.gmP = nullptr;
+    sa.gTw = nullptr;
+    sa.coef = nullptr;
+  }
   if (vec)
     hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, true>), gA, bA, 0, st, sa);
   else
     hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, false>), gA, bA, 0, st, sa);
   int rc = check_launch("pre_bwd_small");
   if (rc) return rc;
+  if (streaming) {
+    rc = lay.P == 1 ? launch_stream<N, 1>(lay, sta, st) : launch_stream<N, 2>(lay, sta, st);
+    if (rc) return rc;
+    return reduce_tail(lay, sa, sta.gphi_part, sta.nsplit, grad_phi, grad_alpha, grad_base, st);
+  }
   const dim3 gB((unsigned)lay.chunks, (unsigned)lay.nsplit), bB(256);
   if (vec)
     hipLaunchKernelGGL((pre_bwd_main_kernel<N, S, true>), gB, bB, 0, st, ma);
@@ -504,25 +811,16 @@ static int launch_pre_bwd(const BwdLayout& lay, const PreBwdSmallArgs& sa,
     hipLaunchKernelGGL((pre_bwd_main_kernel<N, S, false>), gB, bB, 0, st, ma);
   rc = check_launch("pre_bwd_main");
   if (rc) return rc;
-  const int64_t n = (int64_t)lay.M * lay.K;
-  int64_t g = (n + 255) / 256;
-  if (g > 8192) g = 8192;
-  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)g), dim3(256), 0, st, ma.gphi_part, grad_phi, n,
-                     lay.nsplit);
-  rc = check_launch("pre_bwd_sum_splits");
-  if (rc) return rc;
-  hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
-                     lay.nblkA, lay.C, grad_alpha, grad_base);
-  return check_launch("pre_bwd_sum_rows");
+  return reduce_tail(lay, sa, ma.gphi_part, lay.nsplit, grad_phi, grad_alpha, grad_base, st);
 }
 
 template <typename S>
 static int dispatch_pre_bwd(int N, const BwdLayout& lay, const PreBwdSmallArgs& sa,
-                            const PreBwdMainArgs& ma, float* gphi, float* galpha, float* gbase,
-                            bool vec, hipStream_t st) {
+                            const PreBwdMainArgs& ma, const PreBwdStreamArgs& sta, float* gphi,
+                            float* galpha, float* gbase, bool vec, hipStream_t st) {
   switch (N) {
-    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, gphi, galpha, gbase, vec, st);
-    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, gphi, galpha, gbase, vec, st);
+    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, st);
+    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
 }
@@ -591,8 +889,13 @@ extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int3
   sa.cmax = clamp_max;
   sa.apply_clamp = (clamp_min != 0.0f || clamp_max != 0.0f) ? 1 : 0;
   sa.iters = iter_times;
+  sa.pre = pre;
   sa.gm = reinterpret_cast<float*>(ws + lay.off_gm);
   sa.scale = reinterpret_cast<float*>(ws + lay.off_scale);
+  sa.gmP = reinterpret_cast<uint16_t*>(ws + lay.off_gmP);
+  sa.gmP_plane = T * lay.MP32;
+  sa.gTw = reinterpret_cast<uint16_t*>(ws + lay.off_gTw);
+  sa.coef = reinterpret_cast<float4*>(ws + lay.off_coef);
   sa.partial = reinterpret_cast<float*>(ws + lay.off_partial);
   sa.sink_scratch = reinterpret_cast<float*>(ws + lay.off_sink);
   sa.sink_stride = lay.nblkA * kBwdTile * lay.L;
@@ -615,11 +918,26 @@ extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int3
   ma.D = D;
   ma.tok_per_split = lay.tok_per_split;
 
+  PreBwdStreamArgs sta{};
+  sta.x = static_cast<const bf16_t*>(x);
+  sta.gy = static_cast<const bf16_t*>(grad_y);
+  sta.phiT = phiT;
+  sta.phiT_plane_stride = lay.K * lay.MP32;
+  sta.phi_planes = lay.P;
+  sta.gmP = sa.gmP;
+  sta.gmP_plane = sa.gmP_plane;
+  sta.gTw = sa.gTw;
+  sta.coef = sa.coef;
+  sta.gx = static_cast<bf16_t*>(grad_x);
+  sta.gphi_part = ma.gphi_part;
+  sta.T = T;
+  sta.D = D;
+
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(grad_y) && aligned16(grad_x);
   switch (x_dtype) {
-    case MHC_DTYPE_BF16: return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, grad_phi, grad_alpha, grad_base, vec, st);
-    case MHC_DTYPE_F16: return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, grad_phi, grad_alpha, grad_base, vec, st);
-    case MHC_DTYPE_F32: return dispatch_pre_bwd<float>(N, lay, sa, ma, grad_phi, grad_alpha, grad_base, vec, st);
+    case MHC_DTYPE_BF16: return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, st);
+    case MHC_DTYPE_F16: return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, st);
+    case MHC_DTYPE_F32: return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: x dtype %d not supported", x_dtype);
 }

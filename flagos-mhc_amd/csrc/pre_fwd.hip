@@ -2,22 +2,25 @@
 //
 // Semantics: mhc_pre_clamp_sinkhorn_ref, src/mhc_pre_clamp_sinkhorn.py:974-1022.
 //
-// A block (4 waves) owns a tile of 16 tokens:
+// A block (4 waves) owns a tile of 64 tokens (4 row blocks of 16):
 //   1. contraction  acc[t,m] = sum_k x[t,k] * phi[m,k]  (k = n*D + d) on bf16
-//      MFMA 16x16x32 (A = 16 tokens x 32 k of x, B = 32 k x 16 m of phi^T),
-//      the four waves splitting k; the same pass accumulates sum(x^2).
-//      Each lane reads 32 consecutive k of its token row (four 16-byte loads),
-//      and the four MFMAs of a step consume those groups in the same order
-//      for A and B, so the reduction over k is unaffected by the grouping.
-//      mixes = inv_rms * acc, the identity used by the reference's
+//      MFMA 16x16x32: A = 16 tokens x 32 k of x, B = 32 k x 16 m of phi^T.
+//      The 4 waves take the 128-column steps of K round-robin, each for all
+//      4 row blocks, so a phi operand fetched from L2 serves 64 tokens; the
+//      waves' partial sums are reduced through LDS once at the end.  A lane
+//      reads 32 consecutive k of its token row (four 16-byte loads streamed
+//      past the caches, issued without branches); the four MFMAs of a step
+//      consume those groups in the same order for A and B, so the reduction
+//      over k is unaffected by the grouping.  The same pass accumulates
+//      sum(x^2); mixes = inv_rms * acc, the identity used by the reference's
 //      need_backward=False path (src/mhc_pre_clamp_sinkhorn.py:914-916).
 //   2. per-token heads and Sinkhorn, one lane per N x N element (sinkhorn.hpp).
-//   3. y[t,:] = sum_n pre[t,n] * x[t,n,:], re-reading the tile's x (recently
-//      fetched, so mostly served by L2 / the MALL), and optionally the fp32
-//      x_scaled = x * inv_rms of the reference's need_backward dict.
-// fp16 / fp32 activations and fp16 / fp32 phi are split into two bf16 planes
-// each; the products hi*hi + hi*lo + lo*hi keep the contraction within 2^-16
-// relative of fp32.
+//   3. y[t,:] = sum_n pre[t,n] * x[t,n,:], a second pass over the tile's x,
+//      and optionally the fp32 x_scaled = x * inv_rms of the reference's
+//      need_backward dict.
+// fp16 activations / phi are split exactly into two bf16 planes, fp32 ones
+// into three; plane products whose indices sum above 2 are dropped, which
+// keeps the contraction within ~2^-24 relative of an fp32 dot product.
 #include "mhc_launch.hpp"
 #include "pre_common.hpp"
 #include "pre_host.hpp"
@@ -25,15 +28,15 @@
 
 namespace mhc {
 
-constexpr int kPreTile = 16;
-constexpr int kPreThreads = 256;
+constexpr int kFwdTile = 64;  // tokens per block
+constexpr int kFwdThreads = 256;
 
 struct PreFwdArgs {
   const void* x;
-  const uint16_t* phi;       // bf16 planes [P][M][ld]
+  const uint16_t* phi;       // bf16 planes [P][M][ld], P <= 3
   int64_t phi_ld;            // row length of a plane (>= K, multiple of 8)
   int64_t phi_plane_stride;  // elements between planes
-  int phi_planes;            // 1 or 2
+  int phi_planes;            // 1, 2 or 3
   const float* alpha;
   const float* base;
   float norm_eps, hc_eps, cmin, cmax;
@@ -51,99 +54,165 @@ struct PreFwdArgs {
   int D;
 };
 
-template <int N, typename S, bool VEC>
-__global__ __launch_bounds__(kPreThreads) void pre_fwd_kernel(PreFwdArgs a) {
+template <int N, typename S, bool VEC, int P>
+__global__ __launch_bounds__(kFwdThreads) void pre_fwd_kernel(PreFwdArgs a) {
   using PD = PreDims<N>;
-  constexpr int M = PD::M, MT = PD::MT, MP = PD::MP;
   constexpr int XP = XGroup<S>::PLANES;
+  constexpr int M = PD::M, MT = PD::MT, MP = PD::MP;
   constexpr int L = N * N;
+  constexpr int RB = kFwdTile / 16;  // 16-token row blocks, all handled by every wave
 
-  __shared__ floatx4 red[4][MT][kWave];
-  __shared__ float ssq_sh[4][kPreTile];
-  __shared__ float mix_sh[kPreTile][MP + 1];
-  __shared__ float pre_sh[kPreTile][N];
-  __shared__ float inv_sh[kPreTile];
+  __shared__ floatx4 red[4][RB][MT][kWave];
+  __shared__ float ssq_sh[4][kFwdTile];
+  __shared__ float mix_sh[kFwdTile][MP + 1];
+  __shared__ float pre_sh[kFwdTile][N];
+  __shared__ float inv_sh[kFwdTile];
 
   const S* __restrict__ x = static_cast<const S*>(a.x);
   const int D = a.D;
   const int64_t K = (int64_t)N * D;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, kq = lane >> 4;
-  const int64_t t0 = (int64_t)blockIdx.x * kPreTile;
-  const bool row_ok = (t0 + r) < a.T;
-  const S* xrow = x + (row_ok ? (t0 + r) * K : 0);
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * kFwdTile;
 
-  // ---- 1. contraction + sum of squares ----------------------------------
-  floatx4 acc[MT];
+  // row r of each row block; rows past T read row T-1 (and are zeroed)
+  const S* xrow[RB];
+  bool row_ok[RB];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float ssq = 0.f;
-  const int P = a.phi_planes;
+  for (int rb = 0; rb < RB; ++rb) {
+    const int64_t t = t0 + 16 * rb + r;
+    row_ok[rb] = t < a.T;
+    xrow[rb] = x + (row_ok[rb] ? t : a.T - 1) * K;
+  }
+  // phi row 16*mt + r of each plane; rows m >= M read row M-1 (and are zeroed)
+  const uint16_t* prow[MT];
+  bool m_ok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r;
+    m_ok[mt] = m < M;
+    prow[mt] = a.phi + (m_ok[mt] ? m : M - 1) * a.phi_ld;
+  }
 
+  // ---- 1. contraction + sum of squares ------------------------------------
+  // Wave w takes the 128-column steps w, w+4, w+8, ...; lane (r, q) reads
+  // columns 32q .. 32q+31 of the step for the 4 row blocks.  phi operands are
+  // read from L2 once per step and reused by the 4 row blocks.
+  floatx4 acc[RB][MT];
+  float ssq[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    ssq[rb] = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rb][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
   for (int64_t kb = (int64_t)wave * 128; kb < K; kb += 4 * 128) {
-    const int64_t k = kb + kq * 32;
-    u32x4 xp[4][XP];
+    // MFMA g of the step takes columns kb + 32g + 8q .. +8 on lane (r, q): one load
+    // instruction then reads 64 contiguous bytes per row (A and B use the same map)
+    const int64_t k = kb + 8 * q;
+    u32x4 xp[RB][4][XP];
+    // Rows past T read row T-1 and phi rows past M read row M-1: their
+    // results land in accumulator rows / columns that are never used, so only
+    // the columns of a final partial step (k >= K) need masking.
+    const bool full_step = kb + 128 <= K;
+    if constexpr (VEC && XP == 1) {
+      // bf16: issue all 16 row loads and the phi loads before using any
+      u32x4 raw[RB][4];
+      if (full_step) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      float f[8];
-      XGroup<S>::template load<VEC>(xrow, k + 8 * g, K, row_ok, xp[g], f);
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ssq = fmaf(f[i], f[i], ssq);
+          for (int g = 0; g < 4; ++g) raw[rb][g] = ld16nt(xrow[rb] + k + 32 * g);
+      } else {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) raw[rb][g] = ld16_masked(xrow[rb], k + 32 * g, K, true, 2);
+      }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          xp[rb][g][0] = raw[rb][g];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = __uint_as_float(raw[rb][g][i] << 16);
+            const float hi = __uint_as_float(raw[rb][g][i] & 0xffff0000u);
+            ssq[rb] = fmaf(lo, lo, fmaf(hi, hi, ssq[rb]));
+          }
+        }
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float f[8];
+          XGroup<S>::template load<VEC>(xrow[rb], k + 32 * g, K, row_ok[rb], xp[rb][g], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ssq[rb] = fmaf(f[i], f[i], ssq[rb]);
+        }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + r;
-      const bool m_ok = m < M;
-      for (int p = 0; p < P; ++p) {
-        const uint16_t* prow = a.phi + p * a.phi_plane_stride + (m_ok ? m : 0) * a.phi_ld;
-        u32x4 b[4];
+      u32x4 b[P][4];
+#pragma unroll
+      for (int p = 0; p < P; ++p)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          b[g] = (m_ok && k + 8 * g < a.phi_ld) ? ld16(prow + k + 8 * g) : zero4();
+          b[p][g] = full_step ? ld16(prow[mt] + p * a.phi_plane_stride + k + 32 * g)
+                              : ld16_masked(prow[mt] + p * a.phi_plane_stride, k + 32 * g, a.phi_ld, true, 2);
 #pragma unroll
-        for (int xi = 0; xi < XP; ++xi) {
-          if (xi + p > 1) continue;
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) acc[mt] = mfma16x16x32(as_bf16x8(xp[g][xi]), as_bf16x8(b[g]), acc[mt]);
-        }
-      }
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int xi = 0; xi < XP; ++xi)
+              if (xi + p <= 2)  // dropped cross terms are below 2^-26 relative
+                acc[rb][mt] = mfma16x16x32(as_bf16x8(xp[rb][g][xi]), as_bf16x8(b[p][g]), acc[rb][mt]);
     }
   }
 
-  ssq += __shfl_xor(ssq, 16, kWave);
-  ssq += __shfl_xor(ssq, 32, kWave);
-  if (lane < kPreTile) ssq_sh[wave][lane] = ssq;
+  // ---- cross-wave reduction -------------------------------------------------
+  // acc layout: lane (r, q) holds D[i = 4q + v][j = r]: token 16*rb + 4q + v, m = 16*mt + r
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave][rb][mt][lane] = acc[rb][mt];
+    float s = ssq[rb];
+    s += __shfl_xor(s, 16, kWave);
+    s += __shfl_xor(s, 32, kWave);
+    if (q == 0) ssq_sh[wave][16 * rb + r] = s;
+  }
   __syncthreads();
-
-  // acc layout: lane l holds D[i = 4*(l/16) + v][j = l%16]; i = token, j = m % 16
-  for (int idx = tid; idx < kPreTile * MP; idx += kPreThreads) {
+  for (int idx = tid; idx < kFwdTile * MP; idx += kFwdThreads) {
     const int tt = idx / MP, m = idx - (idx / MP) * MP;
-    const int mt = m >> 4, ln = (m & 15) + 16 * (tt >> 2), v = tt & 3;
-    const float s = red[0][mt][ln][v] + red[1][mt][ln][v] + red[2][mt][ln][v] + red[3][mt][ln][v];
+    const int rb = tt >> 4, i = tt & 15;
+    const int mt = m >> 4, ln = (m & 15) + 16 * (i >> 2), v = i & 3;
+    const float sacc = red[0][rb][mt][ln][v] + red[1][rb][mt][ln][v] + red[2][rb][mt][ln][v] +
+                       red[3][rb][mt][ln][v];
     const float ss = ssq_sh[0][tt] + ssq_sh[1][tt] + ssq_sh[2][tt] + ssq_sh[3][tt];
     const float inv = 1.0f / sqrtf(ss / (float)K + a.norm_eps);
-    mix_sh[tt][m] = s * inv;
+    mix_sh[tt][m] = sacc * inv;
     if (m == 0) inv_sh[tt] = inv;
   }
   __syncthreads();
 
   if (a.mixes) {
-    for (int idx = tid; idx < kPreTile * M; idx += kPreThreads) {
+    for (int idx = tid; idx < kFwdTile * M; idx += kFwdThreads) {
       const int tt = idx / M, m = idx - (idx / M) * M;
       if (t0 + tt < a.T) a.mixes[(t0 + tt) * M + m] = mix_sh[tt][m];
     }
   }
-  if (a.inv_rms && tid < kPreTile && t0 + tid < a.T) a.inv_rms[t0 + tid] = inv_sh[tid];
+  if (a.inv_rms && tid < kFwdTile && t0 + tid < a.T) a.inv_rms[t0 + tid] = inv_sh[tid];
 
   // ---- 2. heads + Sinkhorn, lane per matrix element -----------------------
   {
-    constexpr int TPP = kPreThreads / L;  // tokens per pass
-    constexpr int PASSES = kPreTile / TPP;
+    constexpr int TPP = kFwdThreads / L;  // tokens per pass
+    constexpr int PASSES = kFwdTile / TPP;
     const float a0 = a.alpha[0], a1 = a.alpha[1], a2 = a.alpha[2];
-#pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
       const int tt = ps * TPP + tid / L;
       const int e = tid % L;
@@ -169,43 +238,73 @@ __global__ __launch_bounds__(kPreThreads) void pre_fwd_kernel(PreFwdArgs a) {
   __syncthreads();
 
   // ---- 3. y = sum_n pre[n] * x[n] (+ x_scaled) ---------------------------
+  // Each thread takes YU units (8 columns of one token) per round and issues
+  // all their loads before using any, so enough bytes are in flight.
   S* __restrict__ y = static_cast<S*>(a.y);
+  constexpr int YU = 4;
   const int DG = (D + 7) / 8;
-  for (int u = tid; u < kPreTile * DG; u += kPreThreads) {
-    const int tt = u / DG, dg = u - (u / DG) * DG;
-    const int64_t tok = t0 + tt;
-    if (tok >= a.T) break;
-    const int64_t d = (int64_t)dg * 8;
-    float o[8];
+  int64_t ntok = a.T - t0;
+  if (ntok > kFwdTile) ntok = kFwdTile;
+  const int units = (int)ntok * DG;
+  for (int u0 = tid; u0 < units; u0 += YU * kFwdThreads) {
+    float f[YU][N][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = 0.f;
-    const float inv = inv_sh[tt];
+    for (int j = 0; j < YU; ++j) {
+      const int u = u0 + j * kFwdThreads;
+      const int tt = u / DG, dg = u - (u / DG) * DG;
+      const bool ok = u < units;
 #pragma unroll
-    for (int n = 0; n < N; ++n) {
-      float f[8];
-      load8f<S, VEC>(x + (tok * N + n) * D, d, D, true, f);
-      const float p = pre_sh[tt][n];
+      for (int n = 0; n < N; ++n)
+        load8f<S, VEC>(x + ((t0 + (ok ? tt : 0)) * N + n) * D, (int64_t)dg * 8, D, ok, f[j][n]);
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = fmaf(p, f[i], o[i]);
+    for (int j = 0; j < YU; ++j) {
+      const int u = u0 + j * kFwdThreads;
+      if (u >= units) break;
+      const int tt = u / DG, dg = u - (u / DG) * DG;
+      const int64_t tok = t0 + tt, d = (int64_t)dg * 8;
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const float p = pre_sh[tt][n];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = fmaf(p, f[j][n][i], o[i]);
+      }
+      store8<S, VEC>(y + tok * D, d, D, o);
       if (a.x_scaled) {
-        float xs[8];
+        const float inv = inv_sh[tt];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xs[i] = f[i] * inv;
-        store8<float, VEC>(a.x_scaled + tok * K + (int64_t)n * D, d, D, xs);
+        for (int n = 0; n < N; ++n) {
+          float xs[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xs[i] = f[j][n][i] * inv;
+          store8<float, VEC>(a.x_scaled + tok * K + (int64_t)n * D, d, D, xs);
+        }
       }
     }
-    store8<S, VEC>(y + tok * D, d, D, o);
   }
+}
+
+template <int N, typename S, int P>
+static int launch_pre_fwd_p(const PreFwdArgs& a, bool vec, hipStream_t st) {
+  const dim3 grid((unsigned)((a.T + kFwdTile - 1) / kFwdTile)), block(kFwdThreads);
+  if (vec)
+    hipLaunchKernelGGL((pre_fwd_kernel<N, S, true, P>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((pre_fwd_kernel<N, S, false, P>), grid, block, 0, st, a);
+  return check_launch("pre_fwd");
 }
 
 template <int N, typename S>
 static int launch_pre_fwd(const PreFwdArgs& a, bool vec, hipStream_t st) {
-  const dim3 grid((unsigned)((a.T + kPreTile - 1) / kPreTile)), block(kPreThreads);
-  if (vec)
-    hipLaunchKernelGGL((pre_fwd_kernel<N, S, true>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((pre_fwd_kernel<N, S, false>), grid, block, 0, st, a);
-  return check_launch("pre_fwd");
+  switch (a.phi_planes) {
+    case 1: return launch_pre_fwd_p<N, S, 1>(a, vec, st);
+    case 2: return launch_pre_fwd_p<N, S, 2>(a, vec, st);
+    case 3: return launch_pre_fwd_p<N, S, 3>(a, vec, st);
+  }
+  return set_error(MHC_ERR_INVALID, "mhc_pre_fwd: %d phi planes", a.phi_planes);
 }
 
 template <typename S>

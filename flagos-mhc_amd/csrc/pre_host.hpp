@@ -11,17 +11,23 @@ namespace mhc {
 inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
-// bf16 planes needed to carry phi of this dtype (1 for bf16, 2 otherwise).
-inline int phi_plane_count(int32_t phi_dtype) { return phi_dtype == 1 /*MHC_DTYPE_BF16*/ ? 1 : 2; }
+// bf16 planes carrying phi in the forward contraction: 1 for bf16, 2 for fp16
+// (exact), 3 for fp32 (residual below 2^-26, so mixes keep fp32 accuracy).
+inline int phi_fwd_planes(int32_t phi_dtype) {
+  return phi_dtype == 1 /*BF16*/ ? 1 : (phi_dtype == 2 /*F16*/ ? 2 : 3);
+}
+// Planes of phi^T in the backward (grad_mixes @ phi feeds the x-dtype grad_x):
+// 1 for bf16, 2 otherwise.
+inline int phi_bwd_planes(int32_t phi_dtype) { return phi_dtype == 1 ? 1 : 2; }
 
 // Bytes of phi planes laid out [P][M][round_up(K, 8)].
 inline size_t phi_planes_bytes(int32_t phi_dtype, int M, int64_t K) {
-  return (size_t)phi_plane_count(phi_dtype) * (size_t)M * (size_t)round_up(K, 8) * 2;
+  return (size_t)phi_fwd_planes(phi_dtype) * (size_t)M * (size_t)round_up(K, 8) * 2;
 }
 
 // Bytes of transposed phi planes laid out [P][K][MP32], MP32 = M rounded up to 32.
 inline size_t phiT_planes_bytes(int32_t phi_dtype, int M, int64_t K) {
-  return (size_t)phi_plane_count(phi_dtype) * (size_t)K * (size_t)round_up(M, 32) * 2;
+  return (size_t)phi_bwd_planes(phi_dtype) * (size_t)K * (size_t)round_up(M, 32) * 2;
 }
 
 // Makes phi available as bf16 planes [P][M][ld].  bf16 phi with K % 8 == 0

@@ -26,7 +26,7 @@ __device__ __forceinline__ float phi_value(const void* phi, int64_t i) {
   return load_elem(static_cast<const S*>(phi), i);
 }
 
-// planes [P][M][ld]: plane 0 = bf16(phi), plane 1 = bf16(phi - plane0); zero padded.
+// planes [P][M][ld]: plane p = bf16(phi - sum of planes < p); zero padded.
 template <typename S>
 __global__ void phi_planes_kernel(const void* phi, uint16_t* out, int M, int64_t K, int64_t ld,
                                   int P) {
@@ -34,11 +34,12 @@ __global__ void phi_planes_kernel(const void* phi, uint16_t* out, int M, int64_t
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i / ld, k = i - (i / ld) * ld;
-    const float v = k < K ? phi_value<S>(phi, m * K + k) : 0.f;
-    uint32_t hi, lo;
-    split2_bf16(v, hi, lo);
-    out[i] = (uint16_t)hi;
-    if (P > 1) out[total + i] = (uint16_t)lo;
+    float v = k < K ? phi_value<S>(phi, m * K + k) : 0.f;
+    for (int p = 0; p < P; ++p) {
+      const uint32_t h = f32_to_bf16_bits(v);
+      out[p * total + i] = (uint16_t)h;
+      v -= bf16_bits_to_f32(h);
+    }
   }
 }
 
@@ -76,7 +77,7 @@ int prepare_phi_planes(const void* phi, int32_t phi_dtype, int M, int64_t K, voi
     *nplanes = 1;
     return MHC_OK;
   }
-  const int P = phi_plane_count(phi_dtype);
+  const int P = phi_fwd_planes(phi_dtype);
   const int64_t L = round_up(K, 8);
   const size_t need = phi_planes_bytes(phi_dtype, M, K);
   if (!ws || ws_bytes < need)
@@ -106,7 +107,7 @@ int prepare_phi_planes(const void* phi, int32_t phi_dtype, int M, int64_t K, voi
 
 int prepare_phiT_planes(const void* phi, int32_t phi_dtype, int M, int64_t K, uint16_t* dst,
                         hipStream_t st) {
-  const int P = phi_plane_count(phi_dtype);
+  const int P = phi_bwd_planes(phi_dtype);
   const int MP = (int)round_up(M, 32);
   const int64_t total = K * MP;
   switch (phi_dtype) {

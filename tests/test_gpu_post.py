@@ -138,6 +138,18 @@ def test_post_shapes_bsnd():
     assert g4[2].shape == (B, S, D) and g4[3].shape == (B, S, N)
 
 
+def test_post_bf16_rounding_bit_exact():
+    """h_res = diag(c), h_post = 0 makes every output one fp32 product c*x,
+    so the stored bf16 must equal torch's round-to-nearest-even of it, bit for bit."""
+    T, N, D = 512, 4, 1024
+    x, _, h_out, _, _ = post_inputs(T, N, D, torch.bfloat16)
+    c = torch.tensor([1.0 + 2.0 ** -9, 0.7, -1.3333, 3.0], device=DEV)
+    h_res = torch.diag_embed(c).expand(T, N, N).contiguous()
+    y = m.mhc_post(x, h_res, h_out, torch.zeros(T, N, device=DEV))
+    want = (x.float() * c.view(1, N, 1)).to(torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+
+
 def test_post_identity_gates_full_size():
     """h_res = I, h_post = 0 => y == x bit for bit (c5 width)."""
     T, N, D = 8192, 4, 7168
