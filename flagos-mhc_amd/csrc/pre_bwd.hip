@@ -54,7 +54,7 @@ struct PreBwdSmallArgs {
   float* scale;    // (T,), or null
   uint16_t* gmP;   // [2][T][MP32] bf16 planes of grad_mixes, or null
   int64_t gmP_plane;
-  uint16_t* gTw;   // [ceil(T/16)][2][MP][16] bf16 planes of grad_mixes * inv
+  uint16_t* gTw;   // [ceil(T/16)][MT][64][2][4] bf16 planes of grad_mixes * inv
   float4* coef;    // (T, N) {pre, inv, scale, 0}, or null
   float* partial;  // (gridDim.x, 3 + M)
   float* sink_scratch;
@@ -151,35 +151,45 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
       a.gm[tok * M + 2 * N + e] = gml;
       if (e < 2 * N) a.gm[tok * M + e] = gmh;
     }
-    if (ok && a.gmP) {
-      // operand layouts of the streaming kernel: grad_mixes as bf16 planes
-      // [2][T][MP32] and g = grad_mixes * inv as token-transposed 16-token
-      // tiles [T/16][2][MP][16]; padding rows m >= M are zero
+    if (a.gmP) {
+      // operand layouts of the streaming kernels: grad_mixes as bf16 planes
+      // [2][T][MP32], and g = grad_mixes * inv as token-transposed 16-token
+      // tiles [T/16][MT][64][2][4]: element m of token 16*tile + 4*qq + j
+      // sits at [tile][m / 16][m % 16 + 16*qq][plane][j], so MFMA lane
+      // (m % 16, qq) finds both planes of its 4 tokens in 16 contiguous
+      // bytes.  Padding rows m >= M are zero, and so are the g columns of
+      // the padding tokens T..16*ceil(T/16)-1 (this grid covers exactly
+      // those tokens).
       constexpr int MP32 = PD::MP32, MP = PD::MP;
-      uint16_t* gmP = a.gmP + tok * MP32;
-      uint16_t* gTw = a.gTw + (tok >> 4) * (2 * MP * 16) + (tok & 15);
+      uint16_t* gTw = a.gTw + (tok >> 4) * (PD::MT * 64 * 8) + ((tok & 15) >> 2) * 16 * 8 + (tok & 3);
+      auto gtw = [&](int m, int g) -> uint16_t& { return gTw[((m >> 4) * 64 + (m & 15)) * 8 + g * 4]; };
       uint32_t hi, lo;
-      split2_bf16(gml, hi, lo);
-      gmP[2 * N + e] = (uint16_t)hi;
-      gmP[a.gmP_plane + 2 * N + e] = (uint16_t)lo;
-      split2_bf16(gml * inv, hi, lo);
-      gTw[(2 * N + e) * 16] = (uint16_t)hi;
-      gTw[(MP + 2 * N + e) * 16] = (uint16_t)lo;
-      if (e < 2 * N) {
-        split2_bf16(gmh, hi, lo);
-        gmP[e] = (uint16_t)hi;
-        gmP[a.gmP_plane + e] = (uint16_t)lo;
-        split2_bf16(gmh * inv, hi, lo);
-        gTw[e * 16] = (uint16_t)hi;
-        gTw[(MP + e) * 16] = (uint16_t)lo;
+      if (ok) {
+        uint16_t* gmP = a.gmP + tok * MP32;
+        split2_bf16(gml, hi, lo);
+        gmP[2 * N + e] = (uint16_t)hi;
+        gmP[a.gmP_plane + 2 * N + e] = (uint16_t)lo;
+        if (e < 2 * N) {
+          split2_bf16(gmh, hi, lo);
+          gmP[e] = (uint16_t)hi;
+          gmP[a.gmP_plane + e] = (uint16_t)lo;
+        }
+        if (e < MP32 - M) {
+          gmP[M + e] = 0;
+          gmP[a.gmP_plane + M + e] = 0;
+        }
       }
-      if (e < MP32 - M) {
-        gmP[M + e] = 0;
-        gmP[a.gmP_plane + M + e] = 0;
+      split2_bf16(ok ? gml * inv : 0.f, hi, lo);
+      gtw(2 * N + e, 0) = (uint16_t)hi;
+      gtw(2 * N + e, 1) = (uint16_t)lo;
+      if (e < 2 * N) {
+        split2_bf16(ok ? gmh * inv : 0.f, hi, lo);
+        gtw(e, 0) = (uint16_t)hi;
+        gtw(e, 1) = (uint16_t)lo;
       }
       if (e < MP - M) {
-        gTw[(M + e) * 16] = 0;
-        gTw[(MP + M + e) * 16] = 0;
+        gtw(M + e, 0) = 0;
+        gtw(M + e, 1) = 0;
       }
     }
     const float sdot = group_sum<L - 1>(gml * ml + gmh * mh);
@@ -457,11 +467,13 @@ __global__ __launch_bounds__(256) void pre_bwd_main_kernel(PreBwdMainArgs a) {
 //     read from token-transposed 16-token tiles.  MFMA instance c covers the
 //     columns VC*r + c, r = 0..15.
 //   * gs = grad_mixes @ phi (MFMA 16x16x32, reduction over m): A = the 16
-//     tokens' grad_mixes rows, B = phi^T rows kept in registers for the whole
-//     kernel.  Output lane (r, q) holds tokens 4q..4q+3 of columns VC*r + c:
-//     exactly the rows of x and grad_y the lane loaded, so
-//     grad_x = grad_y*pre + inv*gs + scale*x is formed and stored in place.
-// No LDS and no barriers: each wave streams independently.
+//     tokens' grad_mixes rows, B = phi^T rows loaded once per block (kept in
+//     LDS for N=4, in registers for N=8).  Output lane (r, q) holds tokens
+//     4q..4q+3 of columns VC*r + c: exactly the rows of x and grad_y the lane
+//     loaded, so grad_x = grad_y*pre + inv*gs + scale*x is formed and stored
+//     in place.
+// No barriers: each wave streams independently, and for N=4 the next tile's
+// loads are issued before the current tile is computed.
 // ---------------------------------------------------------------------------
 template <int N> struct StreamCfg {
   static constexpr int VC = (N == 4) ? 8 : 4;  // columns per lane
@@ -469,6 +481,7 @@ template <int N> struct StreamCfg {
 };
 
 constexpr int kStreamTile = 16;  // tokens per tile (MFMA K of the grad_phi product)
+static_assert(kStreamTile == kBwdTile, "kernel A zero-fills the g tiles of the padding tokens");
 
 struct PreBwdStreamArgs {
   const bf16_t* x;
@@ -478,7 +491,7 @@ struct PreBwdStreamArgs {
   int phi_planes;
   const uint16_t* gmP;   // [2][T][MP32]
   int64_t gmP_plane;
-  const uint16_t* gTw;   // [ceil(T/16)][2][MP][16]
+  const uint16_t* gTw;   // [ceil(T/16)][MT][64][2][4]
   const float4* coef;    // (T, N) {pre, inv, scale, 0}
   bf16_t* gx;
   float* gphi_part;      // [nsplit][M][K]
@@ -498,13 +511,29 @@ __device__ __forceinline__ floatx4 mfma16x16x16(const u32x2& a, const u32x2& b, 
                                                   __builtin_bit_cast(short4_t, b), c, 0, 0, 0);
 }
 
+// Operands of one 16-token tile, loaded one tile ahead of their use.
+template <int N> struct StreamTile {
+  static constexpr int VC = StreamCfg<N>::VC, VD = VC / 2;
+  typedef typename RowVec<VD>::type Row;
+  Row xr[4], gr[4];                   // x[t, n, cols] and grad_y[t, cols], tokens 4q..4q+3
+  u32x4 gA[PreDims<N>::MK][2];        // grad_mixes row of token tb + r (A of gs), hi/lo
+  u32x2 ga[PreDims<N>::MT][2];        // (grad_mixes*inv)^T, tokens 4q..4q+3 (A of grad_phi)
+  float4 cf[4];                       // {pre[t,n], inv[t], scale[t]} of tokens 4q..4q+3
+};
+
 template <int N, int P>
 __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs a) {
   using PD = PreDims<N>;
+  using Tile = StreamTile<N>;
+  typedef typename Tile::Row Row;
   constexpr int M = PD::M, MT = PD::MT, MP = PD::MP, MK = PD::MK, MP32 = PD::MP32;
   constexpr int VC = StreamCfg<N>::VC, DW = StreamCfg<N>::DW, VD = VC / 2;
   constexpr int TT = kStreamTile;
-  typedef typename RowVec<VD>::type Row;
+  // N = 4: phi^T operands in LDS (frees registers for a second tile in flight);
+  // N = 8: more m chunks, operands stay in registers, one tile in flight.
+  constexpr bool PB_LDS = (N == 4);
+  constexpr bool PIPE = (N == 4);
+  __shared__ u32x4 pb_sh[PB_LDS ? N * VC * MK * P * kWave : 1];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int n = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -513,18 +542,23 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   const int64_t K = (int64_t)N * D, T = a.T;
   const int dl = blockIdx.x * DW + VC * r;  // first column d of this lane
   const bool colok = dl < D;                // D % VC == 0 on this path
+  const int dlc = colok ? dl : 0;           // clamped column for branch-free loads
   const int64_t kcol = (int64_t)n * D + dl;
 
-  u32x4 pb[VC][MK][P];
+  u32x4 pbr[PB_LDS ? 1 : VC][MK][P];
 #pragma unroll
   for (int c = 0; c < VC; ++c)
 #pragma unroll
     for (int mk = 0; mk < MK; ++mk)
 #pragma unroll
-      for (int p = 0; p < P; ++p)
-        pb[c][mk][p] = colok
-                           ? ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q)
-                           : zero4();
+      for (int p = 0; p < P; ++p) {
+        const u32x4 v = colok ? ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q)
+                              : zero4();
+        if constexpr (PB_LDS)
+          pb_sh[(((n * VC + c) * MK + mk) * P + p) * kWave + lane] = v;  // read back by this lane only
+        else
+          pbr[c][mk][p] = v;
+      }
 
   floatx4 ph[MT][VC];
 #pragma unroll
@@ -532,81 +566,82 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 #pragma unroll
     for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t ntiles = (T + TT - 1) / TT;
-  for (int64_t tile = blockIdx.y; tile < ntiles; tile += a.nsplit) {
+  // Loads are unconditional from clamped addresses and their data is used
+  // unmodified, so a tile's loads issue back to back and stay in flight
+  // until compute_tile: a clamped x row meets zero columns of g (kernel A
+  // zero-fills the padding tokens of the last tile), clamped gm rows and
+  // coefficients only reach outputs of tokens >= T, which are not stored.
+  auto load_tile = [&](int64_t tile, Tile& tl) {
     const int64_t tb = tile * TT, tg = tb + 4 * q;
-    Row xr[4], gr[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t t = tg + e;
-      Row zx = {}, zg = {};
-      if (colok && t < T) {
-        zx = __builtin_nontemporal_load(reinterpret_cast<const Row*>(a.x + (t * N + n) * D + dl));
-        zg = *reinterpret_cast<const Row*>(a.gy + t * D + dl);
-      }
-      xr[e] = zx;
-      gr[e] = zg;
+      const int64_t tc = t < T ? t : T - 1;
+      tl.xr[e] = __builtin_nontemporal_load(reinterpret_cast<const Row*>(a.x + (tc * N + n) * D + dlc));
+      tl.gr[e] = *reinterpret_cast<const Row*>(a.gy + tc * D + dlc);
+      tl.cf[e] = a.coef[tc * N + n];
     }
     const int64_t ts = tb + r;  // token of MFMA row r in the gs product
-    u32x4 gA[MK][2];
+    const int64_t tsc = ts < T ? ts : T - 1;
 #pragma unroll
     for (int mk = 0; mk < MK; ++mk)
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
-        gA[mk][g] = ts < T ? ld16(a.gmP + g * a.gmP_plane + ts * MP32 + 32 * mk + 8 * q) : zero4();
-    int nv = (int)(T - tg);
-    nv = nv < 0 ? 0 : (nv > 4 ? 4 : nv);
-    u32x2 ga[MT][2];
+      for (int g = 0; g < 2; ++g) tl.gA[mk][g] = ld16(a.gmP + g * a.gmP_plane + tsc * MP32 + 32 * mk + 8 * q);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        u32x2 v = *reinterpret_cast<const u32x2*>(a.gTw + ((tile * 2 + g) * MP + 16 * mt + r) * TT + 4 * q);
-#pragma unroll
-        for (int w = 0; w < 2; ++w)
-          v[w] &= (2 * w < nv ? 0xffffu : 0u) | (2 * w + 1 < nv ? 0xffff0000u : 0u);
-        ga[mt][g] = v;
-      }
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x4 v = ld16(a.gTw + ((tile * MT + mt) * 64 + lane) * 8);
+      tl.ga[mt][0] = u32x2{v[0], v[1]};
+      tl.ga[mt][1] = u32x2{v[2], v[3]};
+    }
+  };
 
-    // ---- grad_phi partial += g^T @ x over this tile's 16 tokens -----------
+  auto compute_tile = [&](int64_t tile, const Tile& tl) {
+    const int64_t tg = tile * TT + 4 * q;
+    // ---- grad_phi partial += g^T @ x over the tile's 16 tokens ----------
 #pragma unroll
     for (int c = 0; c < VC; ++c) {
       // column c of the lane's 4 x VC block: tokens (2w, 2w+1) in dword w
       u32x2 xt;
 #pragma unroll
       for (int w = 0; w < 2; ++w) {
-        const uint32_t lo = xr[2 * w][c >> 1], hi = xr[2 * w + 1][c >> 1];
+        const uint32_t lo = tl.xr[2 * w][c >> 1], hi = tl.xr[2 * w + 1][c >> 1];
         xt[w] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        ph[mt][c] = mfma16x16x16(ga[mt][0], xt, ph[mt][c]);
-        ph[mt][c] = mfma16x16x16(ga[mt][1], xt, ph[mt][c]);
+        ph[mt][c] = mfma16x16x16(tl.ga[mt][0], xt, ph[mt][c]);
+        ph[mt][c] = mfma16x16x16(tl.ga[mt][1], xt, ph[mt][c]);
       }
     }
-
-    // ---- gs = grad_mixes @ phi and grad_x ----------------------------------
+    // ---- gs = grad_mixes @ phi, then grad_x ---------------------------------
     floatx4 gs[VC];
 #pragma unroll
     for (int c = 0; c < VC; ++c) {
       gs[c] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mk = 0; mk < MK; ++mk) {
-        gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][0]), gs[c]);
-        gs[c] = mfma16x16x32(as_bf16x8(gA[mk][1]), as_bf16x8(pb[c][mk][0]), gs[c]);
-        if constexpr (P > 1)
-          gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][P - 1]), gs[c]);
+        u32x4 b[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          if constexpr (PB_LDS)
+            b[p] = pb_sh[(((n * VC + c) * MK + mk) * P + p) * kWave + lane];
+          else
+            b[p] = pbr[c][mk][p];
+        }
+        gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][0]), as_bf16x8(b[0]), gs[c]);
+        gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][1]), as_bf16x8(b[0]), gs[c]);
+        if constexpr (P > 1) gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][0]), as_bf16x8(b[P - 1]), gs[c]);
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t t = tg + e;
       if (!(colok && t < T)) continue;
-      const float4 cf = a.coef[t * N + n];  // pre[t,n], inv[t], scale[t]
+      const float4 cf = tl.cf[e];  // pre[t,n], inv[t], scale[t]
       Row o;
 #pragma unroll
       for (int w = 0; w < VD; ++w) {
-        const uint32_t xw = xr[e][w], gw = gr[e][w];
+        const uint32_t xw = tl.xr[e][w], gw = tl.gr[e][w];
         const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
         const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
         const float o0 = fmaf(cf.z, x0, fmaf(cf.y, gs[2 * w][e], g0 * cf.x));
@@ -614,6 +649,32 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
         o[w] = pack_bf16x2(o0, o1);
       }
       *reinterpret_cast<Row*>(a.gx + (t * N + n) * D + dl) = o;
+    }
+  };
+
+  const int64_t ntiles = (T + TT - 1) / TT;
+  const int64_t step = a.nsplit;
+  if constexpr (PIPE) {
+    // two tiles in registers: the next tile's loads are in flight while the
+    // current one is computed (loop unrolled by two so the buffers alternate)
+    Tile A, B;
+    int64_t tile = blockIdx.y;
+    if (tile < ntiles) load_tile(tile, A);
+    while (tile < ntiles) {
+      const int64_t t1 = tile + step;
+      if (t1 < ntiles) load_tile(t1, B);
+      compute_tile(tile, A);
+      if (t1 >= ntiles) break;
+      const int64_t t2 = t1 + step;
+      if (t2 < ntiles) load_tile(t2, A);
+      compute_tile(t1, B);
+      tile = t2;
+    }
+  } else {
+    Tile A;
+    for (int64_t tile = blockIdx.y; tile < ntiles; tile += step) {
+      load_tile(tile, A);
+      compute_tile(tile, A);
     }
   }
 
@@ -628,6 +689,321 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 #pragma unroll
       for (int c = 0; c < VC; ++c) part[(int64_t)m * K + kcol + c] = ph[mt][c][v];
     }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel B, LDS-pipelined form (N = 4, bf16 activations, 16-byte rows)
+//
+// Same per-lane arithmetic as the streaming form, but the operands of a
+// 16-token tile reach the lanes through a ring of S stages in LDS filled by
+// direct-to-LDS loads (buffer_load ... lds / global_load_lds): a tile's
+// loads are issued S-1 tiles before it is computed and cost no registers
+// while in flight, so one block of N waves per CU keeps ~(S-1) x 25 KB of
+// HBM reads outstanding.  Each direct load moves 16 bytes per lane to
+// LDS[slot + 16*lane]; a lane later reads back exactly what the same lane
+// index loaded, so every LDS read is a conflict-free 16-byte row.
+//
+// Work split: the items (column block cb, tile) are numbered
+// cb * ntiles + tile and block b takes the contiguous range
+// [b*per, (b+1)*per); grad_phi partials are flushed whenever the column
+// block changes, to slot b + cb of a [nblk + ncb - 1][M][N][DW] buffer
+// (b + cb is distinct for every (b, cb) pair met, because both grow along
+// the range), and summed per column block in the order of b.
+//
+// Synchronisation per tile j (slot j % S):
+//   wait until this wave's loads of tile j have landed (s_waitcnt vmcnt;
+//   vector memory operations complete in issue order), s_barrier, read the
+//   tile's operands from LDS, issue the loads of tile j + S - 1 into the
+//   slot of tile j - 1 (every wave finished reading it before the barrier),
+//   compute, store grad_x with range-checked buffer stores (exactly 4 per
+//   lane and tile, so the vmcnt arithmetic is exact).
+// Rows of tokens >= T and columns >= D load as zero (range-checked buffer
+// loads); grad_mixes rows and coefficients of tokens >= T load from the
+// clamped last token and only reach outputs that are not stored.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+template <int N> struct DmaCfg {
+  using PD = PreDims<N>;
+  static constexpr int VC = 8, VD = 4, DW = 128, TT = 16;
+  static constexpr int MK = PD::MK, MT = PD::MT;
+  // 1 KB units of one stage (16 bytes per lane)
+  static constexpr int X = 0;              // [N][4]  x rows: stream n, tokens 4q+e
+  static constexpr int GY = X + 4 * N;     // [4]     grad_y rows, tokens 4q+e
+  static constexpr int GA = GY + 4;        // [MK][2] grad_mixes rows (A of gs), hi/lo
+  static constexpr int GT = GA + 2 * MK;   // [MT]    g^T blocks (A of grad_phi), both planes
+  static constexpr int CF = GT + MT;       // [N/4]   coefficients of 16 tokens x N streams
+  static constexpr int UNITS = CF + N / 4;
+  static constexpr int SHARED = UNITS - GY;      // units loaded once per block, split over waves
+  static constexpr int LMIN = 4 + SHARED / N;    // fewest loads a wave issues per tile
+};
+
+constexpr int kDmaStages = 5;
+constexpr int kDmaMaxBlocks = 512;
+constexpr uint32_t kBufferOob = 0x80000000u;   // buffer offset beyond every range: dropped / zero
+
+struct PreBwdDmaArgs {
+  const bf16_t* x;
+  const bf16_t* gy;
+  const uint16_t* phiT;  // [P][K][MP32]
+  int64_t phiT_plane_stride;
+  const uint16_t* gmP;   // [2][T][MP32]
+  int64_t gmP_plane;
+  const uint16_t* gTw;   // [ceil(T/16)][MT][64][2][4]
+  const float4* coef;    // (T, N) {pre, inv, scale, 0}
+  bf16_t* gx;
+  float* part;           // [nblk + ncb - 1][M][N][DW]
+  int64_t T;
+  int D;
+  int ncb;
+  int64_t ntiles;
+  int64_t per;           // items per block
+};
+
+// s_waitcnt vmcnt(V) with the other counters left free (gfx9 encoding).
+template <int V>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(V >= 0 && V < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (15 << 8) | ((V >> 4) << 14));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+template <int N, int P, int S>
+__global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
+  using C = DmaCfg<N>;
+  using PD = PreDims<N>;
+  constexpr int M = PD::M, MT = PD::MT, MK = PD::MK, MP32 = PD::MP32;
+  constexpr int VC = C::VC, VD = C::VD, DW = C::DW, TT = C::TT, UNITS = C::UNITS;
+  constexpr int VM_START = (S - 2) * C::LMIN;               // before any grad_x store
+  constexpr int VM_STEADY = (S - 2) * C::LMIN + (S - 1) * 4;
+  static_assert(N % 4 == 0 && S >= 2 && VM_STEADY < 64, "pipeline shape");
+  __shared__ u32x4 ring[S * UNITS * kWave];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int D = a.D;
+  const int64_t T = a.T, K = (int64_t)N * D, ntiles = a.ntiles;
+  const int64_t lin0 = (int64_t)blockIdx.x * a.per;
+  int64_t lin1 = lin0 + a.per;
+  if (lin1 > (int64_t)a.ncb * ntiles) lin1 = (int64_t)a.ncb * ntiles;
+  if (lin0 >= lin1) return;  // uniform over the block
+  const int64_t cnt = lin1 - lin0;
+
+  // Item counters advance incrementally (no 64-bit divisions in the loop):
+  // (icb, itile) is the next item to load, (ccb, ctile) the next to compute.
+  int64_t icb = lin0 / ntiles, itile = lin0 - icb * ntiles;
+  const int64_t cb0 = icb, tile0 = itile;
+
+  auto issue = [&](int64_t j) {
+    const int64_t tile = itile, tb = tile * TT;
+    const int nv = (int)(T - tb < TT ? T - tb : TT);
+    const int dl = (int)icb * DW + VC * r;
+    const bool colok = dl < D;
+    u32x4* st = ring + (int)(j % S) * UNITS * kWave;
+    const auto rx = rows_rsrc(a.x + tb * K, (int64_t)nv * K * 2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(st + (C::X + 4 * n + e) * kWave), 16,
+                                               off, 0, 0, 2 /* nt */);
+    }
+    for (int u = n; u < C::SHARED; u += N) {
+      const int unit = C::GY + u;
+      lds_void_t* dst = (lds_void_t*)(st + unit * kWave);
+      if (unit < C::GA) {
+        const int e = unit - C::GY;
+        const auto rg = rows_rsrc(a.gy + tb * D, (int64_t)nv * D * 2);
+        const uint32_t off = colok ? (uint32_t)(((4 * q + e) * (int64_t)D + dl) * 2) : kBufferOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, dst, 16, off, 0, 0, 2);
+      } else if (unit < C::GT) {
+        const int mk = (unit - C::GA) >> 1, g = (unit - C::GA) & 1;
+        const int64_t ts = tb + r < T ? tb + r : T - 1;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)(a.gmP + g * a.gmP_plane + ts * MP32 + 32 * mk + 8 * q),
+                                         dst, 16, 0, 0);
+      } else if (unit < C::CF) {
+        const int mt = unit - C::GT;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)(a.gTw + ((tile * MT + mt) * kWave + lane) * 8), dst,
+                                         16, 0, 0);
+      } else {
+        const int i = unit - C::CF;
+        int64_t idx = tb * N + i * kWave + lane;
+        if (idx > T * N - 1) idx = T * N - 1;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)(a.coef + idx), dst, 16, 0, 0);
+      }
+    }
+    if (++itile == ntiles) {
+      itile = 0;
+      ++icb;
+    }
+  };
+
+  // LDS reads are inline asm: the compiler does not track which ring slot a
+  // direct-to-LDS load writes and would otherwise wait for all of them
+  // (vmcnt(0)) before every LDS read.  The explicit waits above order them.
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)ring;
+
+  for (int64_t j = 0; j < S - 1 && j < cnt; ++j) issue(j);
+
+  int64_t j = 0, ccb = cb0, ctile = tile0;
+  while (j < cnt) {
+    // one column block: phi^T operands in registers, grad_phi accumulators
+    const int dl = (int)ccb * DW + VC * r;
+    const bool colok = dl < D;
+    u32x4 pb[VC][MK][P];
+    {
+      const int64_t kcol = (int64_t)n * D + (colok ? dl : 0);
+#pragma unroll
+      for (int c = 0; c < VC; ++c)
+#pragma unroll
+        for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            const u32x4 v = ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q);
+            pb[c][mk][p] = colok ? v : zero4();
+          }
+    }
+    floatx4 ph[MT][VC];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t seg_end = j + (ntiles - ctile) < cnt ? j + (ntiles - ctile) : cnt;
+    for (; j < seg_end; ++j, ++ctile) {
+      // this wave's loads of tile j have landed once at most V newer vector
+      // memory operations are outstanding
+      if (j + S - 2 < cnt) {
+        if (j >= S - 1)
+          wait_vmcnt<VM_STEADY>();
+        else
+          wait_vmcnt<VM_START>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+
+      const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
+      const uint32_t la = sbase + lane * 16;
+      const uint32_t lx = la + C::X * 1024 + 4 * n * 1024;
+      const uint32_t lc = sbase + C::CF * 1024 + (4 * q * N + n) * 16;
+      u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) asm volatile("ds_read_b128 %0, %1" : "=v"(xr[e]) : "v"(lx + e * 1024));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        asm volatile("ds_read_b128 %0, %1" : "=v"(gt[mt]) : "v"(la + (C::GT + mt) * 1024));
+#pragma unroll
+      for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+          asm volatile("ds_read_b128 %0, %1" : "=v"(gA[mk][g]) : "v"(la + (C::GA + 2 * mk + g) * 1024));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        asm volatile("ds_read_b128 %0, %1" : "=v"(gr[e]) : "v"(la + (C::GY + e) * 1024));
+        asm volatile("ds_read_b128 %0, %1" : "=v"(cfu[e]) : "v"(lc + e * N * 16));
+      }
+      // the next loads go to the slot of tile j - 1, which every wave
+      // finished reading before the barrier
+      if (j + S - 1 < cnt) issue(j + S - 1);
+      static_assert(MK == 1 && MT == 2, "operand tie list below is written for N = 4");
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(gt[0]), "+v"(gt[1]),
+                     "+v"(gA[0][0]), "+v"(gA[0][1]), "+v"(gr[0]), "+v"(gr[1]), "+v"(gr[2]), "+v"(gr[3]),
+                     "+v"(cfu[0]), "+v"(cfu[1]), "+v"(cfu[2]), "+v"(cfu[3]));
+
+      const int64_t tb = ctile * TT;
+      const int nv = (int)(T - tb < TT ? T - tb : TT);
+
+      // ---- grad_phi partial += g^T @ x over the tile's 16 tokens ----------
+#pragma unroll
+      for (int c = 0; c < VC; ++c) {
+        u32x2 xt;  // column c of the lane's 4 x VC block: tokens (2w, 2w+1) in dword w
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const uint32_t lo = xr[2 * w][c >> 1], hi = xr[2 * w + 1][c >> 1];
+          xt[w] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          ph[mt][c] = mfma16x16x16(u32x2{gt[mt][0], gt[mt][1]}, xt, ph[mt][c]);
+          ph[mt][c] = mfma16x16x16(u32x2{gt[mt][2], gt[mt][3]}, xt, ph[mt][c]);
+        }
+      }
+      // ---- gs = grad_mixes @ phi, then grad_x -------------------------------
+      floatx4 gs[VC];
+#pragma unroll
+      for (int c = 0; c < VC; ++c) {
+        gs[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mk = 0; mk < MK; ++mk) {
+          gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][0]), gs[c]);
+          gs[c] = mfma16x16x32(as_bf16x8(gA[mk][1]), as_bf16x8(pb[c][mk][0]), gs[c]);
+          if constexpr (P > 1) gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][P - 1]), gs[c]);
+        }
+      }
+      const auto rgx = rows_rsrc(a.gx + tb * K, (int64_t)nv * K * 2);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // pre[t,n], inv[t], scale[t]
+        const float fx = __uint_as_float(cfu[e][0]), fy = __uint_as_float(cfu[e][1]),
+                    fz = __uint_as_float(cfu[e][2]);
+        u32x4 o;
+#pragma unroll
+        for (int w = 0; w < VD; ++w) {
+          const uint32_t xw = xr[e][w], gw = gr[e][w];
+          const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
+          const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
+          const float o0 = fmaf(fz, x0, fmaf(fy, gs[2 * w][e], g0 * fx));
+          const float o1 = fmaf(fz, x1, fmaf(fy, gs[2 * w + 1][e], g1 * fx));
+          o[w] = pack_bf16x2(o0, o1);
+        }
+        // rows >= nv fall outside the range and are dropped, as are columns >= D
+        const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
+        __builtin_amdgcn_raw_buffer_store_b128(o, rgx, off, 0, 0);
+      }
+    }
+
+    // flush the column block's grad_phi partial to slot blockIdx.x + ccb
+    float* part = a.part + ((((int64_t)blockIdx.x + ccb) * M) * N + n) * DW + VC * r;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 16 * mt + 4 * q + v;
+        if (m >= M) continue;
+        float4* dst = reinterpret_cast<float4*>(part + (int64_t)m * N * DW);
+        dst[0] = float4{ph[mt][0][v], ph[mt][1][v], ph[mt][2][v], ph[mt][3][v]};
+        dst[1] = float4{ph[mt][4][v], ph[mt][5][v], ph[mt][6][v], ph[mt][7][v]};
+      }
+    ++ccb;
+    ctile = 0;
+  }
+}
+
+// grad_phi[m, n*D + d] = sum over the blocks b that met column block
+// cb = d / DW of part[b + cb][m][n][d % DW], in the order of b.
+template <int N>
+__global__ void sum_dma_parts_kernel(const float* __restrict__ part, float* __restrict__ gphi, int D,
+                                     int64_t ntiles, int64_t per) {
+  constexpr int M = PreDims<N>::M, DW = DmaCfg<N>::DW;
+  const int64_t K = (int64_t)N * D, total = (int64_t)M * K;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i / K, k = i - m * K;
+    const int n = (int)(k / D), d = (int)(k - (int64_t)n * D);
+    const int64_t cb = d / DW;
+    const int64_t b0 = cb * ntiles / per, b1 = ((cb + 1) * ntiles - 1) / per;
+    float s = 0.f;
+    for (int64_t b = b0; b <= b1; ++b) s += part[(((b + cb) * M + m) * N + n) * DW + d % DW];
+    gphi[i] = s;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -711,7 +1087,14 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   b.off_partial = off;
   off += align256((size_t)b.nblkA * b.C * 4);
   b.off_gphi = off;
-  off += align256((size_t)kMaxSplits * b.M * b.K * 4);
+  {
+    // grad_phi partials: [kMaxSplits][M][K] for the split kernels, or
+    // [blocks + column blocks - 1][M][N][DW] for the LDS-pipelined one
+    const size_t ncb = (size_t)(D + DmaCfg<4>::DW - 1) / DmaCfg<4>::DW;
+    const size_t split_parts = (size_t)kMaxSplits * b.M * b.K;
+    const size_t dma_parts = (kDmaMaxBlocks + ncb - 1) * b.M * N * DmaCfg<4>::DW;
+    off += align256((split_parts > dma_parts ? split_parts : dma_parts) * 4);
+  }
   b.off_gmP = off;
   off += align256((size_t)2 * T * b.MP32 * 2);
   b.off_gTw = off;
@@ -764,19 +1147,71 @@ static int launch_stream(const BwdLayout& lay, PreBwdStreamArgs& sta, hipStream_
   return check_launch("pre_bwd_stream");
 }
 
+static unsigned reduce_grid(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  return (unsigned)(g > 8192 ? 8192 : g);
+}
+
+static int sum_alpha_base(const BwdLayout& lay, const PreBwdSmallArgs& sa, float* grad_alpha,
+                          float* grad_base, hipStream_t st) {
+  hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
+                     lay.nblkA, lay.C, grad_alpha, grad_base);
+  return check_launch("pre_bwd_sum_rows");
+}
+
 static int reduce_tail(const BwdLayout& lay, const PreBwdSmallArgs& sa, const float* gphi_part,
                        int nsplit, float* grad_phi, float* grad_alpha, float* grad_base,
                        hipStream_t st) {
   const int64_t n = (int64_t)lay.M * lay.K;
-  int64_t g = (n + 255) / 256;
-  if (g > 8192) g = 8192;
-  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)g), dim3(256), 0, st, gphi_part, grad_phi, n,
+  hipLaunchKernelGGL(sum_splits_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, gphi_part, grad_phi, n,
                      nsplit);
   int rc = check_launch("pre_bwd_sum_splits");
   if (rc) return rc;
-  hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
-                     lay.nblkA, lay.C, grad_alpha, grad_base);
-  return check_launch("pre_bwd_sum_rows");
+  return sum_alpha_base(lay, sa, grad_alpha, grad_base, st);
+}
+
+// The LDS ring needs 16 * N * D * 2 bytes (one tile of x rows) to fit a
+// buffer range, and one block per CU.
+template <int N>
+static bool dma_usable(int D) {
+  return N == 4 && (int64_t)DmaCfg<N>::TT * N * D * 2 < ((int64_t)1 << 31);
+}
+
+template <int N, int P>
+static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* grad_phi,
+                      hipStream_t st) {
+  constexpr int DW = DmaCfg<N>::DW;
+  const int D = sta.D;
+  const int64_t ncb = (D + DW - 1) / DW;
+  const int64_t total = ncb * lay.ntiles;
+  int64_t nblk = device_cus();  // the LDS ring takes most of a CU: one block each
+  if (nblk > kDmaMaxBlocks) nblk = kDmaMaxBlocks;
+  if (nblk > total) nblk = total;
+  const int64_t per = (total + nblk - 1) / nblk;
+  nblk = (total + per - 1) / per;
+  PreBwdDmaArgs da{};
+  da.x = sta.x;
+  da.gy = sta.gy;
+  da.phiT = sta.phiT;
+  da.phiT_plane_stride = sta.phiT_plane_stride;
+  da.gmP = sta.gmP;
+  da.gmP_plane = sta.gmP_plane;
+  da.gTw = sta.gTw;
+  da.coef = sta.coef;
+  da.gx = sta.gx;
+  da.part = sta.gphi_part;
+  da.T = sta.T;
+  da.D = D;
+  da.ncb = (int)ncb;
+  da.ntiles = lay.ntiles;
+  da.per = per;
+  hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages>), dim3((unsigned)nblk), dim3(64 * N), 0, st,
+                     da);
+  int rc = check_launch("pre_bwd_dma");
+  if (rc) return rc;
+  hipLaunchKernelGGL((sum_dma_parts_kernel<N>), dim3(reduce_grid((int64_t)lay.M * lay.K)), dim3(256), 0,
+                     st, sta.gphi_part, grad_phi, D, lay.ntiles, per);
+  return check_launch("pre_bwd_sum_dma_parts");
 }
 
 template <int N, typename S>
@@ -799,6 +1234,13 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
     hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, false>), gA, bA, 0, st, sa);
   int rc = check_launch("pre_bwd_small");
   if (rc) return rc;
+  if constexpr (N == 4) {
+    if (streaming && dma_usable<N>(sta.D)) {
+      rc = lay.P == 1 ? launch_dma<N, 1>(lay, sta, grad_phi, st) : launch_dma<N, 2>(lay, sta, grad_phi, st);
+      if (rc) return rc;
+      return sum_alpha_base(lay, sa, grad_alpha, grad_base, st);
+    }
+  }
   if (streaming) {
     rc = lay.P == 1 ? launch_stream<N, 1>(lay, sta, st) : launch_stream<N, 2>(lay, sta, st);
     if (rc) return rc;

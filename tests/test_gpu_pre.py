@@ -109,6 +109,11 @@ BWD_CASES = [
     (29, 8, 64, torch.float32, torch.float32, "baseline", 2.0, 20),
     (70, 4, 128, torch.bfloat16, torch.bfloat16, "baseline", 0.0, 40),        # scratch Sinkhorn path
     (33, 8, 96, torch.bfloat16, torch.bfloat16, "reftest", 0.2, 1),
+    # LDS-pipelined grad_x/grad_phi kernel (N=4, bf16, D % 8 == 0): work ranges
+    # that cross column blocks, a partial last column block, a ragged last tile
+    (1010, 4, 1288, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    # ranges spanning three column blocks (more column blocks than CUs)
+    (17, 4, 40000, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
 ]
 
 
