@@ -467,13 +467,12 @@ __global__ __launch_bounds__(256) void pre_bwd_main_kernel(PreBwdMainArgs a) {
 //     read from token-transposed 16-token tiles.  MFMA instance c covers the
 //     columns VC*r + c, r = 0..15.
 //   * gs = grad_mixes @ phi (MFMA 16x16x32, reduction over m): A = the 16
-//     tokens' grad_mixes rows, B = phi^T rows loaded once per block (kept in
-//     LDS for N=4, in registers for N=8).  Output lane (r, q) holds tokens
-//     4q..4q+3 of columns VC*r + c: exactly the rows of x and grad_y the lane
-//     loaded, so grad_x = grad_y*pre + inv*gs + scale*x is formed and stored
-//     in place.
-// No barriers: each wave streams independently, and for N=4 the next tile's
-// loads are issued before the current tile is computed.
+//     tokens' grad_mixes rows, B = phi^T rows kept in registers for the whole
+//     kernel.  Output lane (r, q) holds tokens 4q..4q+3 of columns VC*r + c:
+//     exactly the rows of x and grad_y the lane loaded, so
+//     grad_x = grad_y*pre + inv*gs + scale*x is formed and stored in place.
+// No LDS and no barriers: each wave streams independently.  Used for N = 8;
+// N = 4 takes the LDS-pipelined form below.
 // ---------------------------------------------------------------------------
 template <int N> struct StreamCfg {
   static constexpr int VC = (N == 4) ? 8 : 4;  // columns per lane
@@ -511,7 +510,7 @@ __device__ __forceinline__ floatx4 mfma16x16x16(const u32x2& a, const u32x2& b, 
                                                   __builtin_bit_cast(short4_t, b), c, 0, 0, 0);
 }
 
-// Operands of one 16-token tile, loaded one tile ahead of their use.
+// Operands of one 16-token tile.
 template <int N> struct StreamTile {
   static constexpr int VC = StreamCfg<N>::VC, VD = VC / 2;
   typedef typename RowVec<VD>::type Row;
@@ -529,11 +528,6 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   constexpr int M = PD::M, MT = PD::MT, MP = PD::MP, MK = PD::MK, MP32 = PD::MP32;
   constexpr int VC = StreamCfg<N>::VC, DW = StreamCfg<N>::DW, VD = VC / 2;
   constexpr int TT = kStreamTile;
-  // N = 4: phi^T operands in LDS (frees registers for a second tile in flight);
-  // N = 8: more m chunks, operands stay in registers, one tile in flight.
-  constexpr bool PB_LDS = (N == 4);
-  constexpr bool PIPE = (N == 4);
-  __shared__ u32x4 pb_sh[PB_LDS ? N * VC * MK * P * kWave : 1];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int n = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -545,20 +539,15 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   const int dlc = colok ? dl : 0;           // clamped column for branch-free loads
   const int64_t kcol = (int64_t)n * D + dl;
 
-  u32x4 pbr[PB_LDS ? 1 : VC][MK][P];
+  u32x4 pb[VC][MK][P];
 #pragma unroll
   for (int c = 0; c < VC; ++c)
 #pragma unroll
     for (int mk = 0; mk < MK; ++mk)
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const u32x4 v = colok ? ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q)
-                              : zero4();
-        if constexpr (PB_LDS)
-          pb_sh[(((n * VC + c) * MK + mk) * P + p) * kWave + lane] = v;  // read back by this lane only
-        else
-          pbr[c][mk][p] = v;
-      }
+      for (int p = 0; p < P; ++p)
+        pb[c][mk][p] = colok ? ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q)
+                             : zero4();
 
   floatx4 ph[MT][VC];
 #pragma unroll
@@ -620,17 +609,9 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
       gs[c] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mk = 0; mk < MK; ++mk) {
-        u32x4 b[P];
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-          if constexpr (PB_LDS)
-            b[p] = pb_sh[(((n * VC + c) * MK + mk) * P + p) * kWave + lane];
-          else
-            b[p] = pbr[c][mk][p];
-        }
-        gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][0]), as_bf16x8(b[0]), gs[c]);
-        gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][1]), as_bf16x8(b[0]), gs[c]);
-        if constexpr (P > 1) gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][0]), as_bf16x8(b[P - 1]), gs[c]);
+        gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][0]), as_bf16x8(pb[c][mk][0]), gs[c]);
+        gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][1]), as_bf16x8(pb[c][mk][0]), gs[c]);
+        if constexpr (P > 1) gs[c] = mfma16x16x32(as_bf16x8(tl.gA[mk][0]), as_bf16x8(pb[c][mk][P - 1]), gs[c]);
       }
     }
 #pragma unroll
@@ -653,29 +634,10 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   };
 
   const int64_t ntiles = (T + TT - 1) / TT;
-  const int64_t step = a.nsplit;
-  if constexpr (PIPE) {
-    // two tiles in registers: the next tile's loads are in flight while the
-    // current one is computed (loop unrolled by two so the buffers alternate)
-    Tile A, B;
-    int64_t tile = blockIdx.y;
-    if (tile < ntiles) load_tile(tile, A);
-    while (tile < ntiles) {
-      const int64_t t1 = tile + step;
-      if (t1 < ntiles) load_tile(t1, B);
-      compute_tile(tile, A);
-      if (t1 >= ntiles) break;
-      const int64_t t2 = t1 + step;
-      if (t2 < ntiles) load_tile(t2, A);
-      compute_tile(t1, B);
-      tile = t2;
-    }
-  } else {
-    Tile A;
-    for (int64_t tile = blockIdx.y; tile < ntiles; tile += step) {
-      load_tile(tile, A);
-      compute_tile(tile, A);
-    }
+  Tile A;
+  for (int64_t tile = blockIdx.y; tile < ntiles; tile += a.nsplit) {
+    load_tile(tile, A);
+    compute_tile(tile, A);
   }
 
   if (!colok) return;
@@ -699,16 +661,15 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 // direct-to-LDS loads (buffer_load ... lds / global_load_lds): a tile's
 // loads are issued S-1 tiles before it is computed and cost no registers
 // while in flight, so one block of N waves per CU keeps ~(S-1) x 25 KB of
-// HBM reads outstanding.  Each direct load moves 16 bytes per lane to
-// LDS[slot + 16*lane]; a lane later reads back exactly what the same lane
+// reads outstanding.  Each direct load moves 16 bytes per lane to
+// LDS[unit + 16*lane]; a lane later reads back exactly what the same lane
 // index loaded, so every LDS read is a conflict-free 16-byte row.
 //
-// Work split: the items (column block cb, tile) are numbered
-// cb * ntiles + tile and block b takes the contiguous range
-// [b*per, (b+1)*per); grad_phi partials are flushed whenever the column
-// block changes, to slot b + cb of a [nblk + ncb - 1][M][N][DW] buffer
-// (b + cb is distinct for every (b, cb) pair met, because both grow along
-// the range), and summed per column block in the order of b.
+// Block (cb, split) owns the DW = 128 columns cb*DW.. of every stream and
+// the tiles split, split + nsplit, ...; blocks of one split read
+// neighbouring columns of the same token rows at about the same time, which
+// measured faster than giving every block an equal contiguous share of the
+// (column block, tile) items.
 //
 // Synchronisation per tile j (slot j % S):
 //   wait until this wave's loads of tile j have landed (s_waitcnt vmcnt;
@@ -739,8 +700,8 @@ template <int N> struct DmaCfg {
   static constexpr int LMIN = 4 + SHARED / N;    // fewest loads a wave issues per tile
 };
 
-constexpr int kDmaStages = 5;
-constexpr int kDmaMaxBlocks = 512;
+constexpr int kDmaStages = 5;                  // 125 KB of LDS: one block per CU
+constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
 constexpr uint32_t kBufferOob = 0x80000000u;   // buffer offset beyond every range: dropped / zero
 
 struct PreBwdDmaArgs {
@@ -753,12 +714,10 @@ struct PreBwdDmaArgs {
   const uint16_t* gTw;   // [ceil(T/16)][MT][64][2][4]
   const float4* coef;    // (T, N) {pre, inv, scale, 0}
   bf16_t* gx;
-  float* part;           // [nblk + ncb - 1][M][N][DW]
+  float* part;           // [nsplit][M][K] grad_phi partials
   int64_t T;
   int D;
-  int ncb;
   int64_t ntiles;
-  int64_t per;           // items per block
 };
 
 // s_waitcnt vmcnt(V) with the other counters left free (gfx9 encoding).
@@ -780,7 +739,7 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
   constexpr int VC = C::VC, VD = C::VD, DW = C::DW, TT = C::TT, UNITS = C::UNITS;
   constexpr int VM_START = (S - 2) * C::LMIN;               // before any grad_x store
   constexpr int VM_STEADY = (S - 2) * C::LMIN + (S - 1) * 4;
-  static_assert(N % 4 == 0 && S >= 2 && VM_STEADY < 64, "pipeline shape");
+  static_assert(N == 4 && S >= 2 && VM_STEADY < 64, "pipeline shape");
   __shared__ u32x4 ring[S * UNITS * kWave];
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -788,22 +747,17 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
   const int r = lane & 15, q = lane >> 4;
   const int D = a.D;
   const int64_t T = a.T, K = (int64_t)N * D, ntiles = a.ntiles;
-  const int64_t lin0 = (int64_t)blockIdx.x * a.per;
-  int64_t lin1 = lin0 + a.per;
-  if (lin1 > (int64_t)a.ncb * ntiles) lin1 = (int64_t)a.ncb * ntiles;
-  if (lin0 >= lin1) return;  // uniform over the block
-  const int64_t cnt = lin1 - lin0;
+  const int64_t tstep = gridDim.y;
+  const int64_t cnt = (ntiles - blockIdx.y + tstep - 1) / tstep;
+  if (cnt <= 0) return;  // uniform over the block
+  const int dl = blockIdx.x * DW + VC * r;  // first column of this lane
+  const bool colok = dl < D;
 
-  // Item counters advance incrementally (no 64-bit divisions in the loop):
-  // (icb, itile) is the next item to load, (ccb, ctile) the next to compute.
-  int64_t icb = lin0 / ntiles, itile = lin0 - icb * ntiles;
-  const int64_t cb0 = icb, tile0 = itile;
-
+  int64_t itile = blockIdx.y;  // next tile to load
   auto issue = [&](int64_t j) {
     const int64_t tile = itile, tb = tile * TT;
+    itile += tstep;
     const int nv = (int)(T - tb < TT ? T - tb : TT);
-    const int dl = (int)icb * DW + VC * r;
-    const bool colok = dl < D;
     u32x4* st = ring + (int)(j % S) * UNITS * kWave;
     const auto rx = rows_rsrc(a.x + tb * K, (int64_t)nv * K * 2);
 #pragma unroll
@@ -836,174 +790,144 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
         __builtin_amdgcn_global_load_lds((glb_void_t*)(a.coef + idx), dst, 16, 0, 0);
       }
     }
-    if (++itile == ntiles) {
-      itile = 0;
-      ++icb;
-    }
   };
+
+  // phi^T operands of the block's columns and the grad_phi accumulators
+  u32x4 pb[VC][MK][P];
+  {
+    const int64_t kcol = (int64_t)n * D + (colok ? dl : 0);
+#pragma unroll
+    for (int c = 0; c < VC; ++c)
+#pragma unroll
+      for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const u32x4 v = ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q);
+          pb[c][mk][p] = colok ? v : zero4();
+        }
+  }
+  floatx4 ph[MT][VC];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   // LDS reads are inline asm: the compiler does not track which ring slot a
   // direct-to-LDS load writes and would otherwise wait for all of them
-  // (vmcnt(0)) before every LDS read.  The explicit waits above order them.
+  // (vmcnt(0)) before every LDS read.  The explicit waits order them.
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)ring;
 
   for (int64_t j = 0; j < S - 1 && j < cnt; ++j) issue(j);
 
-  int64_t j = 0, ccb = cb0, ctile = tile0;
-  while (j < cnt) {
-    // one column block: phi^T operands in registers, grad_phi accumulators
-    const int dl = (int)ccb * DW + VC * r;
-    const bool colok = dl < D;
-    u32x4 pb[VC][MK][P];
-    {
-      const int64_t kcol = (int64_t)n * D + (colok ? dl : 0);
-#pragma unroll
-      for (int c = 0; c < VC; ++c)
-#pragma unroll
-        for (int mk = 0; mk < MK; ++mk)
-#pragma unroll
-          for (int p = 0; p < P; ++p) {
-            const u32x4 v = ld16(a.phiT + p * a.phiT_plane_stride + (kcol + c) * MP32 + 32 * mk + 8 * q);
-            pb[c][mk][p] = colok ? v : zero4();
-          }
+  int64_t ctile = blockIdx.y;
+  for (int64_t j = 0; j < cnt; ++j, ctile += tstep) {
+    // this wave's loads of tile j have landed once at most V newer vector
+    // memory operations are outstanding
+    if (j + S - 2 < cnt) {
+      if (j >= S - 1)
+        wait_vmcnt<VM_STEADY>();
+      else
+        wait_vmcnt<VM_START>();
+    } else {
+      wait_vmcnt<0>();
     }
-    floatx4 ph[MT][VC];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
+    const uint32_t la = sbase + lane * 16;
+    const uint32_t lx = la + C::X * 1024 + 4 * n * 1024;
+    const uint32_t lc = sbase + C::CF * 1024 + (4 * q * N + n) * 16;
+    u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) asm volatile("ds_read_b128 %0, %1" : "=v"(xr[e]) : "v"(lx + e * 1024));
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
+      asm volatile("ds_read_b128 %0, %1" : "=v"(gt[mt]) : "v"(la + (C::GT + mt) * 1024));
 #pragma unroll
-      for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int mk = 0; mk < MK; ++mk)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+        asm volatile("ds_read_b128 %0, %1" : "=v"(gA[mk][g]) : "v"(la + (C::GA + 2 * mk + g) * 1024));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      asm volatile("ds_read_b128 %0, %1" : "=v"(gr[e]) : "v"(la + (C::GY + e) * 1024));
+      asm volatile("ds_read_b128 %0, %1" : "=v"(cfu[e]) : "v"(lc + e * N * 16));
+    }
+    // the next loads go to the slot of tile j - 1, which every wave
+    // finished reading before the barrier
+    if (j + S - 1 < cnt) issue(j + S - 1);
+    static_assert(MK == 1 && MT == 2, "operand tie list below is written for N = 4");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(gt[0]), "+v"(gt[1]),
+                   "+v"(gA[0][0]), "+v"(gA[0][1]), "+v"(gr[0]), "+v"(gr[1]), "+v"(gr[2]), "+v"(gr[3]),
+                   "+v"(cfu[0]), "+v"(cfu[1]), "+v"(cfu[2]), "+v"(cfu[3]));
 
-    const int64_t seg_end = j + (ntiles - ctile) < cnt ? j + (ntiles - ctile) : cnt;
-    for (; j < seg_end; ++j, ++ctile) {
-      // this wave's loads of tile j have landed once at most V newer vector
-      // memory operations are outstanding
-      if (j + S - 2 < cnt) {
-        if (j >= S - 1)
-          wait_vmcnt<VM_STEADY>();
-        else
-          wait_vmcnt<VM_START>();
-      } else {
-        wait_vmcnt<0>();
-      }
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
+    const int64_t tb = ctile * TT;
+    const int nv = (int)(T - tb < TT ? T - tb : TT);
 
-      const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
-      const uint32_t la = sbase + lane * 16;
-      const uint32_t lx = la + C::X * 1024 + 4 * n * 1024;
-      const uint32_t lc = sbase + C::CF * 1024 + (4 * q * N + n) * 16;
-      u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
+    // ---- grad_phi partial += g^T @ x over the tile's 16 tokens ------------
 #pragma unroll
-      for (int e = 0; e < 4; ++e) asm volatile("ds_read_b128 %0, %1" : "=v"(xr[e]) : "v"(lx + e * 1024));
+    for (int c = 0; c < VC; ++c) {
+      u32x2 xt;  // column c of the lane's 4 x VC block: tokens (2w, 2w+1) in dword w
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        asm volatile("ds_read_b128 %0, %1" : "=v"(gt[mt]) : "v"(la + (C::GT + mt) * 1024));
-#pragma unroll
-      for (int mk = 0; mk < MK; ++mk)
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-          asm volatile("ds_read_b128 %0, %1" : "=v"(gA[mk][g]) : "v"(la + (C::GA + 2 * mk + g) * 1024));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        asm volatile("ds_read_b128 %0, %1" : "=v"(gr[e]) : "v"(la + (C::GY + e) * 1024));
-        asm volatile("ds_read_b128 %0, %1" : "=v"(cfu[e]) : "v"(lc + e * N * 16));
+      for (int w = 0; w < 2; ++w) {
+        const uint32_t lo = xr[2 * w][c >> 1], hi = xr[2 * w + 1][c >> 1];
+        xt[w] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
       }
-      // the next loads go to the slot of tile j - 1, which every wave
-      // finished reading before the barrier
-      if (j + S - 1 < cnt) issue(j + S - 1);
-      static_assert(MK == 1 && MT == 2, "operand tie list below is written for N = 4");
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(gt[0]), "+v"(gt[1]),
-                     "+v"(gA[0][0]), "+v"(gA[0][1]), "+v"(gr[0]), "+v"(gr[1]), "+v"(gr[2]), "+v"(gr[3]),
-                     "+v"(cfu[0]), "+v"(cfu[1]), "+v"(cfu[2]), "+v"(cfu[3]));
-
-      const int64_t tb = ctile * TT;
-      const int nv = (int)(T - tb < TT ? T - tb : TT);
-
-      // ---- grad_phi partial += g^T @ x over the tile's 16 tokens ----------
 #pragma unroll
-      for (int c = 0; c < VC; ++c) {
-        u32x2 xt;  // column c of the lane's 4 x VC block: tokens (2w, 2w+1) in dword w
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-          const uint32_t lo = xr[2 * w][c >> 1], hi = xr[2 * w + 1][c >> 1];
-          xt[w] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          ph[mt][c] = mfma16x16x16(u32x2{gt[mt][0], gt[mt][1]}, xt, ph[mt][c]);
-          ph[mt][c] = mfma16x16x16(u32x2{gt[mt][2], gt[mt][3]}, xt, ph[mt][c]);
-        }
-      }
-      // ---- gs = grad_mixes @ phi, then grad_x -------------------------------
-      floatx4 gs[VC];
-#pragma unroll
-      for (int c = 0; c < VC; ++c) {
-        gs[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int mk = 0; mk < MK; ++mk) {
-          gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][0]), gs[c]);
-          gs[c] = mfma16x16x32(as_bf16x8(gA[mk][1]), as_bf16x8(pb[c][mk][0]), gs[c]);
-          if constexpr (P > 1) gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][P - 1]), gs[c]);
-        }
-      }
-      const auto rgx = rows_rsrc(a.gx + tb * K, (int64_t)nv * K * 2);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // pre[t,n], inv[t], scale[t]
-        const float fx = __uint_as_float(cfu[e][0]), fy = __uint_as_float(cfu[e][1]),
-                    fz = __uint_as_float(cfu[e][2]);
-        u32x4 o;
-#pragma unroll
-        for (int w = 0; w < VD; ++w) {
-          const uint32_t xw = xr[e][w], gw = gr[e][w];
-          const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
-          const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
-          const float o0 = fmaf(fz, x0, fmaf(fy, gs[2 * w][e], g0 * fx));
-          const float o1 = fmaf(fz, x1, fmaf(fy, gs[2 * w + 1][e], g1 * fx));
-          o[w] = pack_bf16x2(o0, o1);
-        }
-        // rows >= nv fall outside the range and are dropped, as are columns >= D
-        const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
-        __builtin_amdgcn_raw_buffer_store_b128(o, rgx, off, 0, 0);
+      for (int mt = 0; mt < MT; ++mt) {
+        ph[mt][c] = mfma16x16x16(u32x2{gt[mt][0], gt[mt][1]}, xt, ph[mt][c]);
+        ph[mt][c] = mfma16x16x16(u32x2{gt[mt][2], gt[mt][3]}, xt, ph[mt][c]);
       }
     }
-
-    // flush the column block's grad_phi partial to slot blockIdx.x + ccb
-    float* part = a.part + ((((int64_t)blockIdx.x + ccb) * M) * N + n) * DW + VC * r;
+    // ---- gs = grad_mixes @ phi, then grad_x ---------------------------------
+    floatx4 gs[VC];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int c = 0; c < VC; ++c) {
+      gs[c] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int m = 16 * mt + 4 * q + v;
-        if (m >= M) continue;
-        float4* dst = reinterpret_cast<float4*>(part + (int64_t)m * N * DW);
-        dst[0] = float4{ph[mt][0][v], ph[mt][1][v], ph[mt][2][v], ph[mt][3][v]};
-        dst[1] = float4{ph[mt][4][v], ph[mt][5][v], ph[mt][6][v], ph[mt][7][v]};
+      for (int mk = 0; mk < MK; ++mk) {
+        gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][0]), gs[c]);
+        gs[c] = mfma16x16x32(as_bf16x8(gA[mk][1]), as_bf16x8(pb[c][mk][0]), gs[c]);
+        if constexpr (P > 1) gs[c] = mfma16x16x32(as_bf16x8(gA[mk][0]), as_bf16x8(pb[c][mk][P - 1]), gs[c]);
       }
-    ++ccb;
-    ctile = 0;
+    }
+    const auto rgx = rows_rsrc(a.gx + tb * K, (int64_t)nv * K * 2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // pre[t,n], inv[t], scale[t]
+      const float fx = __uint_as_float(cfu[e][0]), fy = __uint_as_float(cfu[e][1]),
+                  fz = __uint_as_float(cfu[e][2]);
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < VD; ++w) {
+        const uint32_t xw = xr[e][w], gw = gr[e][w];
+        const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
+        const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
+        const float o0 = fmaf(fz, x0, fmaf(fy, gs[2 * w][e], g0 * fx));
+        const float o1 = fmaf(fz, x1, fmaf(fy, gs[2 * w + 1][e], g1 * fx));
+        o[w] = pack_bf16x2(o0, o1);
+      }
+      // rows >= nv fall outside the range and are dropped, as are columns >= D
+      const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
+      __builtin_amdgcn_raw_buffer_store_b128(o, rgx, off, 0, 0);
+    }
   }
-}
 
-// grad_phi[m, n*D + d] = sum over the blocks b that met column block
-// cb = d / DW of part[b + cb][m][n][d % DW], in the order of b.
-template <int N>
-__global__ void sum_dma_parts_kernel(const float* __restrict__ part, float* __restrict__ gphi, int D,
-                                     int64_t ntiles, int64_t per) {
-  constexpr int M = PreDims<N>::M, DW = DmaCfg<N>::DW;
-  const int64_t K = (int64_t)N * D, total = (int64_t)M * K;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t m = i / K, k = i - m * K;
-    const int n = (int)(k / D), d = (int)(k - (int64_t)n * D);
-    const int64_t cb = d / DW;
-    const int64_t b0 = cb * ntiles / per, b1 = ((cb + 1) * ntiles - 1) / per;
-    float s = 0.f;
-    for (int64_t b = b0; b <= b1; ++b) s += part[(((b + cb) * M + m) * N + n) * DW + d % DW];
-    gphi[i] = s;
-  }
+  if (!colok) return;
+  float* part = a.part + (int64_t)blockIdx.y * M * K + (int64_t)n * D + dl;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 16 * mt + 4 * q + v;
+      if (m >= M) continue;
+      float4* dst = reinterpret_cast<float4*>(part + (int64_t)m * K);
+      dst[0] = float4{ph[mt][0][v], ph[mt][1][v], ph[mt][2][v], ph[mt][3][v]};
+      dst[1] = float4{ph[mt][4][v], ph[mt][5][v], ph[mt][6][v], ph[mt][7][v]};
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1052,6 +976,14 @@ struct BwdLayout {
   size_t off_gmP, off_gTw, off_coef, total;
 };
 
+// Token splits of the grad_phi partials: kMaxSplits for the split kernels,
+// more for the LDS-pipelined kernel when D has few 128-column blocks.
+static int64_t dma_max_splits(int D) {
+  const int64_t ncb = (D + DmaCfg<4>::DW - 1) / DmaCfg<4>::DW;
+  const int64_t s = kDmaMaxBlocks / ncb;
+  return s > kMaxSplits ? s : kMaxSplits;
+}
+
 // Workspace layout.  It covers both forms of kernel B (the streaming one for
 // bf16 activations and the LDS-staged one for the other dtypes / unaligned
 // rows), so the size depends only on (T, N, D, phi dtype, iterations).
@@ -1087,14 +1019,7 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   b.off_partial = off;
   off += align256((size_t)b.nblkA * b.C * 4);
   b.off_gphi = off;
-  {
-    // grad_phi partials: [kMaxSplits][M][K] for the split kernels, or
-    // [blocks + column blocks - 1][M][N][DW] for the LDS-pipelined one
-    const size_t ncb = (size_t)(D + DmaCfg<4>::DW - 1) / DmaCfg<4>::DW;
-    const size_t split_parts = (size_t)kMaxSplits * b.M * b.K;
-    const size_t dma_parts = (kDmaMaxBlocks + ncb - 1) * b.M * N * DmaCfg<4>::DW;
-    off += align256((split_parts > dma_parts ? split_parts : dma_parts) * 4);
-  }
+  off += align256((size_t)dma_max_splits(D) * b.M * b.K * 4);  // grad_phi split partials
   b.off_gmP = off;
   off += align256((size_t)2 * T * b.MP32 * 2);
   b.off_gTw = off;
@@ -1170,8 +1095,7 @@ static int reduce_tail(const BwdLayout& lay, const PreBwdSmallArgs& sa, const fl
   return sum_alpha_base(lay, sa, grad_alpha, grad_base, st);
 }
 
-// The LDS ring needs 16 * N * D * 2 bytes (one tile of x rows) to fit a
-// buffer range, and one block per CU.
+// Buffer ranges are 32-bit: one tile of x rows (16 * N * D bf16) must fit.
 template <int N>
 static bool dma_usable(int D) {
   return N == 4 && (int64_t)DmaCfg<N>::TT * N * D * 2 < ((int64_t)1 << 31);
@@ -1183,12 +1107,12 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* 
   constexpr int DW = DmaCfg<N>::DW;
   const int D = sta.D;
   const int64_t ncb = (D + DW - 1) / DW;
-  const int64_t total = ncb * lay.ntiles;
-  int64_t nblk = device_cus();  // the LDS ring takes most of a CU: one block each
-  if (nblk > kDmaMaxBlocks) nblk = kDmaMaxBlocks;
-  if (nblk > total) nblk = total;
-  const int64_t per = (total + nblk - 1) / nblk;
-  nblk = (total + per - 1) / per;
+  // one block per CU (the ring fills the LDS); as many token splits as fit
+  // next to the column blocks in one wave of blocks
+  int64_t ns = device_cus() / ncb;
+  if (ns > dma_max_splits(D)) ns = dma_max_splits(D);
+  if (ns > lay.ntiles) ns = lay.ntiles;
+  if (ns < 1) ns = 1;
   PreBwdDmaArgs da{};
   da.x = sta.x;
   da.gy = sta.gy;
@@ -1202,16 +1126,15 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* 
   da.part = sta.gphi_part;
   da.T = sta.T;
   da.D = D;
-  da.ncb = (int)ncb;
   da.ntiles = lay.ntiles;
-  da.per = per;
-  hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages>), dim3((unsigned)nblk), dim3(64 * N), 0, st,
-                     da);
+  hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages>), dim3((unsigned)ncb, (unsigned)ns), dim3(64 * N), 0,
+                     st, da);
   int rc = check_launch("pre_bwd_dma");
   if (rc) return rc;
-  hipLaunchKernelGGL((sum_dma_parts_kernel<N>), dim3(reduce_grid((int64_t)lay.M * lay.K)), dim3(256), 0,
-                     st, sta.gphi_part, grad_phi, D, lay.ntiles, per);
-  return check_launch("pre_bwd_sum_dma_parts");
+  const int64_t n = (int64_t)lay.M * lay.K;
+  hipLaunchKernelGGL(sum_splits_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, sta.gphi_part, grad_phi, n,
+                     (int)ns);
+  return check_launch("pre_bwd_sum_splits");
 }
 
 template <int N, typename S>

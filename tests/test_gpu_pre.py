@@ -112,8 +112,10 @@ BWD_CASES = [
     # LDS-pipelined grad_x/grad_phi kernel (N=4, bf16, D % 8 == 0): work ranges
     # that cross column blocks, a partial last column block, a ragged last tile
     (1010, 4, 1288, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
-    # ranges spanning three column blocks (more column blocks than CUs)
+    # more column blocks than CUs (several waves of blocks)
     (17, 4, 40000, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    # few column blocks: many more token splits of the grad_phi partials
+    (4000, 4, 256, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
 ]
 
 
