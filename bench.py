@@ -77,6 +77,40 @@ def run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
     return out, yp, (gx1, g_hres, g_hout, g_hpost), (gx2, gphi, ga, gb)
 
 
+# operators that are one kernel launch at the bench shapes -> that kernel
+SINGLE_KERNEL_OPS = {
+    "pre_fwd": "pre_fwd_kernel<4, bf16_t, true, 1>",
+    "post_fwd": "post_fwd_kernel<4, bf16_t, true>",
+    "post_bwd": "post_bwd_kernel<4, bf16_t, true>",
+}
+
+
+def measured_traffic(op):
+    """HBM bytes per launch of the op's kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy of known
+    size), or None when no summary for it is committed."""
+    path = os.path.join(ROOT, "profiles", "c5_pmc_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["ops"][op]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def pmc_probe(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
+    """One chain step plus a plain 1 GiB device copy, for rocprofv3 --pmc runs:
+    the copy's FETCH_SIZE / WRITE_SIZE give the counters' scale."""
+    import torch
+
+    run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)
+    src = torch.ones(1 << 29, dtype=torch.bfloat16, device=x.device)   # 1 GiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": "done", "copy_bytes": 1 << 30}), flush=True)
+
+
 def time_events(fn, reps, stream):
     import torch
 
@@ -169,6 +203,8 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=3072, help="oracle tokens for cpu_baseline")
     ap.add_argument("--ref-sample", type=int, default=8192, help="torch *_ref tokens on CPU")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run one step and a 1 GiB copy (for rocprofv3 --pmc), no timing")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -192,6 +228,9 @@ def main():
     out = _pre_forward(x, phi, alpha, base, need_backward=True, want_x_scaled=False, **kw)
     h_out = out["y"] + noise
     stream = torch.cuda.current_stream(dev)
+    if args.pmc_probe:
+        pmc_probe(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)
+        return
 
     step = lambda: run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)
     for _ in range(args.warmup):
@@ -232,8 +271,11 @@ def main():
         "h_out_add_ms": round(time_events(lambda: out["y"] + noise, reps, stream)[1], 4),
         "grad_x_accumulate_ms": round(time_events(lambda: pb[0] + res[3][0], reps, stream)[1], 4),
     }
-    dominant = max(op_stats, key=lambda k: op_stats[k]["ms"])
+    # roofline of the dominant kernel: the longest of the operators that run
+    # as a single kernel (pre_bwd is four kernels; its largest is shorter)
+    dominant = max(SINGLE_KERNEL_OPS, key=lambda k: op_stats[k]["ms"])
     dom = op_stats[dominant]
+    traffic = measured_traffic(dominant)
     mhc_ms = sum(v["ms"] for v in op_stats.values())
     chain_bytes = sum(algo.values())
 
@@ -254,9 +296,10 @@ def main():
                    "N": N, "D": D, "T": T, "B": 8, "S": T // 8, "clamp": [-10.0, 10.0],
                    "iter_times": 20, "phi": [2 * N + N * N, N * D]},
         "hbm_frac_chain": round(chain_bytes / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": dom["GBps"],
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": dom["frac_hbm"],
-                     "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": SINGLE_KERNEL_OPS[dominant],
+                     "achieved": dom["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": dom["frac_hbm"], "traffic": traffic,
+                     "algo_bytes": algo[dominant]},
         "ops": op_stats,
         "mhc_ops_ms": round(mhc_ms, 4),
         "glue": glue,
