@@ -682,9 +682,6 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 // loads); grad_mixes rows and coefficients of tokens >= T load from the
 // clamped last token and only reach outputs that are not stored.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
-
 template <int N> struct DmaCfg {
   using PD = PreDims<N>;
   static constexpr int VC = 8, VD = 4, DW = 128, TT = 16;
@@ -702,7 +699,6 @@ template <int N> struct DmaCfg {
 
 constexpr int kDmaStages = 5;                  // 125 KB of LDS: one block per CU
 constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
-constexpr uint32_t kBufferOob = 0x80000000u;   // buffer offset beyond every range: dropped / zero
 
 struct PreBwdDmaArgs {
   const bf16_t* x;
@@ -719,17 +715,6 @@ struct PreBwdDmaArgs {
   int D;
   int64_t ntiles;
 };
-
-// s_waitcnt vmcnt(V) with the other counters left free (gfx9 encoding).
-template <int V>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(V >= 0 && V < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (15 << 8) | ((V >> 4) << 14));
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
 
 template <int N, int P, int S>
 __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
@@ -812,10 +797,9 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
 #pragma unroll
     for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // LDS reads are inline asm: the compiler does not track which ring slot a
-  // direct-to-LDS load writes and would otherwise wait for all of them
-  // (vmcnt(0)) before every LDS read.  The explicit waits order them.
-  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)ring;
+  // LDS reads of the ring are inline asm (ds_read16): the explicit waits
+  // order them after the direct-to-LDS loads.
+  const uint32_t ring_lds = lds_addr(ring);
 
   for (int64_t j = 0; j < S - 1 && j < cnt; ++j) issue(j);
 
@@ -841,19 +825,17 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
     const uint32_t lc = sbase + C::CF * 1024 + (4 * q * N + n) * 16;
     u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) asm volatile("ds_read_b128 %0, %1" : "=v"(xr[e]) : "v"(lx + e * 1024));
+    for (int e = 0; e < 4; ++e) xr[e] = ds_read16(lx + e * 1024);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      asm volatile("ds_read_b128 %0, %1" : "=v"(gt[mt]) : "v"(la + (C::GT + mt) * 1024));
+    for (int mt = 0; mt < MT; ++mt) gt[mt] = ds_read16(la + (C::GT + mt) * 1024);
 #pragma unroll
     for (int mk = 0; mk < MK; ++mk)
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
-        asm volatile("ds_read_b128 %0, %1" : "=v"(gA[mk][g]) : "v"(la + (C::GA + 2 * mk + g) * 1024));
+      for (int g = 0; g < 2; ++g) gA[mk][g] = ds_read16(la + (C::GA + 2 * mk + g) * 1024);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      asm volatile("ds_read_b128 %0, %1" : "=v"(gr[e]) : "v"(la + (C::GY + e) * 1024));
-      asm volatile("ds_read_b128 %0, %1" : "=v"(cfu[e]) : "v"(lc + e * N * 16));
+      gr[e] = ds_read16(la + (C::GY + e) * 1024);
+      cfu[e] = ds_read16(lc + e * N * 16);
     }
     // the next loads go to the slot of tile j - 1, which every wave
     // finished reading before the barrier

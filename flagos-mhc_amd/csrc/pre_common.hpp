@@ -22,6 +22,45 @@ __device__ __forceinline__ floatx4 mfma16x16x32(const bf16x8& a, const bf16x8& b
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 
+// ---- direct-to-LDS loads and range-checked buffer accesses -----------------
+// buffer_load ... lds / global_load_lds move 16 bytes per lane to
+// LDS[base + 16*lane] and count in vmcnt like any vector memory operation
+// (which complete in issue order); a raw buffer access whose offset is
+// beyond the resource's byte range loads zero / stores nothing.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+constexpr uint32_t kBufferOob = 0x80000000u;  // buffer offset beyond every range
+
+// Resource covering `bytes` bytes from `base` (raw buffer: stride 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// s_waitcnt vmcnt(V) with the other counters left free (gfx9 encoding).
+template <int V>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(V >= 0 && V < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (15 << 8) | ((V >> 4) << 14));
+}
+
+// LDS byte address of a __shared__ object.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) T*)p;
+}
+
+// 16-byte LDS read the compiler does not see as an LDS access: it would
+// otherwise wait for every outstanding direct-to-LDS load (vmcnt(0)) before
+// it.  The caller orders it after the loads it needs (wait_vmcnt + barrier)
+// and, before using the results, executes s_waitcnt lgkmcnt(0) in an asm
+// statement that takes them as in/out operands.
+__device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
 __device__ __forceinline__ u32x4 zero4() {
   u32x4 z;
   z[0] = z[1] = z[2] = z[3] = 0u;

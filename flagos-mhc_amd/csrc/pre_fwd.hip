@@ -287,6 +287,296 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_kernel(PreFwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-pipelined form: N = 4, bf16 x and phi (phi used in place), D % 8 == 0,
+// 16-byte aligned rows.
+//
+// A persistent block per CU walks its 64-token tiles; every tile is two
+// streams of stages through one ring of S stage slots in LDS, filled by
+// direct-to-LDS loads issued S-1 stages ahead (no registers held by loads
+// in flight):
+//   contraction stages (128 columns of K each): x[64 tokens][128] (16 KB)
+//     and phi[32 rows][128] (8 KB, rows >= M zero).  Wave w multiplies row
+//     block w (tokens 16w..16w+15) by all of phi: no cross-wave reduction.
+//   y stages (4 tokens x 512 columns of d): x[4][4 streams][512] (16 KB);
+//     wave w forms y of token w, lane l its 8 columns 8l.. locally
+//     (y = sum_n pre[n] * x[n]), so a y store moves 1 KB of one row.
+// A contraction load instruction moves 4 rows x 256 contiguous bytes, a y
+// load one row x 1 KB.  In a contraction slot a row is 256 bytes with its
+// 16-byte chunks XOR-swizzled
+// by (row & 15), so the MFMA operand reads (16 rows, one chunk each) hit 16
+// different chunk positions: conflict-free.  After the last contraction
+// stage the wave's accumulators give mixes; heads and Sinkhorn run as in
+// the generic kernel while the first y stages are already loading.
+// ---------------------------------------------------------------------------
+constexpr int kFwdDmaStages = 4;
+constexpr int kFwdDmaUnits = 24;  // 1 KB units per stage slot
+
+template <bool XS>
+__global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) {
+  constexpr int N = 4, M = PreDims<N>::M, L = N * N, TT = kFwdTile, S = kFwdDmaStages;
+  constexpr int CW = 128;                  // K columns per contraction stage
+  constexpr int YW = 512;                  // d columns per y stage
+  constexpr int YST = XS ? 9 : 1;          // buffer stores per lane and y stage
+  constexpr int VM_C = (S - 2) * 6;        // window of contraction stages only
+  constexpr int VM_Y = (S - 2) * 4 + (S - 1) * YST;  // window of y stages only
+  constexpr int VM_MIN = (S - 2) * 4;      // any window: fewest loads per stage
+  static_assert(VM_Y < 64 && VM_C < 64, "vmcnt range");
+  __shared__ u32x4 ring[S * kFwdDmaUnits * kWave];
+  __shared__ float mix_sh[TT][M + 1];
+  __shared__ __align__(16) float pre_sh[TT][N];
+  __shared__ __align__(16) float inv_sh[TT];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int D = a.D;
+  static_assert(sizeof(pre_sh[0]) == 16, "pre of a token is one 16-byte LDS read");
+  const int K = N * D;
+  const int64_t T = a.T;
+  const int nst_c = (K + CW - 1) / CW;
+  const int ncb = (D + YW - 1) / YW;
+  const int per_tile = nst_c + (TT / 4) * ncb;
+  const int64_t ntiles = (T + TT - 1) / TT;
+  const int64_t my_tiles = (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
+  if (my_tiles <= 0) return;  // uniform over the block
+  const int64_t J = my_tiles * per_tile;
+  const bf16_t* __restrict__ x = static_cast<const bf16_t*>(a.x);
+  const auto rphi = rows_rsrc(a.phi, (int64_t)M * K * 2);
+
+  // per-thread constants of the heads / Sinkhorn step
+  const int e = tid % L;
+  const float a0 = a.alpha[0], a1 = a.alpha[1], a2 = a.alpha[2];
+  const float base_l = a.base[2 * N + e];
+  const float base_h = e < 2 * N ? a.base[e] : 0.f;
+
+  // ---- loads of stage j --------------------------------------------------
+  int64_t itile = blockIdx.x;  // tile and stage of the next issue
+  int is = 0;
+  auto issue = [&](int64_t j) {
+    const int64_t tb = itile * TT;
+    const int nv = (int)(T - tb < TT ? T - tb : TT);
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kFwdDmaUnits * 1024);
+    const auto rx = rows_rsrc(x + tb * K, (int64_t)nv * K * 2);
+    if (is < nst_c) {
+      const int k0 = is * CW;
+      // units 0..15: x rows 4u..4u+3 (u = wave + 4i); 16..23: phi rows
+      // 4(u-16)..+3 (u = 16 + wave + 4i); row chunks XOR-swizzled by row & 15
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        const int u = wave + 4 * i;
+        const int row = 4 * (wave + 4 * (i & 3)) + q;
+        const int k = k0 + 8 * (r ^ (row & 15));
+        const uint32_t off = k < K ? (uint32_t)(((int64_t)row * K + k) * 2) : kBufferOob;
+        lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
+        if (i < 4)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2 /* nt */);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, off, 0, 0, 0);
+      }
+    } else {
+      // unit n + 4i: token 4*tg + i, stream n = wave, columns cb*512 + 8*lane
+      const int sy = is - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
+      const int col = cb * YW + 8 * lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + (wave + 4 * i) * 1024);
+        const uint32_t off =
+            col < D ? (uint32_t)((((int64_t)(4 * tg + i) * N + wave) * D + col) * 2) : kBufferOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2);
+      }
+    }
+    if (++is == per_tile) {
+      is = 0;
+      itile += gridDim.x;
+    }
+  };
+
+  for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
+
+  floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  float ssq = 0.f;
+  int64_t ctile = blockIdx.x;
+  int cs = 0;  // stage of the current tile being consumed
+  for (int64_t j = 0; j < J; ++j) {
+    // this wave's loads of stage j have landed once at most V newer vector
+    // memory operations are outstanding (windows of one stage kind get the
+    // exact count, mixed windows the smallest)
+    if (j + S - 2 < J) {
+      if (cs >= S - 1 && cs + S - 2 < nst_c)
+        wait_vmcnt<VM_C>();
+      else if (cs >= nst_c + S - 1 && cs + S - 2 < per_tile)
+        wait_vmcnt<VM_Y>();
+      else
+        wait_vmcnt<VM_MIN>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kFwdDmaUnits * 1024);
+    const int64_t tb = ctile * TT;
+
+    if (cs < nst_c) {
+      // ---- contraction stage: row block `wave` x all of phi ----------------
+      u32x4 A[4], B[2][4];
+      const int row = 16 * wave + r;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        A[g] = ds_read16(slot + row * 256 + (((4 * g + q) ^ r) << 4));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          B[mt][g] = ds_read16(slot + 16 * 1024 + (16 * mt + r) * 256 + (((4 * g + q) ^ r) << 4));
+      }
+      if (j + S - 1 < J) issue(j + S - 1);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(B[0][0]), "+v"(B[0][1]),
+                     "+v"(B[0][2]), "+v"(B[0][3]), "+v"(B[1][0]), "+v"(B[1][1]), "+v"(B[1][2]),
+                     "+v"(B[1][3]));
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = __uint_as_float(A[g][i] << 16), hi = __uint_as_float(A[g][i] & 0xffff0000u);
+          ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) acc[mt] = mfma16x16x32(as_bf16x8(A[g]), as_bf16x8(B[mt][g]), acc[mt]);
+      }
+
+      if (cs == nst_c - 1) {
+        // ---- tile's mixes, heads and Sinkhorn -----------------------------
+        // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; the
+        // lane of row r (any q) holds sum(x^2) of token 16*wave + r
+        ssq += __shfl_xor(ssq, 16, kWave);
+        ssq += __shfl_xor(ssq, 32, kWave);
+        const float inv_row = 1.0f / sqrtf(ssq / (float)K + a.norm_eps);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float inv = __shfl(inv_row, 4 * q + v, kWave);
+          const int tt = 16 * wave + 4 * q + v;
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            if (16 * mt + r < M) mix_sh[tt][16 * mt + r] = acc[mt][v] * inv;
+        }
+        if (q == 0) inv_sh[16 * wave + r] = inv_row;
+        acc[0] = acc[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ssq = 0.f;
+        __syncthreads();
+        if (a.mixes) {
+          for (int idx = tid; idx < TT * M; idx += kFwdThreads) {
+            const int tt = idx / M, m = idx - (idx / M) * M;
+            if (tb + tt < T) a.mixes[(tb + tt) * M + m] = mix_sh[tt][m];
+          }
+        }
+        if (a.inv_rms && tid < TT && tb + tid < T) a.inv_rms[tb + tid] = inv_sh[tid];
+        constexpr int TPP = kFwdThreads / L;
+#pragma unroll 1
+        for (int ps = 0; ps < TT / TPP; ++ps) {
+          const int tt = ps * TPP + tid / L;
+          const int64_t tok = tb + tt;
+          const bool ok = tok < T;
+          const float logit = mix_sh[tt][2 * N + e] * a2 + base_l;
+          const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
+          const float c = sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
+          if (ok) {
+            a.comb[tok * L + e] = c;
+            if (a.logits) a.logits[tok * L + e] = logit;
+          }
+          if (e < N) {
+            const float p = sigmoidf_(mix_sh[tt][e] * a0 + base_h) + a.hc_eps;
+            pre_sh[tt][e] = p;
+            if (ok && a.pre) a.pre[tok * N + e] = p;
+          } else if (e < 2 * N) {
+            const float po = 2.0f * sigmoidf_(mix_sh[tt][e] * a1 + base_h);
+            if (ok) a.post_out[tok * N + (e - N)] = po;
+          }
+        }
+        __syncthreads();
+      }
+    } else {
+      // ---- y stage: wave w -> token 4*tg + w, lane -> 8 columns ------------
+      const int sy = cs - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
+      const int t = 4 * tg + wave;  // token within the tile
+      u32x4 X[N], P, I = zero4();
+#pragma unroll
+      for (int n = 0; n < N; ++n) X[n] = ds_read16(slot + ((n + 4 * wave) * kWave + lane) * 16);
+      P = ds_read16(lds_addr(&pre_sh[t][0]));  // the same address on every lane: broadcast
+      if constexpr (XS) I = ds_read16(lds_addr(&inv_sh[t]) & ~15u);
+      if (j + S - 1 < J) issue(j + S - 1);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(X[0]), "+v"(X[1]), "+v"(X[2]), "+v"(X[3]), "+v"(P), "+v"(I));
+      const int nv = (int)(T - tb < TT ? T - tb : TT);
+      const int col = cb * YW + 8 * lane;
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const float p = __uint_as_float(P[n]);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          o[2 * w] = fmaf(p, __uint_as_float(X[n][w] << 16), o[2 * w]);
+          o[2 * w + 1] = fmaf(p, __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
+        }
+      }
+      u32x4 ov;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
+      // rows >= nv fall outside the range and are dropped, as are columns >= D
+      const auto ry = rows_rsrc(static_cast<bf16_t*>(a.y) + tb * D, (int64_t)nv * D * 2);
+      __builtin_amdgcn_raw_buffer_store_b128(ov, ry, col < D ? (uint32_t)(((int64_t)t * D + col) * 2) : kBufferOob,
+                                             0, 2 /* nt */);
+      if constexpr (XS) {
+        const float inv = __uint_as_float(I[t & 3]);
+        const auto rs = rows_rsrc(a.x_scaled + tb * K, (int64_t)nv * K * 4);
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            u32x4 xs;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              const uint32_t xw = X[n][2 * h + w];
+              xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv);
+              xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv);
+            }
+            const uint32_t off =
+                col < D ? (uint32_t)(((((int64_t)t * N + n) * D) + col + 4 * h) * 4) : kBufferOob;
+            __builtin_amdgcn_raw_buffer_store_b128(xs, rs, off, 0, 0);
+          }
+      }
+    }
+    if (++cs == per_tile) {
+      cs = 0;
+      ctile += gridDim.x;
+    }
+  }
+}
+
+// The LDS-pipelined kernel covers the bf16 fast path of N = 4.  Buffer
+// ranges are 32-bit: a tile of x rows (64 * 4 * D, fp32 x_scaled) must fit.
+static bool fwd_dma_usable(const PreFwdArgs& a, int N, bool bf16x, bool vec) {
+  return N == 4 && bf16x && vec && a.phi_planes == 1 && a.phi_ld == (int64_t)N * a.D &&
+         (int64_t)kFwdTile * N * a.D * 4 < ((int64_t)1 << 31) && aligned16(a.phi);
+}
+
+static int launch_pre_fwd_dma(const PreFwdArgs& a, hipStream_t st) {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev] && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                    cus[dev] <= 0))
+    cus[dev] = 256;
+  const int64_t ntiles = (a.T + kFwdTile - 1) / kFwdTile;
+  const int64_t grid = ntiles < cus[dev] ? ntiles : cus[dev];  // one block per CU (LDS ring)
+  if (a.x_scaled)
+    hipLaunchKernelGGL(pre_fwd_dma_kernel<true>, dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(pre_fwd_dma_kernel<false>, dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+  return check_launch("pre_fwd_dma");
+}
+
 template <int N, typename S, int P>
 static int launch_pre_fwd_p(const PreFwdArgs& a, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((a.T + kFwdTile - 1) / kFwdTile)), block(kFwdThreads);
@@ -371,6 +661,7 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   a.T = T;
   a.D = D;
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(y) && (!x_scaled || aligned16(x_scaled));
+  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec)) return launch_pre_fwd_dma(a, st);
   switch (x_dtype) {
     case MHC_DTYPE_BF16: return dispatch_pre_fwd<bf16_t>(N, a, vec, st);
     case MHC_DTYPE_F16: return dispatch_pre_fwd<f16_t>(N, a, vec, st);

@@ -66,6 +66,10 @@ FWD_CASES = [
     (21, 8, 128, torch.bfloat16, torch.float32, "reftest", 3.0, 1),
     (64, 4, 256, torch.bfloat16, torch.bfloat16, "baseline", 1.0, 0),
     (48, 4, 128, torch.bfloat16, torch.bfloat16, "baseline", 0.5, 45),        # > 32 iterations
+    # LDS-pipelined kernel (N=4, bf16): partial last 128-column stages of K and
+    # of d, ragged last tile, several tiles per block
+    (100, 4, 520, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (20000, 4, 1288, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
 ]
 
 
