@@ -138,6 +138,10 @@ __device__ __forceinline__ void st16(void* p, const u32x4& v) {
 __device__ __forceinline__ u32x4 ld16nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
+// 16-byte streaming store (output not re-read by this kernel).
+__device__ __forceinline__ void st16nt(void* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 
 // ---------------------------------------------------------------------------
 // wave64 reductions

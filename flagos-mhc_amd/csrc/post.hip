@@ -12,9 +12,10 @@
 // (T, D); gates are fp32 (T, N, N) and (T, N).  A wave owns one token: the
 // N*N + N gates are wave-uniform scalar loads, every lane streams 16-byte
 // vectors of each of the N rows, accumulates in fp32 and stores with
-// round-to-nearest-even.  The backward's N*N + N dot products are reduced
-// across the wave once per token and written by plain stores (no atomics),
-// so results are deterministic.
+// round-to-nearest-even (streaming stores: outputs are not re-read here).
+// The backward's N*N + N dot products are reduced across the wave once per
+// token and written by plain stores (no atomics), so results are
+// deterministic.
 #include "common.hpp"
 #include "mhc_launch.hpp"
 
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(256) void post_fwd_kernel(
           for (int j = 0; j < N; ++j) acc = fmaf(hr[j * N + i], xv[j][e], acc);
           o[e] = acc;
         }
-        st16(y + xrow + (int64_t)i * D + d, Store<S>::pack(o));
+        st16nt(y + xrow + (int64_t)i * D + d, Store<S>::pack(o));
       }
     }
   } else {
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
           for (int i = 0; i < N; ++i) a = fmaf(hr[j * N + i], gv[i][e], a);
           o[e] = a;
         }
-        st16(gx + xrow + (int64_t)j * D + d, Store<S>::pack(o));
+        st16nt(gx + xrow + (int64_t)j * D + d, Store<S>::pack(o));
       }
       float oh[V];
 #pragma unroll
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
         for (int i = 0; i < N; ++i) a = fmaf(hp[i], gv[i][e], a);
         oh[e] = a;
       }
-      st16(g_hout + hrow + d, Store<S>::pack(oh));
+      st16nt(g_hout + hrow + d, Store<S>::pack(oh));
 #pragma unroll
       for (int e = 0; e < V; ++e) {
 #pragma unroll
