@@ -79,7 +79,7 @@ def run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
 
 # operators that are one kernel launch at the bench shapes -> that kernel
 SINGLE_KERNEL_OPS = {
-    "pre_fwd": "pre_fwd_kernel<4, bf16_t, true, 1>",
+    "pre_fwd": "pre_fwd_dma_kernel<false>",
     "post_fwd": "post_fwd_kernel<4, bf16_t, true>",
     "post_bwd": "post_bwd_kernel<4, bf16_t, true>",
 }
