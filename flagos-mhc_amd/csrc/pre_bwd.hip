@@ -797,8 +797,8 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
 #pragma unroll
     for (int c = 0; c < VC; ++c) ph[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // LDS reads of the ring are inline asm (ds_read16): the explicit waits
-  // order them after the direct-to-LDS loads.
+  // LDS reads of the ring are inline asm (lds_read4), ordered after the
+  // direct-to-LDS loads by the explicit waits.
   const uint32_t ring_lds = lds_addr(ring);
 
   for (int64_t j = 0; j < S - 1 && j < cnt; ++j) issue(j);
@@ -819,32 +819,25 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
-    const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
-    const uint32_t la = sbase + lane * 16;
-    const uint32_t lx = la + C::X * 1024 + 4 * n * 1024;
-    const uint32_t lc = sbase + C::CF * 1024 + (4 * q * N + n) * 16;
-    u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xr[e] = ds_read16(lx + e * 1024);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) gt[mt] = ds_read16(la + (C::GT + mt) * 1024);
-#pragma unroll
-    for (int mk = 0; mk < MK; ++mk)
-#pragma unroll
-      for (int g = 0; g < 2; ++g) gA[mk][g] = ds_read16(la + (C::GA + 2 * mk + g) * 1024);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      gr[e] = ds_read16(la + (C::GY + e) * 1024);
-      cfu[e] = ds_read16(lc + e * N * 16);
-    }
     // the next loads go to the slot of tile j - 1, which every wave
     // finished reading before the barrier
     if (j + S - 1 < cnt) issue(j + S - 1);
-    static_assert(MK == 1 && MT == 2, "operand tie list below is written for N = 4");
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(gt[0]), "+v"(gt[1]),
-                   "+v"(gA[0][0]), "+v"(gA[0][1]), "+v"(gr[0]), "+v"(gr[1]), "+v"(gr[2]), "+v"(gr[3]),
-                   "+v"(cfu[0]), "+v"(cfu[1]), "+v"(cfu[2]), "+v"(cfu[3]));
+
+    const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
+    const uint32_t la = sbase + lane * 16;
+    static_assert(MK == 1 && MT == 2 && C::GY + 4 == C::GA && C::GA + 2 == C::GT, "unit order read below");
+    u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
+    lds_read4<1024>(xr, la + (C::X + 4 * n) * 1024);  // x rows of stream n, tokens 4q+e
+    lds_read4<1024>(gr, la + C::GY * 1024);           // grad_y rows
+    {
+      u32x4 ag[4];                                    // grad_mixes hi, lo; g^T blocks mt = 0, 1
+      lds_read4<1024>(ag, la + C::GA * 1024);
+      gA[0][0] = ag[0];
+      gA[0][1] = ag[1];
+      gt[0] = ag[2];
+      gt[1] = ag[3];
+    }
+    lds_read4<N * 16>(cfu, sbase + C::CF * 1024 + (4 * q * N + n) * 16);  // tokens 4q+e, stream n
 
     const int64_t tb = ctile * TT;
     const int nv = (int)(T - tb < TT ? T - tb : TT);

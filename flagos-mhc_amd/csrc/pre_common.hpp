@@ -50,15 +50,26 @@ __device__ __forceinline__ uint32_t lds_addr(T* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) T*)p;
 }
 
-// 16-byte LDS read the compiler does not see as an LDS access: it would
-// otherwise wait for every outstanding direct-to-LDS load (vmcnt(0)) before
-// it.  The caller orders it after the loads it needs (wait_vmcnt + barrier)
-// and, before using the results, executes s_waitcnt lgkmcnt(0) in an asm
-// statement that takes them as in/out operands.
-__device__ __forceinline__ u32x4 ds_read16(uint32_t addr) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
+// LDS reads of a ring slot are inline asm the compiler does not see as LDS
+// accesses (it would otherwise wait for every outstanding direct-to-LDS load,
+// vmcnt(0), before each of them).  The caller orders them after the loads
+// they need (wait_vmcnt + barrier).  Each asm statement issues its reads AND
+// waits for them (s_waitcnt lgkmcnt(0)) before it ends: an asm output that
+// the hardware writes after the statement could otherwise be copied, or its
+// register reused, before the data has landed.
+//   lds_read4(v, a, OFF): v[i] = 16 bytes at a + i * OFF, i = 0..3
+template <int OFF>
+__device__ __forceinline__ void lds_read4(u32x4 (&v)[4], uint32_t a) {
+  static_assert(3 * OFF < 65536, "ds_read offset field");
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %4 offset:%5\n\t"
+      "ds_read_b128 %2, %4 offset:%6\n\t"
+      "ds_read_b128 %3, %4 offset:%7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(a), "i"(OFF), "i"(2 * OFF), "i"(3 * OFF)
+      : "memory");
 }
 
 __device__ __forceinline__ u32x4 zero4() {

@@ -310,6 +310,13 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_kernel(PreFwdArgs a) {
 // the generic kernel while the first y stages are already loading.
 // ---------------------------------------------------------------------------
 constexpr int kFwdDmaStages = 4;
+
+// 16-byte LDS read, complete when the statement ends (see lds_read4).
+__device__ __forceinline__ u32x4 pre_sh4(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
 constexpr int kFwdDmaUnits = 24;  // 1 KB units per stage slot
 
 template <bool XS>
@@ -420,20 +427,34 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
 
     if (cs < nst_c) {
       // ---- contraction stage: row block `wave` x all of phi ----------------
-      u32x4 A[4], B[2][4];
-      const int row = 16 * wave + r;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        A[g] = ds_read16(slot + row * 256 + (((4 * g + q) ^ r) << 4));
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          B[mt][g] = ds_read16(slot + 16 * 1024 + (16 * mt + r) * 256 + (((4 * g + q) ^ r) << 4));
-      }
       if (j + S - 1 < J) issue(j + S - 1);
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(B[0][0]), "+v"(B[0][1]),
-                     "+v"(B[0][2]), "+v"(B[0][3]), "+v"(B[1][0]), "+v"(B[1][1]), "+v"(B[1][2]),
-                     "+v"(B[1][3]));
+      // chunk 4g+q of x row 16*wave + r and of phi rows r, 16 + r: the
+      // swizzled positions differ per g, so each read has its own address;
+      // phi row 16 + r sits 16 rows (4 KB) after row r
+      u32x4 A[4], B[2][4];
+      const uint32_t ca = slot + (16 * wave + r) * 256, cb0 = slot + 16 * 1024 + r * 256;
+      uint32_t sw[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) sw[g] = ((4 * g + q) ^ r) << 4;
+      asm volatile(
+          "ds_read_b128 %0, %12\n\t"
+          "ds_read_b128 %1, %13\n\t"
+          "ds_read_b128 %2, %14\n\t"
+          "ds_read_b128 %3, %15\n\t"
+          "ds_read_b128 %4, %16\n\t"
+          "ds_read_b128 %5, %17\n\t"
+          "ds_read_b128 %6, %18\n\t"
+          "ds_read_b128 %7, %19\n\t"
+          "ds_read_b128 %8, %16 offset:4096\n\t"
+          "ds_read_b128 %9, %17 offset:4096\n\t"
+          "ds_read_b128 %10, %18 offset:4096\n\t"
+          "ds_read_b128 %11, %19 offset:4096\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0][0]), "=&v"(B[0][1]),
+            "=&v"(B[0][2]), "=&v"(B[0][3]), "=&v"(B[1][0]), "=&v"(B[1][1]), "=&v"(B[1][2]), "=&v"(B[1][3])
+          : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
+            "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
+          : "memory");
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
 #pragma unroll
@@ -499,13 +520,12 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
       // ---- y stage: wave w -> token 4*tg + w, lane -> 8 columns ------------
       const int sy = cs - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
       const int t = 4 * tg + wave;  // token within the tile
-      u32x4 X[N], P, I = zero4();
-#pragma unroll
-      for (int n = 0; n < N; ++n) X[n] = ds_read16(slot + ((n + 4 * wave) * kWave + lane) * 16);
-      P = ds_read16(lds_addr(&pre_sh[t][0]));  // the same address on every lane: broadcast
-      if constexpr (XS) I = ds_read16(lds_addr(&inv_sh[t]) & ~15u);
       if (j + S - 1 < J) issue(j + S - 1);
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(X[0]), "+v"(X[1]), "+v"(X[2]), "+v"(X[3]), "+v"(P), "+v"(I));
+      u32x4 X[N], P, I = zero4();
+      lds_read4<1024>(X, slot + ((4 * wave) * kWave + lane) * 16);  // streams n = 0..3 of token t
+      // pre (and inv_rms) of token t: the same address on every lane, a broadcast
+      P = pre_sh4(lds_addr(&pre_sh[t][0]));
+      if constexpr (XS) I = pre_sh4(lds_addr(&inv_sh[t]) & ~15u);
       const int nv = (int)(T - tb < TT ? T - tb : TT);
       const int col = cb * YW + 8 * lane;
       float o[8];
