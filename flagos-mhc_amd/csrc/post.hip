@@ -16,7 +16,10 @@
 // The backward's N*N + N dot products are reduced across the wave once per
 // token and written by plain stores (no atomics), so results are
 // deterministic.
+#include <type_traits>
+
 #include "common.hpp"
+#include "lds_dma.hpp"
 #include "mhc_launch.hpp"
 
 namespace mhc {
@@ -186,6 +189,283 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// LDS-pipelined forms (bf16, 16-byte aligned rows, D % 8 == 0)
+//
+// Same arithmetic, but the input rows reach the lanes through direct-to-LDS
+// loads: every wave of a persistent grid owns a ring of S slots in
+// LDS, one slot = the R input rows of one token over 512 columns (one 1 KB
+// load per row, lane l -> columns 8l..8l+7), issued S-1 slots
+// ahead, so the loads in flight hold no registers and a wave keeps ~3 slots
+// of reads outstanding while it computes and stores.  A wave reads back only
+// what its own loads wrote (no barriers).  Columns >= D load as zero through
+// the buffer range check and their stores are dropped.  Wave w of the grid
+// takes the tokens w, w + W, ... (W waves in all), all column blocks of a
+// token in a row.  Gates are wave-uniform scalar loads (lgkmcnt, outside the
+// vector-memory pipeline).  Measured on the MI355X, this path moves mixed
+// read/write traffic ~7% faster than register loads.
+// ---------------------------------------------------------------------------
+constexpr int kPostFwdStages = 4;  // 4 waves x 4 slots x 5 KB: two blocks per CU
+constexpr int kPostBwdStages = 4;  // 4 waves x 4 slots x 9 KB: one block per CU
+
+// Reads the R 1 KB units of a slot (lane's 16 bytes each), complete on return.
+template <int R>
+__device__ __forceinline__ void read_slot(u32x4 (&v)[R], uint32_t base) {
+  static_assert(R % 4 == 1, "R = 4k + 1 rows");
+#pragma unroll
+  for (int i = 0; i + 4 <= R; i += 4) lds_read4<1024>(*reinterpret_cast<u32x4(*)[4]>(&v[i]), base + i * 1024);
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v[R - 1]) : "v"(base + (R - 1) * 1024) : "memory");
+}
+
+template <int N>
+__global__ __launch_bounds__(256) void post_fwd_dma_kernel(const bf16_t* __restrict__ x,
+                                                           const float* __restrict__ h_res,
+                                                           const bf16_t* __restrict__ h_out,
+                                                           const float* __restrict__ h_post,
+                                                           bf16_t* __restrict__ y, int64_t T, int D) {
+  constexpr int R = N + 1, S = kPostFwdStages;  // slot rows: x[0..N-1], h_out
+  constexpr int VM_START = (S - 2) * R, VM_STEADY = (S - 2) * R + (S - 1) * N;
+  static_assert(VM_STEADY < 64, "vmcnt range");
+  __shared__ u32x4 ring[kPostWavesPerBlock * S * R * kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t gw = (int64_t)blockIdx.x * kPostWavesPerBlock + wave, W = (int64_t)gridDim.x * kPostWavesPerBlock;
+  const int ncb = (D + 511) / 512;
+  const int64_t ntok = (T - gw + W - 1) / W;
+  if (ntok <= 0) return;  // this wave only: no barriers below
+  const int64_t J = ntok * ncb;
+  const uint32_t wring = lds_addr(ring) + (uint32_t)(wave * S * R * 1024);
+  const int64_t ND = (int64_t)N * D;
+
+  int64_t itok = gw;
+  int icb = 0;
+  auto issue = [&](int64_t j) {
+    const uint32_t slot = wring + (uint32_t)((j % S) * R * 1024);
+    const int col = icb * 512 + 8 * lane;
+    const auto rx = rows_rsrc(x + itok * ND, ND * 2);
+    const auto rh = rows_rsrc(h_out + itok * D, (int64_t)D * 2);
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(uintptr_t)(slot + n * 1024), 16,
+                                               col < D ? (uint32_t)(((int64_t)n * D + col) * 2) : kBufferOob,
+                                               0, 0, 2 /* nt */);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void_t*)(uintptr_t)(slot + N * 1024), 16,
+                                             col < D ? (uint32_t)(col * 2) : kBufferOob, 0, 0, 2);
+    if (++icb == ncb) {
+      icb = 0;
+      itok += W;
+    }
+  };
+  for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
+
+  int64_t ctok = gw;
+  int ccb = 0;
+  float hr[N * N], hp[N];
+  auto gates = [&]() {
+#pragma unroll
+    for (int i = 0; i < N * N; ++i) hr[i] = h_res[ctok * (N * N) + i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) hp[i] = h_post[ctok * N + i];
+  };
+  gates();
+  for (int64_t j = 0; j < J; ++j) {
+    // this wave's loads of slot j have landed once at most V newer vector
+    // memory operations are outstanding
+    if (j + S - 2 < J) {
+      if (j >= S - 1)
+        wait_vmcnt<VM_STEADY>();
+      else
+        wait_vmcnt<VM_START>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    // the next loads reuse the slot this wave read (and waited for) last iteration
+    if (j + S - 1 < J) issue(j + S - 1);
+    u32x4 v[R];
+    read_slot<R>(v, wring + (uint32_t)((j % S) * R * 1024) + lane * 16);
+    float xv[N][8], hv[8];
+#pragma unroll
+    for (int n = 0; n < N; ++n) Store<bf16_t>::unpack(v[n], xv[n]);
+    Store<bf16_t>::unpack(v[N], hv);
+    const int col = ccb * 512 + 8 * lane;
+    const auto ry = rows_rsrc(y + ctok * ND, ND * 2);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = hp[i] * hv[e];
+#pragma unroll
+        for (int jj = 0; jj < N; ++jj) acc = fmaf(hr[jj * N + i], xv[jj][e], acc);
+        o[e] = acc;
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(Store<bf16_t>::pack(o), ry,
+                                             col < D ? (uint32_t)(((int64_t)i * D + col) * 2) : kBufferOob, 0,
+                                             2 /* nt */);
+    }
+    if (++ccb == ncb) {
+      ccb = 0;
+      ctok += W;
+      if (ctok < T) gates();
+    }
+  }
+}
+
+template <int N>
+__global__ __launch_bounds__(256) void post_bwd_dma_kernel(
+    const bf16_t* __restrict__ gy, const bf16_t* __restrict__ x, const float* __restrict__ h_res,
+    const bf16_t* __restrict__ h_out, const float* __restrict__ h_post, bf16_t* __restrict__ gx,
+    float* __restrict__ g_hres, bf16_t* __restrict__ g_hout, float* __restrict__ g_hpost, int64_t T,
+    int D) {
+  constexpr int R = 2 * N + 1, S = kPostBwdStages;  // slot rows: gy[0..N-1], x[0..N-1], h_out
+  constexpr int VM_START = (S - 2) * R, VM_STEADY = (S - 2) * R + (S - 1) * (N + 1);
+  static_assert(VM_STEADY < 64, "vmcnt range");
+  __shared__ u32x4 ring[kPostWavesPerBlock * S * R * kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t gw = (int64_t)blockIdx.x * kPostWavesPerBlock + wave, W = (int64_t)gridDim.x * kPostWavesPerBlock;
+  const int ncb = (D + 511) / 512;
+  const int64_t ntok = (T - gw + W - 1) / W;
+  if (ntok <= 0) return;  // this wave only: no barriers below
+  const int64_t J = ntok * ncb;
+  const uint32_t wring = lds_addr(ring) + (uint32_t)(wave * S * R * 1024);
+  const int64_t ND = (int64_t)N * D;
+
+  int64_t itok = gw;
+  int icb = 0;
+  auto issue = [&](int64_t j) {
+    const uint32_t slot = wring + (uint32_t)((j % S) * R * 1024);
+    const int col = icb * 512 + 8 * lane;
+    const auto rg = rows_rsrc(gy + itok * ND, ND * 2);
+    const auto rx = rows_rsrc(x + itok * ND, ND * 2);
+    const auto rh = rows_rsrc(h_out + itok * D, (int64_t)D * 2);
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const uint32_t off = col < D ? (uint32_t)(((int64_t)n * D + col) * 2) : kBufferOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(uintptr_t)(slot + n * 1024), 16, off, 0, 0, 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(uintptr_t)(slot + (N + n) * 1024), 16, off, 0, 0,
+                                               2);
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void_t*)(uintptr_t)(slot + 2 * N * 1024), 16,
+                                             col < D ? (uint32_t)(col * 2) : kBufferOob, 0, 0, 2);
+    if (++icb == ncb) {
+      icb = 0;
+      itok += W;
+    }
+  };
+  for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
+
+  int64_t ctok = gw;
+  int ccb = 0;
+  float hr[N * N], hp[N], acc_r[N * N], acc_p[N];
+  auto gates = [&]() {
+#pragma unroll
+    for (int i = 0; i < N * N; ++i) hr[i] = h_res[ctok * (N * N) + i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) hp[i] = h_post[ctok * N + i];
+#pragma unroll
+    for (int i = 0; i < N * N; ++i) acc_r[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc_p[i] = 0.f;
+  };
+  gates();
+  for (int64_t j = 0; j < J; ++j) {
+    if (j + S - 2 < J) {
+      if (j >= S - 1)
+        wait_vmcnt<VM_STEADY>();
+      else
+        wait_vmcnt<VM_START>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    if (j + S - 1 < J) issue(j + S - 1);
+    u32x4 v[R];
+    read_slot<R>(v, wring + (uint32_t)((j % S) * R * 1024) + lane * 16);
+    float gv[N][8], xv[N][8], hv[8];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      Store<bf16_t>::unpack(v[n], gv[n]);
+      Store<bf16_t>::unpack(v[N + n], xv[n]);
+    }
+    Store<bf16_t>::unpack(v[2 * N], hv);
+    const int col = ccb * 512 + 8 * lane;
+    const auto rgx = rows_rsrc(gx + ctok * ND, ND * 2);
+#pragma unroll
+    for (int jj = 0; jj < N; ++jj) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) a = fmaf(hr[jj * N + i], gv[i][e], a);
+        o[e] = a;
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(Store<bf16_t>::pack(o), rgx,
+                                             col < D ? (uint32_t)(((int64_t)jj * D + col) * 2) : kBufferOob, 0,
+                                             2);
+    }
+    {
+      float oh[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) a = fmaf(hp[i], gv[i][e], a);
+        oh[e] = a;
+      }
+      const auto rgh = rows_rsrc(g_hout + ctok * D, (int64_t)D * 2);
+      __builtin_amdgcn_raw_buffer_store_b128(Store<bf16_t>::pack(oh), rgh, col < D ? (uint32_t)(col * 2) : kBufferOob,
+                                             0, 2);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+#pragma unroll
+      for (int jj = 0; jj < N; ++jj)
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc_r[jj * N + i] = fmaf(xv[jj][e], gv[i][e], acc_r[jj * N + i]);
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc_p[i] = fmaf(hv[e], gv[i][e], acc_p[i]);
+    }
+    if (++ccb == ncb) {
+      // token done: reduce the N*N + N dot products across the wave
+#pragma unroll
+      for (int i = 0; i < N * N; ++i) acc_r[i] = wave_sum(acc_r[i]);
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc_p[i] = wave_sum(acc_p[i]);
+      if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < N * N; ++i) g_hres[ctok * (N * N) + i] = acc_r[i];
+#pragma unroll
+        for (int i = 0; i < N; ++i) g_hpost[ctok * N + i] = acc_p[i];
+      }
+      ccb = 0;
+      ctok += W;
+      if (ctok < T) gates();
+    }
+  }
+}
+
+// Persistent grid: as many blocks as fit on the device at once (the LDS rings
+// bound the residency), at most one wave per token.
+template <typename K>
+static int64_t post_dma_grid(K kernel, int64_t T) {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev] && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                    cus[dev] <= 0))
+    cus[dev] = 256;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWave * kPostWavesPerBlock, 0) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  const int64_t grid = (int64_t)cus[dev] * per_cu;
+  const int64_t max_grid = (T + kPostWavesPerBlock - 1) / kPostWavesPerBlock;
+  return grid < max_grid ? grid : max_grid;
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
 template <int N, typename S>
@@ -194,6 +474,14 @@ static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
   const dim3 grid((unsigned)((T + kPostWavesPerBlock - 1) / kPostWavesPerBlock));
   const dim3 block(kWave * kPostWavesPerBlock);
   const bool vec = (D % Store<S>::VEC == 0) && aligned16(x) && aligned16(h_out) && aligned16(y);
+  if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
+    if (vec && D % 8 == 0) {
+      const int64_t g = post_dma_grid(post_fwd_dma_kernel<N>, T);
+      hipLaunchKernelGGL((post_fwd_dma_kernel<N>), dim3((unsigned)g), block, 0, st, (const bf16_t*)x, h_res,
+                         (const bf16_t*)h_out, h_post, (bf16_t*)y, T, D);
+      return check_launch("post_fwd_dma");
+    }
+  }
   if (vec)
     hipLaunchKernelGGL((post_fwd_kernel<N, S, true>), grid, block, 0, st, (const S*)x, h_res,
                        (const S*)h_out, h_post, (S*)y, T, D);
@@ -211,6 +499,15 @@ static int launch_post_bwd(const void* gy, const void* x, const float* h_res, co
   const dim3 block(kWave * kPostWavesPerBlock);
   const bool vec = (D % Store<S>::VEC == 0) && aligned16(gy) && aligned16(x) &&
                    aligned16(h_out) && aligned16(gx) && aligned16(g_hout);
+  if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
+    if (vec && D % 8 == 0) {
+      const int64_t g = post_dma_grid(post_bwd_dma_kernel<N>, T);
+      hipLaunchKernelGGL((post_bwd_dma_kernel<N>), dim3((unsigned)g), block, 0, st, (const bf16_t*)gy,
+                         (const bf16_t*)x, h_res, (const bf16_t*)h_out, h_post, (bf16_t*)gx, g_hres,
+                         (bf16_t*)g_hout, g_hpost, T, D);
+      return check_launch("post_bwd_dma");
+    }
+  }
   if (vec)
     hipLaunchKernelGGL((post_bwd_kernel<N, S, true>), grid, block, 0, st, (const S*)gy,
                        (const S*)x, h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout,
