@@ -152,20 +152,52 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// DPP lane moves inside 16-lane rows (a few cycles, no LDS round trip):
+// quad_perm swaps lanes xor 1 / xor 2, row_ror rotates a row by 4 / 8 lanes
+// (row_ror:8 is lane xor 8).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRor4 = 0x124;
+constexpr int kDppRor8 = 0x128;
+
 // Sum over lanes whose indices differ only in the bits of `mask`
 // (mask is a compile-time set of xor offsets, e.g. 0b0011 -> offsets 1 and 2).
+// Offsets 1, 2, 8 and the pair {4, 8} run on DPP; 4 alone and 16, 32 use
+// cross-lane shuffles.
 template <int MASK>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1)
-    if (MASK & o) v += __shfl_xor(v, o, kWave);
+  if constexpr (MASK & 1) v += dpp_mov<kDppXor1>(v);
+  if constexpr (MASK & 2) v += dpp_mov<kDppXor2>(v);
+  if constexpr ((MASK & 12) == 12) {
+    v += dpp_mov<kDppRor4>(v);  // {l, l-4}
+    v += dpp_mov<kDppRor8>(v);  // {l, l-4, l-8, l-12}: the 4 lanes of l's class mod 4
+  } else if constexpr (MASK & 8) {
+    v += dpp_mov<kDppRor8>(v);
+  } else if constexpr (MASK & 4) {
+    v += __shfl_xor(v, 4, kWave);
+  }
+  if constexpr (MASK & 16) v += __shfl_xor(v, 16, kWave);
+  if constexpr (MASK & 32) v += __shfl_xor(v, 32, kWave);
   return v;
 }
 template <int MASK>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1)
-    if (MASK & o) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  if constexpr (MASK & 1) v = fmaxf(v, dpp_mov<kDppXor1>(v));
+  if constexpr (MASK & 2) v = fmaxf(v, dpp_mov<kDppXor2>(v));
+  if constexpr ((MASK & 12) == 12) {
+    v = fmaxf(v, dpp_mov<kDppRor4>(v));
+    v = fmaxf(v, dpp_mov<kDppRor8>(v));
+  } else if constexpr (MASK & 8) {
+    v = fmaxf(v, dpp_mov<kDppRor8>(v));
+  } else if constexpr (MASK & 4) {
+    v = fmaxf(v, __shfl_xor(v, 4, kWave));
+  }
+  if constexpr (MASK & 16) v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  if constexpr (MASK & 32) v = fmaxf(v, __shfl_xor(v, 32, kWave));
   return v;
 }
 
