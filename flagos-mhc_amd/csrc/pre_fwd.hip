@@ -288,8 +288,8 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_kernel(PreFwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// LDS-pipelined form: N = 4, bf16 x and phi (phi used in place), D % 8 == 0,
-// 16-byte aligned rows.
+// LDS-pipelined form: N = 4 or 8, bf16 x and phi (phi used in place),
+// D % 8 == 0, 16-byte aligned rows.
 //
 // A persistent block per CU walks its 64-token tiles; every tile is two
 // streams of stages through one ring of S stage slots in LDS, filled by
@@ -317,19 +317,30 @@ __device__ __forceinline__ u32x4 pre_sh4(uint32_t a) {
   asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
   return v;
 }
-constexpr int kFwdDmaUnits = 24;  // 1 KB units per stage slot
+// Slot geometry per N: a contraction slot holds 16 units of x and 4*MT of phi
+// (MT 16-row m blocks), a y slot 4 tokens x N streams; 1 KB units.
+template <int N> struct FwdDmaCfg {
+  static constexpr int MT = PreDims<N>::MT;
+  static constexpr int CU = 16 + 4 * MT;              // contraction units
+  static constexpr int YU = 4 * N;                    // y units
+  static constexpr int UNITS = CU > YU ? CU : YU;
+  static constexpr int S = N == 4 ? kFwdDmaStages : 3;  // slots (LDS: S * UNITS KB + mixes)
+};
 
-template <bool XS>
+template <int N, bool XS>
 __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) {
-  constexpr int N = 4, M = PreDims<N>::M, L = N * N, TT = kFwdTile, S = kFwdDmaStages;
+  using C = FwdDmaCfg<N>;
+  constexpr int M = PreDims<N>::M, MT = C::MT, L = N * N, TT = kFwdTile, S = C::S, UNITS = C::UNITS;
   constexpr int CW = 128;                  // K columns per contraction stage
   constexpr int YW = 512;                  // d columns per y stage
-  constexpr int YST = XS ? 9 : 1;          // buffer stores per lane and y stage
-  constexpr int VM_C = (S - 2) * 6;        // window of contraction stages only
-  constexpr int VM_Y = (S - 2) * 4 + (S - 1) * YST;  // window of y stages only
-  constexpr int VM_MIN = (S - 2) * 4;      // any window: fewest loads per stage
-  static_assert(VM_Y < 64 && VM_C < 64, "vmcnt range");
-  __shared__ u32x4 ring[S * kFwdDmaUnits * kWave];
+  constexpr int CI = 4 + MT;               // loads per wave and contraction stage
+  constexpr int YI = N;                    // loads per wave and y stage
+  constexpr int YST = XS ? 1 + 2 * N : 1;  // buffer stores per lane and y stage
+  constexpr int VM_C = (S - 2) * CI;       // window of contraction stages only
+  constexpr int VM_Y = (S - 2) * YI + (S - 1) * YST;  // window of y stages only
+  constexpr int VM_MIN = (S - 2) * (CI < YI ? CI : YI);  // any window: fewest loads per stage
+  static_assert(N % 4 == 0 && VM_Y < 64 && VM_C < 64, "vmcnt range");
+  __shared__ u32x4 ring[S * UNITS * kWave];
   __shared__ float mix_sh[TT][M + 1];
   __shared__ __align__(16) float pre_sh[TT][N];
   __shared__ __align__(16) float inv_sh[TT];
@@ -338,7 +349,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int D = a.D;
-  static_assert(sizeof(pre_sh[0]) == 16, "pre of a token is one 16-byte LDS read");
+  static_assert(sizeof(pre_sh[0]) % 16 == 0, "pre of a token is whole 16-byte LDS reads");
   const int K = N * D;
   const int64_t T = a.T;
   const int nst_c = (K + CW - 1) / CW;
@@ -363,16 +374,16 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   auto issue = [&](int64_t j) {
     const int64_t tb = itile * TT;
     const int nv = (int)(T - tb < TT ? T - tb : TT);
-    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kFwdDmaUnits * 1024);
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * UNITS * 1024);
     const auto rx = rows_rsrc(x + tb * K, (int64_t)nv * K * 2);
     if (is < nst_c) {
       const int k0 = is * CW;
-      // units 0..15: x rows 4u..4u+3 (u = wave + 4i); 16..23: phi rows
-      // 4(u-16)..+3 (u = 16 + wave + 4i); row chunks XOR-swizzled by row & 15
+      // units 0..15: x rows 4u..4u+3 (u = wave + 4i, i < 4); 16..: phi rows
+      // 4(u-16)..+3 (u = 16 + wave + 4(i-4)); chunks XOR-swizzled by row & 15
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
+      for (int i = 0; i < CI; ++i) {
         const int u = wave + 4 * i;
-        const int row = 4 * (wave + 4 * (i & 3)) + q;
+        const int row = 4 * (wave + 4 * (i < 4 ? i : i - 4)) + q;
         const int k = k0 + 8 * (r ^ (row & 15));
         const uint32_t off = k < K ? (uint32_t)(((int64_t)row * K + k) * 2) : kBufferOob;
         lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
@@ -382,16 +393,20 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, off, 0, 0, 0);
       }
     } else {
-      // unit n + 4i: token 4*tg + i, stream n = wave, columns cb*512 + 8*lane
+      // unit n + N*i: token 4*tg + i, stream n (this wave: n = wave, wave + 4, ..),
+      // columns cb*512 + 8*lane
       const int sy = is - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
       const int col = cb * YW + 8 * lane;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + (wave + 4 * i) * 1024);
-        const uint32_t off =
-            col < D ? (uint32_t)((((int64_t)(4 * tg + i) * N + wave) * D + col) * 2) : kBufferOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2);
-      }
+      for (int nn = 0; nn < N; nn += 4)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = nn + wave;
+          lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + (n + N * i) * 1024);
+          const uint32_t off =
+              col < D ? (uint32_t)((((int64_t)(4 * tg + i) * N + n) * D + col) * 2) : kBufferOob;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2);
+        }
     }
     if (++is == per_tile) {
       is = 0;
@@ -401,7 +416,9 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
 
   for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
 
-  floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  floatx4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float ssq = 0.f;
   int64_t ctile = blockIdx.x;
   int cs = 0;  // stage of the current tile being consumed
@@ -422,16 +439,16 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kFwdDmaUnits * 1024);
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * UNITS * 1024);
     const int64_t tb = ctile * TT;
 
     if (cs < nst_c) {
       // ---- contraction stage: row block `wave` x all of phi ----------------
       if (j + S - 1 < J) issue(j + S - 1);
-      // chunk 4g+q of x row 16*wave + r and of phi rows r, 16 + r: the
+      // chunk 4g+q of x row 16*wave + r and of phi rows 16*mt + r: the
       // swizzled positions differ per g, so each read has its own address;
-      // phi row 16 + r sits 16 rows (4 KB) after row r
-      u32x4 A[4], B[2][4];
+      // phi row 16*mt + r sits mt*4 KB after row r
+      u32x4 A[4], B[MT][4];
       const uint32_t ca = slot + (16 * wave + r) * 256, cb0 = slot + 16 * 1024 + r * 256;
       uint32_t sw[4];
 #pragma unroll
@@ -455,6 +472,35 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
           : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
             "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
           : "memory");
+      if constexpr (MT == 5) {  // N = 8: phi rows 32..79
+        asm volatile(
+            "ds_read_b128 %0, %12 offset:8192\n\t"
+            "ds_read_b128 %1, %13 offset:8192\n\t"
+            "ds_read_b128 %2, %14 offset:8192\n\t"
+            "ds_read_b128 %3, %15 offset:8192\n\t"
+            "ds_read_b128 %4, %12 offset:12288\n\t"
+            "ds_read_b128 %5, %13 offset:12288\n\t"
+            "ds_read_b128 %6, %14 offset:12288\n\t"
+            "ds_read_b128 %7, %15 offset:12288\n\t"
+            "ds_read_b128 %8, %12 offset:16384\n\t"
+            "ds_read_b128 %9, %13 offset:16384\n\t"
+            "ds_read_b128 %10, %14 offset:16384\n\t"
+            "ds_read_b128 %11, %15 offset:16384\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(B[2][0]), "=&v"(B[2][1]), "=&v"(B[2][2]), "=&v"(B[2][3]), "=&v"(B[3][0]), "=&v"(B[3][1]),
+              "=&v"(B[3][2]), "=&v"(B[3][3]), "=&v"(B[4][0]), "=&v"(B[4][1]), "=&v"(B[4][2]), "=&v"(B[4][3])
+            : "v"(cb0 + sw[0]), "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
+            : "memory");
+      } else {
+        static_assert(MT == 2, "phi row blocks read above");
+      }
+      // The stage's 128 columns go through a fresh 4-step MFMA chain that is
+      // then added to the running sums with round-to-nearest-even adds: a
+      // single MFMA accumulator chain over all of K (up to ~900 steps) drifts
+      // measurably (2e-5 relative at K = 16384).
+      floatx4 part[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) part[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
 #pragma unroll
@@ -463,8 +509,10 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
           ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
         }
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) acc[mt] = mfma16x16x32(as_bf16x8(A[g]), as_bf16x8(B[mt][g]), acc[mt]);
+        for (int mt = 0; mt < MT; ++mt) part[mt] = mfma16x16x32(as_bf16x8(A[g]), as_bf16x8(B[mt][g]), part[mt]);
       }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
 
       if (cs == nst_c - 1) {
         // ---- tile's mixes, heads and Sinkhorn -----------------------------
@@ -478,11 +526,12 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
           const float inv = __shfl(inv_row, 4 * q + v, kWave);
           const int tt = 16 * wave + 4 * q + v;
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
+          for (int mt = 0; mt < MT; ++mt)
             if (16 * mt + r < M) mix_sh[tt][16 * mt + r] = acc[mt][v] * inv;
         }
         if (q == 0) inv_sh[16 * wave + r] = inv_row;
-        acc[0] = acc[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
         ssq = 0.f;
         __syncthreads();
         if (a.mixes) {
@@ -521,10 +570,13 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
       const int sy = cs - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
       const int t = 4 * tg + wave;  // token within the tile
       if (j + S - 1 < J) issue(j + S - 1);
-      u32x4 X[N], P, I = zero4();
-      lds_read4<1024>(X, slot + ((4 * wave) * kWave + lane) * 16);  // streams n = 0..3 of token t
+      u32x4 X[N], P[N / 4], I = zero4();
+#pragma unroll
+      for (int nn = 0; nn < N; nn += 4)  // streams nn..nn+3 of token t (units n + N*wave)
+        lds_read4<1024>(*reinterpret_cast<u32x4(*)[4]>(&X[nn]), slot + ((nn + N * wave) * kWave + lane) * 16);
       // pre (and inv_rms) of token t: the same address on every lane, a broadcast
-      P = pre_sh4(lds_addr(&pre_sh[t][0]));
+#pragma unroll
+      for (int nn = 0; nn < N; nn += 4) P[nn / 4] = pre_sh4(lds_addr(&pre_sh[t][nn]));
       if constexpr (XS) I = pre_sh4(lds_addr(&inv_sh[t]) & ~15u);
       const int nv = (int)(T - tb < TT ? T - tb : TT);
       const int col = cb * YW + 8 * lane;
@@ -533,7 +585,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
       for (int i = 0; i < 8; ++i) o[i] = 0.f;
 #pragma unroll
       for (int n = 0; n < N; ++n) {
-        const float p = __uint_as_float(P[n]);
+        const float p = __uint_as_float(P[n / 4][n % 4]);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           o[2 * w] = fmaf(p, __uint_as_float(X[n][w] << 16), o[2 * w]);
@@ -574,13 +626,14 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   }
 }
 
-// The LDS-pipelined kernel covers the bf16 fast path of N = 4.  Buffer
-// ranges are 32-bit: a tile of x rows (64 * 4 * D, fp32 x_scaled) must fit.
+// The LDS-pipelined kernel covers the bf16 fast path (N = 4, 8).  Buffer
+// ranges are 32-bit: a tile of x rows (64 * N * D, fp32 x_scaled) must fit.
 static bool fwd_dma_usable(const PreFwdArgs& a, int N, bool bf16x, bool vec) {
-  return N == 4 && bf16x && vec && a.phi_planes == 1 && a.phi_ld == (int64_t)N * a.D &&
+  return (N == 4 || N == 8) && bf16x && vec && a.phi_planes == 1 && a.phi_ld == (int64_t)N * a.D &&
          (int64_t)kFwdTile * N * a.D * 4 < ((int64_t)1 << 31) && aligned16(a.phi);
 }
 
+template <int N>
 static int launch_pre_fwd_dma(const PreFwdArgs& a, hipStream_t st) {
   static int cus[64];
   int dev = 0;
@@ -591,9 +644,9 @@ static int launch_pre_fwd_dma(const PreFwdArgs& a, hipStream_t st) {
   const int64_t ntiles = (a.T + kFwdTile - 1) / kFwdTile;
   const int64_t grid = ntiles < cus[dev] ? ntiles : cus[dev];  // one block per CU (LDS ring)
   if (a.x_scaled)
-    hipLaunchKernelGGL(pre_fwd_dma_kernel<true>, dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, true>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   else
-    hipLaunchKernelGGL(pre_fwd_dma_kernel<false>, dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   return check_launch("pre_fwd_dma");
 }
 
@@ -681,7 +734,8 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   a.T = T;
   a.D = D;
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(y) && (!x_scaled || aligned16(x_scaled));
-  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec)) return launch_pre_fwd_dma(a, st);
+  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec))
+    return N == 4 ? launch_pre_fwd_dma<4>(a, st) : launch_pre_fwd_dma<8>(a, st);
   switch (x_dtype) {
     case MHC_DTYPE_BF16: return dispatch_pre_fwd<bf16_t>(N, a, vec, st);
     case MHC_DTYPE_F16: return dispatch_pre_fwd<f16_t>(N, a, vec, st);

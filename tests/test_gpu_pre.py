@@ -54,6 +54,25 @@ def check_fwd(out, want, dtype, idx=None, what=""):
         assert_close(sel(out[k]), w, 1e-4, 1e-5, what + " " + k)
 
 
+def check_fwd_vs_ref(out, ref, x, phi, alpha, base, kw):
+    """Whole outputs against the fp32 torch *_ref.  That reference carries its
+    own fp32 rounding (a 16K-deep GEMM), so tokens where the two disagree
+    beyond tolerance are settled against the float64 oracle, which both the
+    kernel and the tolerance are defined by."""
+    T = out["y"].shape[0]
+    disputed = np.zeros(T, dtype=bool)
+    g, w = _np(out["y"].reshape(T, -1)), _np(ref["y"].reshape(T, -1))
+    disputed |= (np.abs(g - w) > 2e-2 + 2e-2 * np.abs(w)).reshape(T, -1).any(1)
+    for k in FWD_KEYS:
+        g, w = _np(out[k]), _np(ref[k])
+        disputed |= (np.abs(g - w) > 1e-5 + 1e-4 * np.abs(w)).reshape(T, -1).any(1)
+    idx = np.nonzero(disputed)[0]
+    assert idx.size <= max(4, T // 1000), f"{idx.size} of {T} tokens disagree with the fp32 reference"
+    if idx.size:
+        check_fwd(out, _oracle_fwd(torch.from_numpy(idx).to(DEV), x, phi, alpha, base, kw), None,
+                  torch.from_numpy(idx).to(DEV), "oracle (disputed tokens):")
+
+
 FWD_CASES = [
     # T, N, D, x dtype, phi dtype, recipe, clamp, iters
     (16384, 4, 4096, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),   # config 3
@@ -70,6 +89,7 @@ FWD_CASES = [
     # of d, ragged last tile, several tiles per block
     (100, 4, 520, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (20000, 4, 1288, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (70, 8, 200, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),       # N = 8, partial stages
 ]
 
 
@@ -87,7 +107,7 @@ def test_pre_fwd_parity(T, N, D, dtype, phi_dtype, recipe, clamp, iters):
     assert_close(out["x_scaled"][idx], want["x_scaled"], 1e-5, 1e-6, "x_scaled")
     if T * N * D >= 1 << 24:   # whole output against the package's fp32 *_ref on the GPU
         ref = m.mhc_pre_clamp_sinkhorn_ref(x, phi, alpha, base, **kw)
-        check_fwd(out, ref, dtype, None, "ref:")
+        check_fwd_vs_ref(out, ref, x, phi, alpha, base, kw)
     # need_backward=False returns exactly the three outputs, same values
     small = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=False, **kw)
     assert set(small) == {"y", "post_out", "comb_frag"}
