@@ -90,6 +90,16 @@ FWD_CASES = [
     (100, 4, 520, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (20000, 4, 1288, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (70, 8, 200, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),       # N = 8, partial stages
+    # N=4 bf16 at the model widths D = 1024..8192: ragged last 64-token
+    # tiles, fewer tiles than blocks, clamp off, few Sinkhorn iterations
+    (1000, 4, 7168, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (37, 4, 1024, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (700, 4, 2048, torch.bfloat16, torch.bfloat16, "baseline", 3.0, 20),
+    (333, 4, 3072, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 5),
+    (4133, 4, 5120, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (515, 4, 6144, torch.bfloat16, torch.bfloat16, "baseline", 0.0, 20),
+    (2050, 4, 8192, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (65536, 4, 7168, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),  # config 5 (bench)
 ]
 
 
@@ -113,6 +123,20 @@ def test_pre_fwd_parity(T, N, D, dtype, phi_dtype, recipe, clamp, iters):
     assert set(small) == {"y", "post_out", "comb_frag"}
     for k in small:
         assert torch.equal(small[k], out[k])
+
+
+@pytest.mark.parametrize("T,D", [(4133, 7168), (70, 1024)])
+def test_pre_fwd_deterministic(T, D):
+    """Every reduction runs in a fixed order (no atomics): two runs give
+    identical bits."""
+    print(f"[pre_fwd determinism] T={T} D={D}", flush=True)
+    x, phi, alpha, base, *_ = pre_inputs(T, 4, D)
+    kw = dict(clamp_min=-10.0, clamp_max=10.0)
+    a = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **kw)
+    b = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **kw)
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
 
 
 def test_pre_fwd_bsnd_shape():
