@@ -11,6 +11,9 @@ functions are the pure-PyTorch references of the same semantics.
     mhc_pre_clamp_sinkhorn         (forward, returns dict)
     mhc_pre_clamp_sinkhorn_backward
     mhc_post_fn, mhc_pre_clamp_sinkhorn_fn   (autograd wrappers)
+
+Importing the package also registers the operators as torch.ops.flagos_mhc.*
+(``FlagOS_mhc.library``) for torch.compile and HIP-graph capture.
 """
 
 from .mhc_post import mhc_post, mhc_post_ref
@@ -29,6 +32,7 @@ from .autograd import (
     mhc_post_fn,
     mhc_pre_clamp_sinkhorn_fn,
 )
+from . import library  # registers torch.ops.flagos_mhc.* (torch.compile / HIP graphs)
 
 __all__ = [
     "mhc_post",
