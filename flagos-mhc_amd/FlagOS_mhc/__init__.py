@@ -12,6 +12,9 @@ functions are the pure-PyTorch references of the same semantics.
     mhc_pre_clamp_sinkhorn_backward
     mhc_post_fn, mhc_pre_clamp_sinkhorn_fn   (autograd wrappers)
 
+Beyond the reference: ``mhc_post_pre_clamp_sinkhorn`` (and its autograd
+form) fuses mhc_post of one layer with mhc_pre_clamp_sinkhorn of the next.
+
 Importing the package also registers the operators as torch.ops.flagos_mhc.*
 (``FlagOS_mhc.library``) for torch.compile and HIP-graph capture.
 """
@@ -31,7 +34,10 @@ from .autograd import (
     MhcPreClampSinkhornFn,
     mhc_post_fn,
     mhc_pre_clamp_sinkhorn_fn,
+    MhcPostPreClampSinkhornFn,
+    mhc_post_pre_clamp_sinkhorn_fn,
 )
+from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from . import library  # registers torch.ops.flagos_mhc.* (torch.compile / HIP graphs)
 
 __all__ = [
@@ -47,4 +53,8 @@ __all__ = [
     "MhcPreClampSinkhornFn",
     "mhc_post_fn",
     "mhc_pre_clamp_sinkhorn_fn",
+    # beyond the reference: mhc_post (layer l) fused with mhc_pre_clamp_sinkhorn (layer l+1)
+    "mhc_post_pre_clamp_sinkhorn",
+    "MhcPostPreClampSinkhornFn",
+    "mhc_post_pre_clamp_sinkhorn_fn",
 ]

@@ -7,6 +7,7 @@ import torch
 
 from .mhc_post import mhc_post
 from .mhc_post_backward import mhc_post_backward
+from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from .mhc_pre_clamp_sinkhorn import _pre_forward
 from .mhc_pre_clamp_sinkhorn_backward import mhc_pre_clamp_sinkhorn_backward
 
@@ -75,3 +76,53 @@ def mhc_pre_clamp_sinkhorn_fn(
     """Autograd-aware mhc_pre_clamp_sinkhorn. Returns (y, post_out, comb_frag)."""
     return MhcPreClampSinkhornFn.apply(
         x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+
+
+class MhcPostPreClampSinkhornFn(torch.autograd.Function):
+    """mhc_post (layer l) + mhc_pre_clamp_sinkhorn (layer l+1) with one fused
+    forward.  The backward runs the pre backward on x_next, adds the gradient
+    that reaches x_next directly, and runs the post backward."""
+
+    @staticmethod
+    def forward(ctx, x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
+                clamp_max, iter_times):
+        x_next, out = mhc_post_pre_clamp_sinkhorn(
+            x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
+            iter_times, need_backward=True)
+        ctx.save_for_backward(x, h_res, h_out, h_post, phi, alpha, base, x_next, out["inv_rms"],
+                              out["mixes"], out["pre"])
+        ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+        return x_next, out["y"], out["post_out"], out["comb_frag"]
+
+    @staticmethod
+    def backward(ctx, grad_x_next, grad_y, grad_post_out, grad_comb_frag):
+        x, h_res, h_out, h_post, phi, alpha, base, x_next, inv_rms, mixes, pre = ctx.saved_tensors
+        norm_eps, hc_eps, clamp_min, clamp_max, iter_times = ctx.args
+        if grad_y is None:
+            grad_y = torch.zeros(x_next.shape[:-2] + x_next.shape[-1:], dtype=x.dtype, device=x.device)
+        if grad_post_out is None:
+            grad_post_out = torch.zeros_like(pre)
+        if grad_comb_frag is None:
+            N = pre.shape[-1]
+            grad_comb_frag = torch.zeros((pre.shape[0], N, N), dtype=torch.float32, device=pre.device)
+        gxn, gphi, galpha, gbase = mhc_pre_clamp_sinkhorn_backward(
+            x_next, phi, alpha, base, inv_rms, None, mixes, None, pre,
+            grad_y.contiguous(), grad_post_out.contiguous(), grad_comb_frag.contiguous(),
+            norm_eps=norm_eps, hc_eps=hc_eps, clamp_min=clamp_min, clamp_max=clamp_max,
+            iter_times=iter_times)
+        g = gxn if grad_x_next is None else grad_x_next + gxn
+        gx, ghres, ghout, ghpost = mhc_post_backward(g.contiguous(), x, h_res, h_out, h_post)
+        return gx, ghres, ghout, ghpost, gphi, galpha, gbase, None, None, None, None, None
+
+
+def mhc_post_pre_clamp_sinkhorn_fn(
+    x, h_res, h_out, h_post, phi, alpha, base,
+    norm_eps=1e-6, hc_eps=1e-6,
+    clamp_min=0.0, clamp_max=0.0,
+    iter_times=20,
+):
+    """Autograd-aware fused mhc_post + mhc_pre_clamp_sinkhorn.  Returns
+    (x_next, y, post_out, comb_frag)."""
+    return MhcPostPreClampSinkhornFn.apply(
+        x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
+        iter_times)

@@ -1,0 +1,526 @@
+// Fused forward of mhc_post (layer l) and mhc_pre_clamp_sinkhorn (layer l+1).
+//
+// The post output x_next = h_res^T x + h_post h_out (src/mhc_post.py:344-352)
+// is exactly the next layer's pre input.  Run separately, mhc_post reads x and
+// writes x_next, then the pre kernel reads x_next twice (contraction, then y).
+// Here the contraction stages compute x_next from x and h_out on the fly,
+// write it once and feed the same bf16 values to the MFMA contraction; only
+// the y stages read x_next back.  Per token that saves one full read of the
+// N streams (N*D*2 bytes, a quarter of the pair's traffic).
+//
+// Shape: N = 4, bf16 x / h_out / phi, D a multiple of 64 and >= 3136 (see
+// the read-after-write argument below); the C entry point runs mhc_post then
+// mhc_pre_clamp_sinkhorn for every other shape.
+//
+// A block (8 waves, two per SIMD so that one wave's waits overlap the other's
+// work) owns a tile of 32 tokens.  Wave w handles row block rb = w & 1
+// (tokens 16rb..16rb+15), stream pair sp = (w >> 1) & 1 (streams 2sp, 2sp+1)
+// and column half hh = w >> 2.  Contraction stage s covers columns d in
+// [64s, 64s+64) of all four streams, staged in LDS as 1 KB units filled by
+// direct-to-LDS loads (lane L of a unit holds row L % 16, 16-byte chunk
+// L / 16):
+//   units  0..15  x[t][j][64s + 32h + 8c]      unit 8rb + 2j + h
+//   units 16..19  h_out[t][64s + 32h + 8c]     unit 16 + 2rb + h
+//   units 20..35  phi[16mt + i][n*D + 64s + 32h + 8c]   unit 20 + 4n + 2h + mt
+// Lane (r, c) of a wave reads back exactly the slots it needs (conflict-free
+// 16-byte rows), forms x_next[t][n][d..d+8] for its two streams with the
+// post kernel's fp32 FMA order and round-to-nearest-even (bit-identical to
+// mhc_post), stores it, and uses the packed values as MFMA A operands
+// (v_mfma_f32_16x16x32_bf16; B = phi^T from the same stage).  The four waves
+// of a row block hold partial sums over their (stream pair, column half);
+// they are added in a fixed order through LDS after the tile's last
+// contraction stage, followed by heads and Sinkhorn exactly as in the pre
+// kernel.  y stages then read x_next back (8 tokens x 4 streams x 512
+// columns per stage, a token per wave).
+//
+// Read-after-write of x_next: a lane's stores of stage s were issued after
+// its loads for stage s + S - 1, so they have completed once the wave's wait
+// at stage s + S returns (vector memory operations complete in issue order),
+// and the barrier that follows makes them visible to loads any wave issues
+// from then on.  The y stage (tg, cb) reads columns stored by contraction
+// stages up to s_max = min(8cb + 7, nst_c - 1) (nst_c = D/64) and its loads
+// are issued at stage nst_c + tg*ncb + cb - (S - 1) >= nst_c + cb - S + 1.
+// That is >= s_max + S when cb >= 2S - 2 (s_max <= nst_c - 1) and, for
+// cb <= 2S - 3, when nst_c >= 7cb + 2S + 6 (s_max <= 8cb + 7): both hold for
+// every cb once nst_c >= 16S - 15, i.e. D >= 3136 for S = 4.
+#include "mhc_launch.hpp"
+#include "pre_common.hpp"
+#include "sinkhorn.hpp"
+
+namespace mhc {
+
+namespace {
+
+constexpr int kPPN = 4;
+constexpr int kPPM = 2 * kPPN + kPPN * kPPN;  // 24
+constexpr int kPPMT = 2;                      // 16-row m tiles (rows >= 24 load as zero)
+constexpr int kPPTile = 32;                   // tokens per tile
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = kPPWaves * kWave;
+constexpr int kPPStages = 4;                  // ring slots
+constexpr int kPPCW = 64;                     // d columns per contraction stage
+constexpr int kPPYW = 512;                    // d columns per y stage
+constexpr int kPPYT = 8;                      // tokens per y stage (one per wave)
+constexpr int kPPMinD = kPPCW * (16 * kPPStages - 15);  // 3136: the y loads follow the stores
+constexpr int kUH = 16, kUP = 20;             // first h_out / phi unit of a contraction slot
+constexpr int kPPUnits = 36;                  // 1 KB units per slot (y stages use 32)
+constexpr int kPPCImax = (kPPUnits + kPPWaves - 1) / kPPWaves;  // 5: loads of waves 0..3
+constexpr int kPPCImin = kPPUnits / kPPWaves;                   // 4: loads of waves 4..7
+constexpr int kPPYI = 4;                      // loads per wave and y stage
+constexpr int kPPCST = 2;                     // x_next stores per lane and contraction stage
+constexpr int kPPYST = 1;                     // y stores per lane and y stage
+static_assert(kPPYT * kPPN <= kPPUnits && kPPYT == kPPWaves, "y slot layout");
+
+struct PostPreArgs {
+  const bf16_t* x;       // (T, 4, D)
+  const float* h_res;    // (T, 4, 4)
+  const bf16_t* h_out;   // (T, D)
+  const float* h_post;   // (T, 4)
+  const uint16_t* phi;   // (M, 4D) bf16
+  const float* alpha;
+  const float* base;
+  float norm_eps, hc_eps, cmin, cmax;
+  int apply_clamp;
+  int iters;
+  bf16_t* x_next;        // (T, 4, D)
+  bf16_t* y;             // (T, D)
+  float* post_out;
+  float* comb;
+  float* inv_rms;
+  float* mixes;
+  float* logits;
+  float* pre;
+  int64_t T;
+  int D;
+};
+
+__device__ __forceinline__ u32x4 lds_read1(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+
+__global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a) {
+  constexpr int N = kPPN, M = kPPM, MT = kPPMT, L = N * N, TT = kPPTile, S = kPPStages;
+  // windows of one stage kind get the count of the wave issuing fewest
+  // operations; mixed windows the smallest of both kinds
+  constexpr int VM_C = (S - 2) * kPPCImin + (S - 1) * kPPCST;
+  constexpr int VM_Y = (S - 2) * kPPYI + (S - 1) * kPPYST;
+  constexpr int VM_MIN = (S - 2) * (kPPCImin < kPPYI ? kPPCImin : kPPYI) + (S - 1) * (kPPCST < kPPYST ? kPPCST : kPPYST);
+  static_assert(VM_C < 64 && VM_Y < 64 && VM_MIN <= VM_C && VM_MIN <= VM_Y, "vmcnt range");
+  __shared__ u32x4 ring[S * kPPUnits * kWave];
+  __shared__ u32x4 gates[3 * kWave];  // h_res rows of the 32 tokens (2 units), h_post (1 unit)
+  __shared__ float red_ssq[2][3][16];
+  __shared__ float mix_sh[TT][M + 1];
+  __shared__ __align__(16) float pre_sh[TT][N];
+  __shared__ __align__(16) float inv_sh[TT];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rb = wave & 1, sp = (wave >> 1) & 1, hh = wave >> 2;
+  const int part_k = 2 * hh + sp;  // this wave's partial sum of its row block (0 = the reducer)
+  const int r = lane & 15, q = lane >> 4;
+  const int D = a.D;
+  const int64_t K = (int64_t)N * D;
+  const int64_t T = a.T;
+  const int nst_c = D / kPPCW;
+  const int ncb = (D + kPPYW - 1) / kPPYW;
+  const int per_tile = nst_c + (TT / kPPYT) * ncb;
+  const int64_t ntiles = (T + TT - 1) / TT;
+  const int64_t my_tiles = (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
+  if (my_tiles <= 0) return;  // uniform over the block
+  const int64_t J = my_tiles * per_tile;
+  const auto rphi = rows_rsrc(a.phi, (int64_t)M * K * 2);
+  const uint32_t gates_lds = lds_addr(gates);
+
+  const int e = tid % L;
+  const float a0 = a.alpha[0], a1 = a.alpha[1], a2 = a.alpha[2];
+  const float base_l = a.base[2 * N + e];
+  const float base_h = e < 2 * N ? a.base[e] : 0.f;
+
+  // Per-lane byte offsets of this wave's contraction-stage units (u = wave +
+  // 8i) at d0 = 0 (a stage adds 2*d0), of its x_next stores and of its y
+  // loads; rows >= M of phi are out of range.
+  const int nci = wave < kPPUnits - kPPCImin * kPPWaves ? kPPCImax : kPPCImin;
+  uint32_t cbase[kPPCImax];
+#pragma unroll
+  for (int i = 0; i < kPPCImax; ++i) {
+    const int u = wave + kPPWaves * i;
+    if (u < kUH) {  // x: unit 8rb + 2j + h
+      const int ur = u >> 3, uj = (u >> 1) & 3, uh = u & 1;
+      cbase[i] = (uint32_t)((((int64_t)(16 * ur + r) * N + uj) * D + 32 * uh + 8 * q) * 2);
+    } else if (u < kUP) {  // h_out: unit 16 + 2rb + h
+      const int v = u - kUH, ur = v >> 1, uh = v & 1;
+      cbase[i] = (uint32_t)(((int64_t)(16 * ur + r) * D + 32 * uh + 8 * q) * 2);
+    } else {  // phi: unit 20 + 4n + 2h + mt
+      const int v = u - kUP, un = v >> 2, uh = (v >> 1) & 1, mt = v & 1;
+      cbase[i] = 16 * mt + r < M ? (uint32_t)(((int64_t)(16 * mt + r) * K + (int64_t)un * D + 32 * uh + 8 * q) * 2)
+                                 : kBufferOob;
+    }
+  }
+  uint32_t sbase[2];
+#pragma unroll
+  for (int nl = 0; nl < 2; ++nl)
+    sbase[nl] = (uint32_t)((((int64_t)(16 * rb + r) * N + 2 * sp + nl) * D + 32 * hh + 8 * q) * 2);
+  // y loads: unit 4w + n = token 8tg + w, stream n, columns cb*512 + 8*lane
+  const uint32_t ybase = (uint32_t)(((int64_t)wave * N * D) * 2 + 16 * lane);
+
+  // ---- loads of stage j (issued S - 1 stages ahead) ------------------------
+  int64_t itile = blockIdx.x;
+  int is = 0, itg = 0, icb = 0;  // stage of the next issue; its y token group / column block
+  auto issue = [&](int64_t j) {
+    const int64_t tb = itile * TT;
+    const int nv = (int)(T - tb < TT ? T - tb : TT);
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kPPUnits * 1024);
+    if (is < nst_c) {
+      if (is == 0 && wave == 0) {
+        // the tile's gates: h_res rows (64 bytes a token), h_post (16 bytes)
+        const auto rg = rows_rsrc(a.h_res + tb * L, (int64_t)nv * L * 4);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(uintptr_t)(gates_lds + u * 1024), 16,
+                                                   (uint32_t)((16 * u + (lane >> 2)) * 64 + (lane & 3) * 16), 0,
+                                                   0, 0);
+        const auto rp = rows_rsrc(a.h_post + tb * N, (int64_t)nv * N * 4);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void_t*)(uintptr_t)(gates_lds + 2048), 16,
+                                                 lane < TT ? (uint32_t)(lane * 16) : kBufferOob, 0, 0, 0);
+      }
+      const uint32_t d2 = (uint32_t)(is * kPPCW * 2);
+      const auto rx = rows_rsrc(a.x + tb * K, (int64_t)nv * K * 2);
+      const auto rh = rows_rsrc(a.h_out + tb * D, (int64_t)nv * D * 2);
+#pragma unroll
+      for (int i = 0; i < kPPCImax; ++i) {
+        if (i < nci) {
+          const int u = wave + kPPWaves * i;
+          lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
+          if (u < kUH)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, cbase[i] + d2, 0, 0, 2 /* nt */);
+          else if (u < kUP)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, dst, 16, cbase[i] + d2, 0, 0, 2);
+          else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, cbase[i] + d2, 0, 0, 0);
+        }
+      }
+    } else {
+      // columns >= D read zero
+      const bool colok = icb * kPPYW + 8 * lane < D;
+      const uint32_t yo = ybase + (uint32_t)(((int64_t)kPPYT * itg * N * D + icb * kPPYW) * 2);
+      const auto rxn = rows_rsrc(a.x_next + tb * K, (int64_t)nv * K * 2);
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rxn, (lds_void_t*)(uintptr_t)(slot + (N * wave + n) * 1024), 16,
+                                                 colok ? yo + (uint32_t)(n * D * 2) : kBufferOob, 0, 0, 2);
+      if (++icb == ncb) {
+        icb = 0;
+        ++itg;
+      }
+    }
+    if (++is == per_tile) {
+      is = 0;
+      itg = 0;
+      itile += gridDim.x;
+    }
+  };
+
+  for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
+
+  floatx4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float ssq = 0.f;
+  float hr[N][2], hp[2];  // gates of this lane's token for streams 2sp, 2sp + 1
+#pragma unroll
+  for (int jj = 0; jj < N; ++jj) hr[jj][0] = hr[jj][1] = 0.f;
+  hp[0] = hp[1] = 0.f;
+  int64_t ctile = blockIdx.x;
+  int cs = 0, ctg = 0, ccb = 0;  // stage being consumed; its y token group / column block
+  for (int64_t j = 0; j < J; ++j) {
+    // this wave's loads of stage j have landed once at most V newer vector
+    // memory operations are outstanding
+    if (j + S - 2 < J) {
+      if (cs >= S - 1 && cs + S - 2 < nst_c)
+        wait_vmcnt<VM_C>();
+      else if (cs >= nst_c + S - 1 && cs + S - 2 < per_tile)
+        wait_vmcnt<VM_Y>();
+      else
+        wait_vmcnt<VM_MIN>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kPPUnits * 1024);
+    const int64_t tb = ctile * TT;
+    const int nv = (int)(T - tb < TT ? T - tb : TT);
+
+    if (cs < nst_c) {
+      // ---- contraction stage --------------------------------------------
+      if (j + S - 1 < J) issue(j + S - 1);
+      if (cs == 0) {
+        const int tt = 16 * rb + r;
+        u32x4 G[4];
+        lds_read4<16>(G, gates_lds + (tt >> 4) * 1024 + (tt & 15) * 64);  // h_res[t][j][0..3]
+        const u32x4 P = lds_read1(gates_lds + 2048 + tt * 16);           // h_post[t][0..3]
+#pragma unroll
+        for (int jj = 0; jj < N; ++jj)
+#pragma unroll
+          for (int nl = 0; nl < 2; ++nl) hr[jj][nl] = __uint_as_float(sp ? G[jj][2 + nl] : G[jj][nl]);
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl) hp[nl] = __uint_as_float(sp ? P[2 + nl] : P[nl]);
+      }
+      // x (streams 0..3, columns 64s + 32hh + 8c), h_out and phi^T of streams
+      // 2sp, 2sp + 1 ([nl][mt]): one batch of 9 reads and one wait
+      u32x4 X[4], H, B[2][2];
+      {
+        const uint32_t la = slot + lane * 16;
+        const uint32_t ax = la + (8 * rb + hh) * 1024;
+        const uint32_t ah = la + (kUH + 2 * rb + hh) * 1024;
+        const uint32_t ap = la + (kUP + 8 * sp + 2 * hh) * 1024;
+        asm volatile(
+            "ds_read_b128 %0, %9\n\t"
+            "ds_read_b128 %1, %9 offset:2048\n\t"
+            "ds_read_b128 %2, %9 offset:4096\n\t"
+            "ds_read_b128 %3, %9 offset:6144\n\t"
+            "ds_read_b128 %4, %10\n\t"
+            "ds_read_b128 %5, %11\n\t"
+            "ds_read_b128 %6, %11 offset:1024\n\t"
+            "ds_read_b128 %7, %11 offset:4096\n\t"
+            "ds_read_b128 %8, %11 offset:5120\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(X[0]), "=&v"(X[1]), "=&v"(X[2]), "=&v"(X[3]), "=&v"(H), "=&v"(B[0][0]), "=&v"(B[0][1]),
+              "=&v"(B[1][0]), "=&v"(B[1][1])
+            : "v"(ax), "v"(ah), "v"(ap)
+            : "memory");
+      }
+      // x_next for streams 2sp + nl, columns 64s + 32hh + 8c..+8 (mhc_post's FMA order)
+      u32x4 A[2];
+      {
+        float hv[8], xv[N][8];
+        Store<bf16_t>::unpack(H, hv);
+#pragma unroll
+        for (int jj = 0; jj < N; ++jj) Store<bf16_t>::unpack(X[jj], xv[jj]);
+#pragma unroll
+        for (int nl = 0; nl < 2; ++nl) {
+          float o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float v = hp[nl] * hv[i];
+#pragma unroll
+            for (int jj = 0; jj < N; ++jj) v = fmaf(hr[jj][nl], xv[jj][i], v);
+            o[i] = v;
+          }
+          A[nl] = Store<bf16_t>::pack(o);
+        }
+      }
+      // store x_next (rows >= nv fall outside the range and are dropped)
+      const auto rxn = rows_rsrc(a.x_next + tb * K, (int64_t)nv * K * 2);
+      const uint32_t d2 = (uint32_t)(cs * kPPCW * 2);
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl)
+        __builtin_amdgcn_raw_buffer_store_b128(A[nl], rxn, sbase[nl] + d2, 0, 2 /* nt */);
+      // sum(x_next^2) and the stage's MFMA chain, added to the running sums
+      floatx4 part[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) part[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int nl = 0; nl < 2; ++nl) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = __uint_as_float(A[nl][i] << 16), hi = __uint_as_float(A[nl][i] & 0xffff0000u);
+          ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) part[mt] = mfma16x16x32(as_bf16x8(A[nl]), as_bf16x8(B[nl][mt]), part[mt]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
+
+      if (cs == nst_c - 1) {
+        // ---- tile's mixes (partials added in a fixed order), heads, Sinkhorn
+        // acc: lane (r, c) holds token 16rb + 4c + v, m = 16mt + r; after the
+        // shuffles the lanes of row r hold sum(x_next^2) of token 16rb + r
+        // over this wave's streams and columns.  The slot of this stage is
+        // free once every wave has read it (first barrier) and serves as the
+        // exchange buffer: [rb][part_k - 1][mt][lane].
+        ssq += __shfl_xor(ssq, 16, kWave);
+        ssq += __shfl_xor(ssq, 32, kWave);
+        __syncthreads();
+        floatx4* xch = reinterpret_cast<floatx4*>(ring + (size_t)(j % S) * kPPUnits * kWave);
+        if (part_k != 0) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) xch[((rb * 3 + part_k - 1) * MT + mt) * kWave + lane] = acc[mt];
+          if (q == 0) red_ssq[rb][part_k - 1][r] = ssq;
+        }
+        __syncthreads();
+        if (part_k == 0) {
+          float ssq_t = ssq;
+#pragma unroll
+          for (int k = 0; k < 3; ++k) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] += xch[((rb * 3 + k) * MT + mt) * kWave + lane];
+            ssq_t += red_ssq[rb][k][r];
+          }
+          const float inv_row = 1.0f / sqrtf(ssq_t / (float)K + a.norm_eps);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float inv = __shfl(inv_row, 4 * q + v, kWave);
+            const int tt = 16 * rb + 4 * q + v;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              if (16 * mt + r < M) mix_sh[tt][16 * mt + r] = acc[mt][v] * inv;
+          }
+          if (q == 0) inv_sh[16 * rb + r] = inv_row;
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ssq = 0.f;
+        __syncthreads();
+        if (a.mixes) {
+          for (int idx = tid; idx < TT * M; idx += kPPThreads) {
+            const int tt = idx / M, m = idx - (idx / M) * M;
+            if (tt < nv) a.mixes[(tb + tt) * M + m] = mix_sh[tt][m];
+          }
+        }
+        if (a.inv_rms && tid < nv) a.inv_rms[tb + tid] = inv_sh[tid];
+        static_assert(kPPThreads / L == TT, "one pass of heads and Sinkhorn");
+        {
+          const int tt = tid / L;
+          const int64_t tok = tb + tt;
+          const bool ok = tt < nv;
+          const float logit = mix_sh[tt][2 * N + e] * a2 + base_l;
+          const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
+          const float c = sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
+          if (ok) {
+            a.comb[tok * L + e] = c;
+            if (a.logits) a.logits[tok * L + e] = logit;
+          }
+          if (e < N) {
+            const float p = sigmoidf_(mix_sh[tt][e] * a0 + base_h) + a.hc_eps;
+            pre_sh[tt][e] = p;
+            if (ok && a.pre) a.pre[tok * N + e] = p;
+          } else if (e < 2 * N) {
+            const float po = 2.0f * sigmoidf_(mix_sh[tt][e] * a1 + base_h);
+            if (ok) a.post_out[tok * N + (e - N)] = po;
+          }
+        }
+        __syncthreads();
+      }
+    } else {
+      // ---- y stage: wave w -> token 8tg + w, lane -> 8 columns --------------
+      const int t = kPPYT * ctg + wave, cb = ccb;
+      if (++ccb == ncb) {
+        ccb = 0;
+        ++ctg;
+      }
+      if (j + S - 1 < J) issue(j + S - 1);
+      u32x4 X[N];
+      lds_read4<1024>(X, slot + ((N * wave) * kWave + lane) * 16);
+      const u32x4 P = lds_read1(lds_addr(&pre_sh[t][0]));
+      const int col = cb * kPPYW + 8 * lane;
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const float p = __uint_as_float(P[n]);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          o[2 * w] = fmaf(p, __uint_as_float(X[n][w] << 16), o[2 * w]);
+          o[2 * w + 1] = fmaf(p, __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
+        }
+      }
+      u32x4 ov;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
+      const auto ry = rows_rsrc(a.y + tb * D, (int64_t)nv * D * 2);
+      __builtin_amdgcn_raw_buffer_store_b128(ov, ry, col < D ? (uint32_t)(((int64_t)t * D + col) * 2) : kBufferOob,
+                                             0, 2 /* nt */);
+    }
+    if (++cs == per_tile) {
+      cs = 0;
+      ctg = 0;
+      ctile += gridDim.x;
+    }
+  }
+}
+
+bool post_pre_usable(const void* x, const void* h_out, const void* phi, const void* x_next, const void* y,
+                     int32_t x_dtype, int32_t phi_dtype, int32_t N, int32_t D) {
+  return N == kPPN && x_dtype == MHC_DTYPE_BF16 && phi_dtype == MHC_DTYPE_BF16 && D % kPPCW == 0 &&
+         D >= kPPMinD && (int64_t)kPPTile * N * D * 2 < ((int64_t)1 << 31) &&
+         (int64_t)kPPM * N * D * 2 < ((int64_t)1 << 31) && aligned16(x) && aligned16(h_out) && aligned16(phi) &&
+         aligned16(x_next) && aligned16(y);
+}
+
+int device_cu_count() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev] && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                    cus[dev] <= 0))
+    cus[dev] = 256;
+  return cus[dev];
+}
+
+}  // namespace
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" size_t mhc_post_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype) {
+  return mhc_pre_fwd_workspace_size(T, N, D, phi_dtype);
+}
+
+extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                                int32_t x_dtype, const void* phi, int32_t phi_dtype, const float* alpha,
+                                const float* base, float norm_eps, float hc_eps, float clamp_min, float clamp_max,
+                                int32_t iter_times, void* x_next, void* y, float* post_out, float* comb_frag,
+                                float* inv_rms, float* mixes, float* h_res_logits, float* pre, void* workspace,
+                                size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream) {
+  clear_error();
+  if (T < 0 || D <= 0 || N <= 0)
+    return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
+  if (N != 4 && N != 8)
+    return set_error(MHC_ERR_UNSUPPORTED, "mhc_post_pre_fwd: N=%d not supported (4, 8)", N);
+  if (T == 0) return MHC_OK;
+  if (!x || !h_res || !h_out || !h_post || !phi || !alpha || !base || !x_next || !y || !post_out || !comb_frag)
+    return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: null pointer");
+  if (!post_pre_usable(x, h_out, phi, x_next, y, x_dtype, phi_dtype, N, D)) {
+    // every other shape: the two operators one after the other
+    int rc = mhc_post_fwd(x, h_res, h_out, h_post, x_next, T, N, D, x_dtype, stream);
+    if (rc) return rc;
+    return mhc_pre_fwd(x_next, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
+                       iter_times, y, post_out, comb_frag, inv_rms, mixes, h_res_logits, pre, nullptr, workspace,
+                       workspace_bytes, T, N, D, stream);
+  }
+  PostPreArgs a{};
+  a.x = static_cast<const bf16_t*>(x);
+  a.h_res = h_res;
+  a.h_out = static_cast<const bf16_t*>(h_out);
+  a.h_post = h_post;
+  a.phi = static_cast<const uint16_t*>(phi);
+  a.alpha = alpha;
+  a.base = base;
+  a.norm_eps = norm_eps;
+  a.hc_eps = hc_eps;
+  a.cmin = clamp_min;
+  a.cmax = clamp_max;
+  a.apply_clamp = (clamp_min != 0.0f || clamp_max != 0.0f) ? 1 : 0;
+  a.iters = iter_times;
+  a.x_next = static_cast<bf16_t*>(x_next);
+  a.y = static_cast<bf16_t*>(y);
+  a.post_out = post_out;
+  a.comb = comb_frag;
+  a.inv_rms = inv_rms;
+  a.mixes = mixes;
+  a.logits = h_res_logits;
+  a.pre = pre;
+  a.T = T;
+  a.D = D;
+  const int64_t ntiles = (T + kPPTile - 1) / kPPTile;
+  const int64_t cus = device_cu_count();
+  const int64_t grid = ntiles < cus ? ntiles : cus;  // one block per CU (LDS ring)
+  hipLaunchKernelGGL(post_pre_fwd_kernel, dim3((unsigned)grid), dim3(kPPThreads), 0, (hipStream_t)stream, a);
+  return check_launch("post_pre_fwd");
+}

@@ -113,6 +113,30 @@ int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dty
                 float* grad_base, void* workspace, size_t workspace_bytes, int64_t T, int32_t N,
                 int32_t D, void* stream);
 
+/*
+ * Fused forward of mhc_post (layer l) and mhc_pre_clamp_sinkhorn (layer l+1).
+ * No single counterpart in the reference: it replaces the device work of
+ * mhc_post (src/mhc_post.py:296-352) followed by mhc_pre_clamp_sinkhorn on its
+ * output (src/mhc_pre_clamp_sinkhorn.py:857-971), the pair the reference's
+ * model code runs between two sublayers.
+ * x: (T,N,D), h_out: (T,D) `x_dtype`; h_res (T,N,N), h_post (T,N) fp32;
+ * phi, alpha, base, eps / clamp / iter_times as in mhc_pre_fwd.
+ * Outputs: x_next = mhc_post(x, h_res, h_out, h_post) (T,N,D) `x_dtype`,
+ * bit-identical to mhc_post_fwd; y, post_out, comb_frag and the optional
+ * inv_rms, mixes, h_res_logits, pre of mhc_pre_fwd applied to x_next (no
+ * x_scaled).  N = 4 with bf16 x, h_out and phi, D % 64 == 0, D >= 3136 and
+ * 16-byte aligned rows runs one kernel that reads x once and writes x_next
+ * once; every other shape runs mhc_post_fwd then mhc_pre_fwd.
+ */
+size_t mhc_post_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype);
+int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                     int32_t x_dtype, const void* phi, int32_t phi_dtype, const float* alpha,
+                     const float* base, float norm_eps, float hc_eps, float clamp_min,
+                     float clamp_max, int32_t iter_times, void* x_next, void* y, float* post_out,
+                     float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
+                     float* pre, void* workspace, size_t workspace_bytes, int64_t T, int32_t N,
+                     int32_t D, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

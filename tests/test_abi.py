@@ -97,12 +97,17 @@ def test_ops_refuse_cpu_tensors():
 
 
 def test_public_api_names():
+    """The reference's twelve names (src/__init__.py:34-47) come first and
+    unchanged; the fused post+pre operator is the only addition."""
     import FlagOS_mhc as m
-    assert m.__all__ == [
+    assert m.__all__[:12] == [
         "mhc_post", "mhc_post_ref", "mhc_post_backward", "mhc_post_backward_ref",
         "mhc_pre_clamp_sinkhorn", "mhc_pre_clamp_sinkhorn_ref",
         "mhc_pre_clamp_sinkhorn_backward", "mhc_pre_clamp_sinkhorn_backward_ref",
         "MhcPostFn", "MhcPreClampSinkhornFn", "mhc_post_fn", "mhc_pre_clamp_sinkhorn_fn",
+    ]
+    assert m.__all__[12:] == [
+        "mhc_post_pre_clamp_sinkhorn", "MhcPostPreClampSinkhornFn", "mhc_post_pre_clamp_sinkhorn_fn",
     ]
     for name in m.__all__:
         assert callable(getattr(m, name))
