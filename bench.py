@@ -98,11 +98,14 @@ def measured_traffic(op):
 
 
 def pmc_probe(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
-    """One chain step plus a plain 1 GiB device copy, for rocprofv3 --pmc runs:
-    the copy's FETCH_SIZE / WRITE_SIZE give the counters' scale."""
+    """One chain step, one fused post + pre forward and a plain 1 GiB device
+    copy, for rocprofv3 --pmc runs: the copy's FETCH_SIZE / WRITE_SIZE give
+    the counters' scale."""
     import torch
 
-    run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)
+    o = run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward)[0]
+    m.mhc_post_pre_clamp_sinkhorn(x, o["comb_frag"], h_out, o["post_out"], phi, alpha, base,
+                                  need_backward=True, **kw)
     src = torch.ones(1 << 29, dtype=torch.bfloat16, device=x.device)   # 1 GiB
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
