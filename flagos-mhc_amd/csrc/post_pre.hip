@@ -14,24 +14,28 @@
 //
 // A block (8 waves, two per SIMD so that one wave's waits overlap the other's
 // work) owns a tile of 32 tokens.  Wave w handles row block rb = w & 1
-// (tokens 16rb..16rb+15), stream pair sp = (w >> 1) & 1 (streams 2sp, 2sp+1)
-// and column half hh = w >> 2.  Contraction stage s covers columns d in
-// [64s, 64s+64) of all four streams, staged in LDS as 1 KB units filled by
-// direct-to-LDS loads (lane L of a unit holds row L % 16, 16-byte chunk
-// L / 16):
-//   units  0..15  x[t][j][64s + 32h + 8c]      unit 8rb + 2j + h
-//   units 16..19  h_out[t][64s + 32h + 8c]     unit 16 + 2rb + h
+// (tokens 16rb..16rb+15) and output stream n = w >> 1.  Contraction stage s
+// covers columns d in [64s, 64s+64) of all four streams, staged in LDS as
+// 1 KB units filled by direct-to-LDS loads:
+//   units  0..15  x[t][j][64s..64s+64]   unit 8rb + 2j + g, rows 16rb + 8g + i
+//   units 16..19  h_out[t][64s..64s+64]  unit 16 + 2rb + g
 //   units 20..35  phi[16mt + i][n*D + 64s + 32h + 8c]   unit 20 + 4n + 2h + mt
-// Lane (r, c) of a wave reads back exactly the slots it needs (conflict-free
-// 16-byte rows), forms x_next[t][n][d..d+8] for its two streams with the
-// post kernel's fp32 FMA order and round-to-nearest-even (bit-identical to
-// mhc_post), stores it, and uses the packed values as MFMA A operands
-// (v_mfma_f32_16x16x32_bf16; B = phi^T from the same stage).  The four waves
-// of a row block hold partial sums over their (stream pair, column half);
-// they are added in a fixed order through LDS after the tile's last
-// contraction stage, followed by heads and Sinkhorn exactly as in the pre
-// kernel.  y stages then read x_next back (8 tokens x 4 streams x 512
-// columns per stage, a token per wave).
+// An x / h_out unit holds 8 rows x 128 bytes, so each load instruction reads
+// whole 128-byte row segments; slot p of a unit holds chunk
+// (p & 7) ^ f(i, g) of row i = p >> 3, f(i, g) = (i >> 1) ^ 4g, which makes
+// the 16 lanes of a read phase (16 rows, one chunk each) hit 16 different
+// 16-byte bank groups.  A phi unit holds 16 rows (m) x 64 bytes, lane L = row
+// L % 16, chunk L / 16, the MFMA B-operand layout.  Lane (r, c) of a wave
+// forms x_next[t][n][64s + 32h + 8c..+8] (h = 0, 1) with the post kernel's
+// fp32 FMA order and round-to-nearest-even (bit-identical to mhc_post) and
+// uses the packed values as MFMA A operands (v_mfma_f32_16x16x32_bf16; B =
+// phi^T of stream n).  The two halves are stored by two instructions that
+// each write 8 whole 128-byte row segments: lanes r and r ^ 8 trade their
+// second halves through a DPP row rotation first.  The four waves of a row
+// block hold partial sums over their streams; they are added in a fixed order
+// through LDS after the tile's last contraction stage, followed by heads and
+// Sinkhorn exactly as in the pre kernel.  y stages then read x_next back (8
+// tokens x 4 streams x 512 columns per stage, a token per wave).
 //
 // Read-after-write of x_next: a lane's stores of stage s were issued after
 // its loads for stage s + S - 1, so they have completed once the wave's wait
@@ -117,8 +121,8 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rb = wave & 1, sp = (wave >> 1) & 1, hh = wave >> 2;
-  const int part_k = 2 * hh + sp;  // this wave's partial sum of its row block (0 = the reducer)
+  const int rb = wave & 1, n = wave >> 1;
+  const int part_k = n;  // this wave's partial sum of its row block (0 = the reducer)
   const int r = lane & 15, q = lane >> 4;
   const int D = a.D;
   const int64_t K = (int64_t)N * D;
@@ -142,26 +146,41 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
   // 8i) at d0 = 0 (a stage adds 2*d0), of its x_next stores and of its y
   // loads; rows >= M of phi are out of range.
   const int nci = wave < kPPUnits - kPPCImin * kPPWaves ? kPPCImax : kPPCImin;
+  // DMA lane L of an x / h_out unit: row i = L >> 3 of its half, chunk
+  // (L & 7) ^ f(i, g)
+  const int di = lane >> 3;
   uint32_t cbase[kPPCImax];
 #pragma unroll
   for (int i = 0; i < kPPCImax; ++i) {
     const int u = wave + kPPWaves * i;
-    if (u < kUH) {  // x: unit 8rb + 2j + h
-      const int ur = u >> 3, uj = (u >> 1) & 3, uh = u & 1;
-      cbase[i] = (uint32_t)((((int64_t)(16 * ur + r) * N + uj) * D + 32 * uh + 8 * q) * 2);
-    } else if (u < kUP) {  // h_out: unit 16 + 2rb + h
-      const int v = u - kUH, ur = v >> 1, uh = v & 1;
-      cbase[i] = (uint32_t)(((int64_t)(16 * ur + r) * D + 32 * uh + 8 * q) * 2);
+    if (u < kUH) {  // x: unit 8rb + 2j + g
+      const int ur = u >> 3, uj = (u >> 1) & 3, ug = u & 1;
+      const int c = (lane & 7) ^ ((di >> 1) ^ (ug << 2));
+      cbase[i] = (uint32_t)((((int64_t)(16 * ur + 8 * ug + di) * N + uj) * D + 8 * c) * 2);
+    } else if (u < kUP) {  // h_out: unit 16 + 2rb + g
+      const int v = u - kUH, ur = v >> 1, ug = v & 1;
+      const int c = (lane & 7) ^ ((di >> 1) ^ (ug << 2));
+      cbase[i] = (uint32_t)(((int64_t)(16 * ur + 8 * ug + di) * D + 8 * c) * 2);
     } else {  // phi: unit 20 + 4n + 2h + mt
       const int v = u - kUP, un = v >> 2, uh = (v >> 1) & 1, mt = v & 1;
       cbase[i] = 16 * mt + r < M ? (uint32_t)(((int64_t)(16 * mt + r) * K + (int64_t)un * D + 32 * uh + 8 * q) * 2)
                                  : kBufferOob;
     }
   }
-  uint32_t sbase[2];
+  // x_next stores: instruction 0 writes rows 16rb + (r & 7), instruction 1
+  // rows 16rb + 8 + (r & 7); lanes r < 8 write the first 64 bytes of a row
+  // segment in instruction 0 and the last 64 in instruction 1, lanes r >= 8
+  // the other way round
+  const int hi = r >> 3;
+  const uint32_t sbase0 = (uint32_t)((((int64_t)(16 * rb + (r & 7)) * N + n) * D + 32 * hi + 8 * q) * 2);
+  const uint32_t sbase1 = (uint32_t)((((int64_t)(16 * rb + 8 + (r & 7)) * N + n) * D + 32 * (1 - hi) + 8 * q) * 2);
+  // read slots of this lane's x / h_out chunks c = 4h + q of row r
+  uint32_t rpos[2];
 #pragma unroll
-  for (int nl = 0; nl < 2; ++nl)
-    sbase[nl] = (uint32_t)((((int64_t)(16 * rb + r) * N + 2 * sp + nl) * D + 32 * hh + 8 * q) * 2);
+  for (int h = 0; h < 2; ++h) {
+    const int c = 4 * h + q, ri = r & 7;
+    rpos[h] = (uint32_t)(hi * 1024 + (ri * 8 + (c ^ ((ri >> 1) ^ (hi << 2)))) * 16);
+  }
   // y loads: unit 4w + n = token 8tg + w, stream n, columns cb*512 + 8*lane
   const uint32_t ybase = (uint32_t)(((int64_t)wave * N * D) * 2 + 16 * lane);
 
@@ -228,10 +247,9 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float ssq = 0.f;
-  float hr[N][2], hp[2];  // gates of this lane's token for streams 2sp, 2sp + 1
+  float hr[N], hp = 0.f;  // gates of this lane's token for stream n
 #pragma unroll
-  for (int jj = 0; jj < N; ++jj) hr[jj][0] = hr[jj][1] = 0.f;
-  hp[0] = hp[1] = 0.f;
+  for (int jj = 0; jj < N; ++jj) hr[jj] = 0.f;
   int64_t ctile = blockIdx.x;
   int cs = 0, ctg = 0, ccb = 0;  // stage being consumed; its y token group / column block
   for (int64_t j = 0; j < J; ++j) {
@@ -258,80 +276,98 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
       // ---- contraction stage --------------------------------------------
       if (j + S - 1 < J) issue(j + S - 1);
       if (cs == 0) {
+        // h_res[t][jj][n] (row jj of the token's 64-byte h_res) and h_post[t][n]
         const int tt = 16 * rb + r;
-        u32x4 G[4];
-        lds_read4<16>(G, gates_lds + (tt >> 4) * 1024 + (tt & 15) * 64);  // h_res[t][j][0..3]
-        const u32x4 P = lds_read1(gates_lds + 2048 + tt * 16);           // h_post[t][0..3]
-#pragma unroll
-        for (int jj = 0; jj < N; ++jj)
-#pragma unroll
-          for (int nl = 0; nl < 2; ++nl) hr[jj][nl] = __uint_as_float(sp ? G[jj][2 + nl] : G[jj][nl]);
-#pragma unroll
-        for (int nl = 0; nl < 2; ++nl) hp[nl] = __uint_as_float(sp ? P[2 + nl] : P[nl]);
-      }
-      // x (streams 0..3, columns 64s + 32hh + 8c), h_out and phi^T of streams
-      // 2sp, 2sp + 1 ([nl][mt]): one batch of 9 reads and one wait
-      u32x4 X[4], H, B[2][2];
-      {
-        const uint32_t la = slot + lane * 16;
-        const uint32_t ax = la + (8 * rb + hh) * 1024;
-        const uint32_t ah = la + (kUH + 2 * rb + hh) * 1024;
-        const uint32_t ap = la + (kUP + 8 * sp + 2 * hh) * 1024;
+        const uint32_t ga = gates_lds + (tt >> 4) * 1024 + (tt & 15) * 64 + n * 4;
         asm volatile(
-            "ds_read_b128 %0, %9\n\t"
-            "ds_read_b128 %1, %9 offset:2048\n\t"
-            "ds_read_b128 %2, %9 offset:4096\n\t"
-            "ds_read_b128 %3, %9 offset:6144\n\t"
-            "ds_read_b128 %4, %10\n\t"
-            "ds_read_b128 %5, %11\n\t"
-            "ds_read_b128 %6, %11 offset:1024\n\t"
-            "ds_read_b128 %7, %11 offset:4096\n\t"
-            "ds_read_b128 %8, %11 offset:5120\n\t"
+            "ds_read_b32 %0, %5\n\t"
+            "ds_read_b32 %1, %5 offset:16\n\t"
+            "ds_read_b32 %2, %5 offset:32\n\t"
+            "ds_read_b32 %3, %5 offset:48\n\t"
+            "ds_read_b32 %4, %6\n\t"
             "s_waitcnt lgkmcnt(0)"
-            : "=&v"(X[0]), "=&v"(X[1]), "=&v"(X[2]), "=&v"(X[3]), "=&v"(H), "=&v"(B[0][0]), "=&v"(B[0][1]),
-              "=&v"(B[1][0]), "=&v"(B[1][1])
-            : "v"(ax), "v"(ah), "v"(ap)
+            : "=&v"(hr[0]), "=&v"(hr[1]), "=&v"(hr[2]), "=&v"(hr[3]), "=&v"(hp)
+            : "v"(ga), "v"(gates_lds + 2048 + tt * 16 + n * 4)
             : "memory");
       }
-      // x_next for streams 2sp + nl, columns 64s + 32hh + 8c..+8 (mhc_post's FMA order)
-      u32x4 A[2];
+      // x (streams 0..3) and h_out at columns 64s + 32h + 8c (h = 0, 1) and
+      // phi^T of stream n ([h][mt]): one batch of 14 reads and one wait
+      u32x4 X0[4], X1[4], H[2], B[4];
       {
-        float hv[8], xv[N][8];
-        Store<bf16_t>::unpack(H, hv);
-#pragma unroll
-        for (int jj = 0; jj < N; ++jj) Store<bf16_t>::unpack(X[jj], xv[jj]);
-#pragma unroll
-        for (int nl = 0; nl < 2; ++nl) {
-          float o[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            float v = hp[nl] * hv[i];
-#pragma unroll
-            for (int jj = 0; jj < N; ++jj) v = fmaf(hr[jj][nl], xv[jj][i], v);
-            o[i] = v;
-          }
-          A[nl] = Store<bf16_t>::pack(o);
-        }
+        const uint32_t ax = slot + (8 * rb) * 1024;
+        const uint32_t ah = slot + (kUH + 2 * rb) * 1024;
+        const uint32_t ap = slot + (kUP + 4 * n) * 1024 + lane * 16;
+        asm volatile(
+            "ds_read_b128 %0, %14\n\t"
+            "ds_read_b128 %1, %14 offset:2048\n\t"
+            "ds_read_b128 %2, %14 offset:4096\n\t"
+            "ds_read_b128 %3, %14 offset:6144\n\t"
+            "ds_read_b128 %4, %15\n\t"
+            "ds_read_b128 %5, %15 offset:2048\n\t"
+            "ds_read_b128 %6, %15 offset:4096\n\t"
+            "ds_read_b128 %7, %15 offset:6144\n\t"
+            "ds_read_b128 %8, %16\n\t"
+            "ds_read_b128 %9, %17\n\t"
+            "ds_read_b128 %10, %18\n\t"
+            "ds_read_b128 %11, %18 offset:1024\n\t"
+            "ds_read_b128 %12, %18 offset:2048\n\t"
+            "ds_read_b128 %13, %18 offset:3072\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(X0[0]), "=&v"(X0[1]), "=&v"(X0[2]), "=&v"(X0[3]), "=&v"(X1[0]), "=&v"(X1[1]),
+              "=&v"(X1[2]), "=&v"(X1[3]), "=&v"(H[0]), "=&v"(H[1]), "=&v"(B[0]), "=&v"(B[1]), "=&v"(B[2]),
+              "=&v"(B[3])
+            : "v"(ax + rpos[0]), "v"(ax + rpos[1]), "v"(ah + rpos[0]), "v"(ah + rpos[1]), "v"(ap)
+            : "memory");
       }
-      // store x_next (rows >= nv fall outside the range and are dropped)
-      const auto rxn = rows_rsrc(a.x_next + tb * K, (int64_t)nv * K * 2);
-      const uint32_t d2 = (uint32_t)(cs * kPPCW * 2);
+      // x_next for stream n, columns 64s + 32h + 8c..+8 (mhc_post's FMA order)
+      u32x4 A[2];
 #pragma unroll
-      for (int nl = 0; nl < 2; ++nl)
-        __builtin_amdgcn_raw_buffer_store_b128(A[nl], rxn, sbase[nl] + d2, 0, 2 /* nt */);
+      for (int h = 0; h < 2; ++h) {
+        float hv[8], xv[N][8];
+        Store<bf16_t>::unpack(H[h], hv);
+#pragma unroll
+        for (int jj = 0; jj < N; ++jj) Store<bf16_t>::unpack(h ? X1[jj] : X0[jj], xv[jj]);
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float v = hp * hv[i];
+#pragma unroll
+          for (int jj = 0; jj < N; ++jj) v = fmaf(hr[jj], xv[jj][i], v);
+          o[i] = v;
+        }
+        A[h] = Store<bf16_t>::pack(o);
+      }
+      // store x_next as whole 128-byte row segments: lane r takes the second
+      // half of lane r ^ 8 (DPP row rotation by 8); rows >= nv fall outside
+      // the range and are dropped
+      {
+        u32x4 S1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S1[i] = (uint32_t)__builtin_amdgcn_mov_dpp((int)A[1][i], kDppRor8, 0xF, 0xF, false);
+        const auto rxn = rows_rsrc(a.x_next + tb * K, (int64_t)nv * K * 2);
+        const uint32_t d2 = (uint32_t)(cs * kPPCW * 2);
+        u32x4 W0, W1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          W0[i] = hi ? S1[i] : A[0][i];
+          W1[i] = hi ? A[0][i] : S1[i];
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(W0, rxn, sbase0 + d2, 0, 2 /* nt */);
+        __builtin_amdgcn_raw_buffer_store_b128(W1, rxn, sbase1 + d2, 0, 2 /* nt */);
+      }
       // sum(x_next^2) and the stage's MFMA chain, added to the running sums
       floatx4 part[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) part[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int nl = 0; nl < 2; ++nl) {
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float lo = __uint_as_float(A[nl][i] << 16), hi = __uint_as_float(A[nl][i] & 0xffff0000u);
-          ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
+          const float lo = __uint_as_float(A[h][i] << 16), hi2 = __uint_as_float(A[h][i] & 0xffff0000u);
+          ssq = fmaf(lo, lo, fmaf(hi2, hi2, ssq));
         }
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) part[mt] = mfma16x16x32(as_bf16x8(A[nl]), as_bf16x8(B[nl][mt]), part[mt]);
+        for (int mt = 0; mt < MT; ++mt) part[mt] = mfma16x16x32(as_bf16x8(A[h]), as_bf16x8(B[2 * h + mt]), part[mt]);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
