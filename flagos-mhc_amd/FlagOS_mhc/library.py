@@ -1,4 +1,4 @@
-"""torch.library registration of the four mHC operators (namespace ``flagos_mhc``).
+"""torch.library registration of the mHC operators (namespace ``flagos_mhc``).
 
 Registered ops (opaque to torch.compile, with shape functions for fake/meta
 tensors and autograd formulas, so a compiled graph keeps them whole and
@@ -14,12 +14,16 @@ HIP-graph capture records their kernels on the current stream):
         inv_rms, mixes, pre, grad_y, grad_post_out, grad_comb_frag, norm_eps,
         hc_eps, clamp_min, clamp_max, iter_times)
         -> (grad_x, grad_phi, grad_alpha, grad_base)
+    torch.ops.flagos_mhc.mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post,
+        phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+        -> (x_next, y, post_out, comb_frag, inv_rms, mixes, pre)
 
 The forward pre op also returns the fp32 inv_rms, mixes and pre its backward
-needs; they are marked non-differentiable.  ``mhc_post_op`` and
-``mhc_pre_clamp_sinkhorn_op`` are the autograd-aware entry points with the
-return conventions of ``mhc_post_fn`` / ``mhc_pre_clamp_sinkhorn_fn``
-(src/autograd.py:14-87).  The kernels allocate nothing outside torch's
+needs; they are marked non-differentiable (likewise for the fused op).
+``mhc_post_op``, ``mhc_pre_clamp_sinkhorn_op`` and
+``mhc_post_pre_clamp_sinkhorn_op`` are the autograd-aware entry points with
+the return conventions of ``mhc_post_fn`` / ``mhc_pre_clamp_sinkhorn_fn``
+(src/autograd.py:14-87) and ``mhc_post_pre_clamp_sinkhorn_fn``.  The kernels allocate nothing outside torch's
 allocator and call no host synchronisation, so they can be captured in a
 HIP graph (``torch.cuda.graph``) after one eager warm-up call.
 """
@@ -34,6 +38,7 @@ from torch import Tensor
 
 from .mhc_post import mhc_post
 from .mhc_post_backward import mhc_post_backward
+from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from .mhc_pre_clamp_sinkhorn import _pre_forward
 from .mhc_pre_clamp_sinkhorn_backward import mhc_pre_clamp_sinkhorn_backward
 
@@ -145,6 +150,49 @@ def _pre_grad(ctx, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes, _g_p
 _pre.register_autograd(_pre_grad, setup_context=_pre_setup)
 
 
+# ---- mhc_post (layer l) fused with mhc_pre_clamp_sinkhorn (layer l+1) --------
+
+@torch.library.custom_op(f"{NAMESPACE}::mhc_post_pre_clamp_sinkhorn", mutates_args=())
+def _post_pre(x: Tensor, h_res: Tensor, h_out: Tensor, h_post: Tensor, phi: Tensor, alpha: Tensor,
+              base: Tensor, norm_eps: float, hc_eps: float, clamp_min: float, clamp_max: float,
+              iter_times: int) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    x_next, out = mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post, phi, alpha, base, norm_eps,
+                                              hc_eps, clamp_min, clamp_max, iter_times,
+                                              need_backward=True)
+    return (x_next, out["y"], out["post_out"], out["comb_frag"], out["inv_rms"], out["mixes"],
+            out["pre"])
+
+
+@_post_pre.register_fake
+def _post_pre_fake(x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
+                   clamp_max, iter_times):
+    return (torch.empty_like(x, memory_format=torch.contiguous_format),) + tuple(
+        _pre_fake(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times))
+
+
+def _post_pre_setup(ctx, inputs, output):
+    x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times = inputs
+    x_next, _, _, _, inv_rms, mixes, pre = output
+    ctx.mark_non_differentiable(inv_rms, mixes, pre)
+    ctx.save_for_backward(x, h_res, h_out, h_post, phi, alpha, base, x_next, inv_rms, mixes, pre)
+    ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+
+
+def _post_pre_grad(ctx, grad_x_next, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes,
+                   _g_pre):
+    x, h_res, h_out, h_post, phi, alpha, base, x_next, inv_rms, mixes, pre = ctx.saved_tensors
+    gxn, gphi, galpha, gbase = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward(
+        x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
+        grad_post_out.contiguous(), grad_comb_frag.contiguous(), *ctx.args)
+    gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward(
+        (grad_x_next + gxn).contiguous(), x, h_res, h_out, h_post)
+    return (gx, ghres, ghout, ghpost, gphi.to(phi.dtype), galpha.reshape(alpha.shape).to(alpha.dtype),
+            gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None)
+
+
+_post_pre.register_autograd(_post_pre_grad, setup_context=_post_pre_setup)
+
+
 # ---- autograd-aware entry points ---------------------------------------------
 
 def mhc_post_op(x, h_res, h_out, h_post):
@@ -160,3 +208,13 @@ def mhc_pre_clamp_sinkhorn_op(x, phi, alpha, base, norm_eps=1e-6, hc_eps=1e-6, c
         x, phi, alpha, base, float(norm_eps), float(hc_eps), float(clamp_min), float(clamp_max),
         int(iter_times))
     return y, post_out, comb
+
+
+def mhc_post_pre_clamp_sinkhorn_op(x, h_res, h_out, h_post, phi, alpha, base, norm_eps=1e-6,
+                                   hc_eps=1e-6, clamp_min=0.0, clamp_max=0.0, iter_times=20):
+    """The fused mhc_post + mhc_pre_clamp_sinkhorn through the registered op:
+    (x_next, y, post_out, comb_frag), differentiable in every tensor input."""
+    x_next, y, post_out, comb, _, _, _ = torch.ops.flagos_mhc.mhc_post_pre_clamp_sinkhorn(
+        x, h_res, h_out, h_post, phi, alpha, base, float(norm_eps), float(hc_eps), float(clamp_min),
+        float(clamp_max), int(iter_times))
+    return x_next, y, post_out, comb

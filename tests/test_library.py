@@ -1,11 +1,12 @@
 """torch.library registration of the mHC operators (FlagOS_mhc.library).
 
-CPU: the four ops are registered, their shape functions give the real
+CPU: the five ops are registered, their shape functions give the real
 kernels' output shapes / dtypes on meta tensors, and the real implementations
 refuse CPU tensors (no CPU path).  GPU: torch.library.opcheck (schema,
-fake-tensor and autograd registration checks), a compiled mHC layer
-(torch.compile, aot_eager backend, fullgraph) against the same layer run
-eagerly through the autograd wrappers, and HIP-graph capture of the four-op
+fake-tensor and autograd registration checks), compiled mHC layers (unfused
+and fused post + pre; torch.compile, aot_eager backend, fullgraph) against
+the same layers run eagerly through the autograd wrappers, and HIP-graph
+capture of the four-op
 chain replayed several times against eager results (bit equality: the kernels
 are deterministic and the replay runs the same launches)."""
 
@@ -17,7 +18,8 @@ import torch
 import FlagOS_mhc as m
 from FlagOS_mhc import library as L
 
-OPS = ("mhc_post", "mhc_post_backward", "mhc_pre_clamp_sinkhorn", "mhc_pre_clamp_sinkhorn_backward")
+OPS = ("mhc_post", "mhc_post_backward", "mhc_pre_clamp_sinkhorn", "mhc_pre_clamp_sinkhorn_backward",
+       "mhc_post_pre_clamp_sinkhorn")
 
 
 def test_ops_registered():
@@ -54,6 +56,9 @@ def test_meta_shapes(lead, N):
         assert [(tuple(o.shape), o.dtype) for o in g] == [
             (x.shape, torch.bfloat16), ((M, N * D), torch.float32), ((3,), torch.float32),
             ((M,), torch.float32)]
+        f = torch.ops.flagos_mhc.mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post, phi, alpha, base,
+                                                             1e-6, 1e-6, 0.0, 0.0, 20)
+        assert [(tuple(o.shape), o.dtype) for o in f] == [(x.shape, torch.bfloat16)] + want
 
 
 def test_cpu_tensors_refused():
@@ -102,6 +107,58 @@ def test_opcheck():
     torch.library.opcheck(torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward.default,
                           (x.detach(), phi.detach(), alpha, base, inv, mixes, pre, noise,
                            torch.randn_like(post_out), torch.randn_like(comb)) + args)
+
+
+@pytest.mark.gpu
+def test_opcheck_post_pre():
+    T, N, D = 40, 4, 3136   # the fused kernel (D >= 3136, D % 64 == 0)
+    print(f"[opcheck post_pre] T={T} N={N} D={D}", flush=True)
+    x, phi, alpha, base, noise, upstream = _layer_inputs(T, N, D)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(4)
+    h_res = torch.softmax(torch.randn(T, N, N, device=DEV, generator=g), -1)
+    h_post = torch.rand(T, N, device=DEV, generator=g) * 2
+    torch.library.opcheck(torch.ops.flagos_mhc.mhc_post_pre_clamp_sinkhorn.default,
+                          (x.requires_grad_(True), h_res, noise, h_post, phi.requires_grad_(True), alpha,
+                           base) + tuple(KW.values()))
+
+
+@pytest.mark.gpu
+def test_compiled_fused_layer_matches_eager():
+    """x -> fused(post, pre) op -> loss, compiled (aot_eager, fullgraph) and
+    eager through the autograd Function."""
+    T, N, D = 64, 4, 3136
+    print(f"[compile post_pre] T={T} N={N} D={D}", flush=True)
+    x, phi, alpha, base, noise, upstream = _layer_inputs(T, N, D, seed=21)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(22)
+    h_res = torch.softmax(torch.randn(T, N, N, device=DEV, generator=g), -1)
+    h_post = torch.rand(T, N, device=DEV, generator=g) * 2
+    w = torch.randn(T, D, device=DEV, generator=g)
+
+    def loss_of(fn, *a):
+        xn, y, p, c = fn(*a, **KW)
+        return (xn.float() * upstream.float()).sum() + (y.float() * w).sum() + p.sum() + c.sum()
+
+    def run(fn):
+        leaves = [t.clone().requires_grad_(True) for t in (x, h_res, noise, h_post, phi, alpha, base)]
+        loss_of(fn, *leaves).backward()
+        return [t.grad for t in leaves]
+
+    torch._dynamo.reset()
+    compiled = torch.compile(lambda *a: loss_of(L.mhc_post_pre_clamp_sinkhorn_op, *a), backend="aot_eager",
+                             fullgraph=True)
+
+    def run_compiled():
+        leaves = [t.clone().requires_grad_(True) for t in (x, h_res, noise, h_post, phi, alpha, base)]
+        compiled(*leaves).backward()
+        return [t.grad for t in leaves]
+
+    got = run_compiled()
+    want = run(m.mhc_post_pre_clamp_sinkhorn_fn)
+    torch.cuda.synchronize()
+    for a, b, name in zip(got, want, ("x", "h_res", "h_out", "h_post", "phi", "alpha", "base")):
+        torch.testing.assert_close(a.float(), b.float(), rtol=1e-5, atol=1e-5, msg=name)
 
 
 def _layer(ops, x, phi, alpha, base, noise, upstream):
