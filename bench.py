@@ -270,25 +270,38 @@ def main():
         op_stats[name] = {"ms": round(mean, 4), "ms_median": round(med, 4),
                           "algo_GB": round(algo[name] / 1e9, 4), "GBps": round(gbs, 1),
                           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
-    # mhc_post of layer l fused with mhc_pre_clamp_sinkhorn of layer l+1: in a
-    # stack of layers it replaces post_fwd + pre_fwd, so the per-layer chain
-    # becomes fused + post_bwd + pre_bwd (reported beside the defined metric)
-    fused = lambda: m.mhc_post_pre_clamp_sinkhorn(x, o["comb_frag"], h_out, o["post_out"], phi, alpha,
-                                                  base, need_backward=True, **kw)
-    fused()
-    f_med, f_mean = time_events(fused, reps, stream)
-    f_algo = T * (2 * N * D * 2 + 2 * D * 2 + 4 * (N * N + N) + 4 * (2 * N + 2 * N * N + 1 + 2 * N + N * N)) \
-        + (2 * N + N * N) * N * D * 2
-    post_pre = {"ms": round(f_mean, 4), "ms_median": round(f_med, 4),
-                "unfused_ms": round(op_stats["post_fwd"]["ms"] + op_stats["pre_fwd"]["ms"], 4),
-                "algo_GB": round(f_algo / 1e9, 4),
-                "GBps": round(f_algo / (f_mean * 1e-3) / 1e9, 1),
-                "layer_tokens_per_s": round(T / ((f_mean + op_stats["post_bwd"]["ms"]
-                                                  + op_stats["pre_bwd"]["ms"]) * 1e-3), 1)}
     glue = {
         "h_out_add_ms": round(time_events(lambda: out["y"] + noise, reps, stream)[1], 4),
         "grad_x_accumulate_ms": round(time_events(lambda: pb[0] + res[3][0], reps, stream)[1], 4),
     }
+    # A stack of mHC layers runs mhc_post of layer l and mhc_pre_clamp_sinkhorn
+    # of layer l+1 back to back, and its backward adds the pre backward's
+    # grad_x to the residual-stream gradient of the same tensor.  The fused
+    # forward replaces post_fwd + pre_fwd; the accumulating pre backward
+    # replaces pre_bwd + that add.  Reported beside the defined metric.
+    from FlagOS_mhc.mhc_pre_clamp_sinkhorn_backward import _pre_backward
+    fused = lambda: m.mhc_post_pre_clamp_sinkhorn(x, o["comb_frag"], h_out, o["post_out"], phi, alpha,
+                                                  base, need_backward=True, **kw)
+    acc = lambda: _pre_backward(x, phi, alpha, base, o["inv_rms"], o["mixes"], o["pre"], pb[2], pb[3],
+                                pb[1], kw["norm_eps"], kw["hc_eps"], kw["clamp_min"], kw["clamp_max"],
+                                kw["iter_times"], grad_x_in=pb[0])
+    fused()
+    acc()
+    f_med, f_mean = time_events(fused, reps, stream)
+    a_mean = time_events(acc, reps, stream)[1]
+    f_algo = T * (2 * N * D * 2 + 2 * D * 2 + 4 * (N * N + N) + 4 * (4 * N + 3 * N * N + 1)) \
+        + (2 * N + N * N) * N * D * 2
+    layer_fused = f_mean + op_stats["post_bwd"]["ms"] + a_mean
+    layer_unfused = sum(v["ms"] for v in op_stats.values()) + glue["grad_x_accumulate_ms"]
+    post_pre = {"fwd_ms": round(f_mean, 4), "fwd_ms_median": round(f_med, 4),
+                "fwd_unfused_ms": round(op_stats["post_fwd"]["ms"] + op_stats["pre_fwd"]["ms"], 4),
+                "fwd_algo_GB": round(f_algo / 1e9, 4),
+                "fwd_GBps": round(f_algo / (f_mean * 1e-3) / 1e9, 1),
+                "pre_bwd_acc_ms": round(a_mean, 4),
+                "pre_bwd_plus_add_ms": round(op_stats["pre_bwd"]["ms"] + glue["grad_x_accumulate_ms"], 4),
+                "layer_ms": round(layer_fused, 4), "layer_unfused_ms": round(layer_unfused, 4),
+                "layer_tokens_per_s": round(T / (layer_fused * 1e-3), 1),
+                "layer_unfused_tokens_per_s": round(T / (layer_unfused * 1e-3), 1)}
     # roofline of the dominant kernel: the longest of the operators that run
     # as a single kernel (pre_bwd is four kernels; its largest is shorter)
     dominant = max(SINGLE_KERNEL_OPS, key=lambda k: op_stats[k]["ms"])

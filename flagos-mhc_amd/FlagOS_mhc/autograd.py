@@ -9,7 +9,7 @@ from .mhc_post import mhc_post
 from .mhc_post_backward import mhc_post_backward
 from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from .mhc_pre_clamp_sinkhorn import _pre_forward
-from .mhc_pre_clamp_sinkhorn_backward import mhc_pre_clamp_sinkhorn_backward
+from .mhc_pre_clamp_sinkhorn_backward import _pre_backward, mhc_pre_clamp_sinkhorn_backward
 
 
 class MhcPostFn(torch.autograd.Function):
@@ -80,8 +80,9 @@ def mhc_pre_clamp_sinkhorn_fn(
 
 class MhcPostPreClampSinkhornFn(torch.autograd.Function):
     """mhc_post (layer l) + mhc_pre_clamp_sinkhorn (layer l+1) with one fused
-    forward.  The backward runs the pre backward on x_next, adds the gradient
-    that reaches x_next directly, and runs the post backward."""
+    forward.  The backward runs the pre backward on x_next with the gradient
+    that reaches x_next directly accumulated into its grad_x in the same
+    kernel (``mhc_pre_bwd_acc``), then the post backward."""
 
     @staticmethod
     def forward(ctx, x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
@@ -105,13 +106,11 @@ class MhcPostPreClampSinkhornFn(torch.autograd.Function):
         if grad_comb_frag is None:
             N = pre.shape[-1]
             grad_comb_frag = torch.zeros((pre.shape[0], N, N), dtype=torch.float32, device=pre.device)
-        gxn, gphi, galpha, gbase = mhc_pre_clamp_sinkhorn_backward(
-            x_next, phi, alpha, base, inv_rms, None, mixes, None, pre,
-            grad_y.contiguous(), grad_post_out.contiguous(), grad_comb_frag.contiguous(),
-            norm_eps=norm_eps, hc_eps=hc_eps, clamp_min=clamp_min, clamp_max=clamp_max,
-            iter_times=iter_times)
-        g = gxn if grad_x_next is None else grad_x_next + gxn
-        gx, ghres, ghout, ghpost = mhc_post_backward(g.contiguous(), x, h_res, h_out, h_post)
+        g, gphi, galpha, gbase = _pre_backward(
+            x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
+            grad_post_out.contiguous(), grad_comb_frag.contiguous(), norm_eps, hc_eps, clamp_min,
+            clamp_max, iter_times, grad_x_in=grad_x_next)
+        gx, ghres, ghout, ghpost = mhc_post_backward(g, x, h_res, h_out, h_post)
         return gx, ghres, ghout, ghpost, gphi, galpha, gbase, None, None, None, None, None
 
 

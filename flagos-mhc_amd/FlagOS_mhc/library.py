@@ -14,6 +14,10 @@ HIP-graph capture records their kernels on the current stream):
         inv_rms, mixes, pre, grad_y, grad_post_out, grad_comb_frag, norm_eps,
         hc_eps, clamp_min, clamp_max, iter_times)
         -> (grad_x, grad_phi, grad_alpha, grad_base)
+    torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward_acc(x, phi, alpha, base,
+        inv_rms, mixes, pre, grad_y, grad_post_out, grad_comb_frag, grad_x_in,
+        norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+        -> (grad_x_in + grad_x, grad_phi, grad_alpha, grad_base)
     torch.ops.flagos_mhc.mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post,
         phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
         -> (x_next, y, post_out, comb_frag, inv_rms, mixes, pre)
@@ -40,7 +44,7 @@ from .mhc_post import mhc_post
 from .mhc_post_backward import mhc_post_backward
 from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from .mhc_pre_clamp_sinkhorn import _pre_forward
-from .mhc_pre_clamp_sinkhorn_backward import mhc_pre_clamp_sinkhorn_backward
+from .mhc_pre_clamp_sinkhorn_backward import _pre_backward, mhc_pre_clamp_sinkhorn_backward
 
 NAMESPACE = "flagos_mhc"
 
@@ -130,6 +134,24 @@ def _pre_bwd_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_ou
             base.new_empty((base.numel(),), **f32))
 
 
+@torch.library.custom_op(f"{NAMESPACE}::mhc_pre_clamp_sinkhorn_backward_acc", mutates_args=())
+def _pre_bwd_acc(x: Tensor, phi: Tensor, alpha: Tensor, base: Tensor, inv_rms: Tensor,
+                 mixes: Tensor, pre: Tensor, grad_y: Tensor, grad_post_out: Tensor,
+                 grad_comb_frag: Tensor, grad_x_in: Tensor, norm_eps: float, hc_eps: float,
+                 clamp_min: float, clamp_max: float,
+                 iter_times: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    return tuple(_pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                               grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+                               grad_x_in=grad_x_in))
+
+
+@_pre_bwd_acc.register_fake
+def _pre_bwd_acc_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                      grad_comb_frag, grad_x_in, norm_eps, hc_eps, clamp_min, clamp_max, iter_times):
+    return _pre_bwd_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                         grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+
+
 def _pre_setup(ctx, inputs, output):
     x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times = inputs
     _, _, _, inv_rms, mixes, pre = output
@@ -181,11 +203,10 @@ def _post_pre_setup(ctx, inputs, output):
 def _post_pre_grad(ctx, grad_x_next, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes,
                    _g_pre):
     x, h_res, h_out, h_post, phi, alpha, base, x_next, inv_rms, mixes, pre = ctx.saved_tensors
-    gxn, gphi, galpha, gbase = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward(
+    g, gphi, galpha, gbase = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward_acc(
         x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
-        grad_post_out.contiguous(), grad_comb_frag.contiguous(), *ctx.args)
-    gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward(
-        (grad_x_next + gxn).contiguous(), x, h_res, h_out, h_post)
+        grad_post_out.contiguous(), grad_comb_frag.contiguous(), grad_x_next.contiguous(), *ctx.args)
+    gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward(g, x, h_res, h_out, h_post)
     return (gx, ghres, ghout, ghpost, gphi.to(phi.dtype), galpha.reshape(alpha.shape).to(alpha.dtype),
             gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None)
 

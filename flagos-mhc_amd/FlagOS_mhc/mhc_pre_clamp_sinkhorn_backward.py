@@ -48,9 +48,19 @@ def mhc_pre_clamp_sinkhorn_backward(
     """Returns (grad_x shaped like x in x's dtype, grad_phi (M, N*D) fp32,
     grad_alpha (3,) fp32, grad_base (M,) fp32)
     (src/mhc_pre_clamp_sinkhorn_backward.py:1292-1391)."""
-    del x_scaled, h_res_logits, norm_eps  # recomputed / folded into inv_rms
+    del x_scaled, h_res_logits  # recomputed
+    return _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                         grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+
+
+def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out, grad_comb_frag,
+                  norm_eps, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in=None):
+    """mhc_pre_clamp_sinkhorn_backward; with ``grad_x_in`` (shaped and typed
+    like x) the returned grad_x is grad_x_in + dL/dx, accumulated inside the
+    kernel (``mhc_pre_bwd_acc``)."""
+    del norm_eps  # folded into inv_rms
     _lib.require_device("mhc_pre_clamp_sinkhorn_backward", x, phi, alpha, base, inv_rms, mixes,
-                        pre, grad_y, grad_post_out, grad_comb_frag)
+                        pre, grad_y, grad_post_out, grad_comb_frag, grad_x_in)
     if x.dim() not in (3, 4):
         raise ValueError(f"unsupported x.dim()={x.dim()}")
     shape = tuple(x.shape)
@@ -88,14 +98,18 @@ def mhc_pre_clamp_sinkhorn_backward(
     lib = _lib.load()
     ws_bytes = int(lib.mhc_pre_bwd_workspace_size(T, N, D, pcode, int(iter_times)))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    common = (xf.data_ptr(), xcode, phi_c.data_ptr(), pcode, alpha_c.data_ptr(), base_c.data_ptr(),
+              inv_c.data_ptr(), mixes_c.data_ptr(), pre_c.data_ptr(), gy.data_ptr(),
+              gpost.data_ptr(), gcomb.data_ptr(), float(hc_eps), float(clamp_min),
+              float(clamp_max), int(iter_times))
+    tail = (grad_x.data_ptr(), grad_phi.data_ptr(), grad_alpha.data_ptr(), grad_base.data_ptr(),
+            ws.data_ptr(), ws_bytes, T, N, D, _lib.stream_of(xf))
     with torch.cuda.device(dev):
-        rc = lib.mhc_pre_bwd(
-            xf.data_ptr(), xcode, phi_c.data_ptr(), pcode, alpha_c.data_ptr(), base_c.data_ptr(),
-            inv_c.data_ptr(), mixes_c.data_ptr(), pre_c.data_ptr(), gy.data_ptr(),
-            gpost.data_ptr(), gcomb.data_ptr(), float(hc_eps), float(clamp_min),
-            float(clamp_max), int(iter_times), grad_x.data_ptr(), grad_phi.data_ptr(),
-            grad_alpha.data_ptr(), grad_base.data_ptr(), ws.data_ptr(), ws_bytes, T, N, D,
-            _lib.stream_of(xf))
+        if grad_x_in is None:
+            rc = lib.mhc_pre_bwd(*common, *tail)
+        else:
+            gin = grad_x_in.reshape(T, N * D).to(xf.dtype).contiguous()
+            rc = lib.mhc_pre_bwd_acc(*common, gin.data_ptr(), *tail)
     _lib.check(rc, "mhc_pre_clamp_sinkhorn_backward")
     return grad_x.view(*shape), grad_phi.reshape(phi.shape), grad_alpha, grad_base
 

@@ -493,6 +493,7 @@ struct PreBwdStreamArgs {
   const uint16_t* gTw;   // [ceil(T/16)][MT][64][2][4]
   const float4* coef;    // (T, N) {pre, inv, scale, 0}
   bf16_t* gx;
+  const bf16_t* gin;     // accumulating form (LDS-pipelined kernel): grad_x = gin + dL/dx
   float* gphi_part;      // [nsplit][M][K]
   int64_t T;
   int D;
@@ -693,11 +694,14 @@ template <int N> struct DmaCfg {
   static constexpr int GT = GA + 2 * MK;   // [MT]    g^T blocks (A of grad_phi), both planes
   static constexpr int CF = GT + MT;       // [N/4]   coefficients of 16 tokens x N streams
   static constexpr int UNITS = CF + N / 4;
+  static constexpr int GI = UNITS;               // [N][4]  grad_x_in rows (accumulating form)
+  static constexpr int UNITS_ACC = GI + 4 * N;
   static constexpr int SHARED = UNITS - GY;      // units loaded once per block, split over waves
   static constexpr int LMIN = 4 + SHARED / N;    // fewest loads a wave issues per tile
 };
 
 constexpr int kDmaStages = 5;                  // 125 KB of LDS: one block per CU
+constexpr int kDmaAccStages = 3;               // accumulating form: 3 x 41 KB
 constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
 
 struct PreBwdDmaArgs {
@@ -710,20 +714,23 @@ struct PreBwdDmaArgs {
   const uint16_t* gTw;   // [ceil(T/16)][MT][64][2][4]
   const float4* coef;    // (T, N) {pre, inv, scale, 0}
   bf16_t* gx;
+  const bf16_t* gin;     // accumulating form: grad_x = gin + dL/dx (same layout as x)
   float* part;           // [nsplit][M][K] grad_phi partials
   int64_t T;
   int D;
   int64_t ntiles;
 };
 
-template <int N, int P, int S>
+template <int N, int P, int S, bool ACC>
 __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
   using C = DmaCfg<N>;
   using PD = PreDims<N>;
   constexpr int M = PD::M, MT = PD::MT, MK = PD::MK, MP32 = PD::MP32;
-  constexpr int VC = C::VC, VD = C::VD, DW = C::DW, TT = C::TT, UNITS = C::UNITS;
-  constexpr int VM_START = (S - 2) * C::LMIN;               // before any grad_x store
-  constexpr int VM_STEADY = (S - 2) * C::LMIN + (S - 1) * 4;
+  constexpr int VC = C::VC, VD = C::VD, DW = C::DW, TT = C::TT;
+  constexpr int UNITS = ACC ? C::UNITS_ACC : C::UNITS;
+  constexpr int LMIN = C::LMIN + (ACC ? 4 : 0);             // grad_x_in: 4 more loads a wave
+  constexpr int VM_START = (S - 2) * LMIN;                  // before any grad_x store
+  constexpr int VM_STEADY = (S - 2) * LMIN + (S - 1) * 4;
   static_assert(N == 4 && S >= 2 && VM_STEADY < 64, "pipeline shape");
   __shared__ u32x4 ring[S * UNITS * kWave];
 
@@ -750,6 +757,15 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
       const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(st + (C::X + 4 * n + e) * kWave), 16,
                                                off, 0, 0, 2 /* nt */);
+    }
+    if constexpr (ACC) {
+      const auto ri = rows_rsrc(a.gin + tb * K, (int64_t)nv * K * 2);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ri, (lds_void_t*)(st + (C::GI + 4 * n + e) * kWave), 16,
+                                                 off, 0, 0, 2 /* nt */);
+      }
     }
     for (int u = n; u < C::SHARED; u += N) {
       const int unit = C::GY + u;
@@ -838,6 +854,8 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
       gt[1] = ag[3];
     }
     lds_read4<N * 16>(cfu, sbase + C::CF * 1024 + (4 * q * N + n) * 16);  // tokens 4q+e, stream n
+    u32x4 gi[4];
+    if constexpr (ACC) lds_read4<1024>(gi, la + (C::GI + 4 * n) * 1024);  // grad_x_in rows, tokens 4q+e
 
     const int64_t tb = ctile * TT;
     const int nv = (int)(T - tb < TT ? T - tb : TT);
@@ -881,8 +899,12 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
         const uint32_t xw = xr[e][w], gw = gr[e][w];
         const float x0 = __uint_as_float(xw << 16), x1 = __uint_as_float(xw & 0xffff0000u);
         const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
-        const float o0 = fmaf(fz, x0, fmaf(fy, gs[2 * w][e], g0 * fx));
-        const float o1 = fmaf(fz, x1, fmaf(fy, gs[2 * w + 1][e], g1 * fx));
+        float o0 = fmaf(fz, x0, fmaf(fy, gs[2 * w][e], g0 * fx));
+        float o1 = fmaf(fz, x1, fmaf(fy, gs[2 * w + 1][e], g1 * fx));
+        if constexpr (ACC) {
+          o0 += __uint_as_float(gi[e][w] << 16);
+          o1 += __uint_as_float(gi[e][w] & 0xffff0000u);
+        }
         o[w] = pack_bf16x2(o0, o1);
       }
       // rows >= nv fall outside the range and are dropped, as are columns >= D;
@@ -1099,12 +1121,17 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* 
   da.gTw = sta.gTw;
   da.coef = sta.coef;
   da.gx = sta.gx;
+  da.gin = sta.gin;
   da.part = sta.gphi_part;
   da.T = sta.T;
   da.D = D;
   da.ntiles = lay.ntiles;
-  hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages>), dim3((unsigned)ncb, (unsigned)ns), dim3(64 * N), 0,
-                     st, da);
+  if (sta.gin)
+    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), dim3((unsigned)ncb, (unsigned)ns),
+                       dim3(64 * N), 0, st, da);
+  else
+    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages, false>), dim3((unsigned)ncb, (unsigned)ns),
+                       dim3(64 * N), 0, st, da);
   int rc = check_launch("pre_bwd_dma");
   if (rc) return rc;
   const int64_t n = (int64_t)lay.M * lay.K;
@@ -1113,10 +1140,24 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* 
   return check_launch("pre_bwd_sum_splits");
 }
 
+// grad_x += grad_x_in for the kernels without an accumulating form
+template <typename S>
+__global__ void add_into_kernel(S* out, const S* in, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    store_elem(out, i, load_elem(out, i) + load_elem(in, i));
+}
+
+template <typename S>
+static int add_into(void* out, const void* in, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL((add_into_kernel<S>), dim3(reduce_grid(n)), dim3(256), 0, st, static_cast<S*>(out),
+                     static_cast<const S*>(in), n);
+  return check_launch("pre_bwd_add_into");
+}
+
 template <int N, typename S>
 static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwdMainArgs& ma,
                           PreBwdStreamArgs sta, float* grad_phi, float* grad_alpha,
-                          float* grad_base, bool vec, hipStream_t st) {
+                          float* grad_base, bool vec, const void* gin, hipStream_t st) {
   const dim3 gA((unsigned)lay.nblkA), bA(kBwdThreads);
   const bool streaming = vec && std::is_same<S, bf16_t>::value;
   if (streaming) {
@@ -1135,14 +1176,17 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
   if (rc) return rc;
   if constexpr (N == 4) {
     if (streaming && dma_usable<N>(sta.D)) {
+      sta.gin = static_cast<const bf16_t*>(gin);  // accumulated inside the kernel
       rc = lay.P == 1 ? launch_dma<N, 1>(lay, sta, grad_phi, st) : launch_dma<N, 2>(lay, sta, grad_phi, st);
       if (rc) return rc;
       return sum_alpha_base(lay, sa, grad_alpha, grad_base, st);
     }
   }
+  const int64_t nx = sta.T * N * (int64_t)sta.D;
   if (streaming) {
     rc = lay.P == 1 ? launch_stream<N, 1>(lay, sta, st) : launch_stream<N, 2>(lay, sta, st);
     if (rc) return rc;
+    if (gin && (rc = add_into<S>(sta.gx, gin, nx, st))) return rc;
     return reduce_tail(lay, sa, sta.gphi_part, sta.nsplit, grad_phi, grad_alpha, grad_base, st);
   }
   const dim3 gB((unsigned)lay.chunks, (unsigned)lay.nsplit), bB(256);
@@ -1152,16 +1196,17 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
     hipLaunchKernelGGL((pre_bwd_main_kernel<N, S, false>), gB, bB, 0, st, ma);
   rc = check_launch("pre_bwd_main");
   if (rc) return rc;
+  if (gin && (rc = add_into<S>(ma.gx, gin, nx, st))) return rc;
   return reduce_tail(lay, sa, ma.gphi_part, lay.nsplit, grad_phi, grad_alpha, grad_base, st);
 }
 
 template <typename S>
 static int dispatch_pre_bwd(int N, const BwdLayout& lay, const PreBwdSmallArgs& sa,
                             const PreBwdMainArgs& ma, const PreBwdStreamArgs& sta, float* gphi,
-                            float* galpha, float* gbase, bool vec, hipStream_t st) {
+                            float* galpha, float* gbase, bool vec, const void* gin, hipStream_t st) {
   switch (N) {
-    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, st);
-    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, st);
+    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, st);
+    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
 }
@@ -1182,14 +1227,13 @@ extern "C" size_t mhc_pre_bwd_workspace_size(int64_t T, int32_t N, int32_t D, in
   return bwd_layout(T, N, D, phi_dtype, iter_times).total;
 }
 
-extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
-                           const float* alpha, const float* base, const float* inv_rms,
-                           const float* mixes, const float* pre, const void* grad_y,
-                           const float* grad_post_out, const float* grad_comb_frag, float hc_eps,
-                           float clamp_min, float clamp_max, int32_t iter_times, void* grad_x,
-                           float* grad_phi, float* grad_alpha, float* grad_base, void* workspace,
-                           size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
-                           void* stream) {
+static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                         const float* alpha, const float* base, const float* inv_rms, const float* mixes,
+                         const float* pre, const void* grad_y, const float* grad_post_out,
+                         const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
+                         int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
+                         float* grad_alpha, float* grad_base, void* workspace, size_t workspace_bytes,
+                         int64_t T, int32_t N, int32_t D, void* stream) {
   clear_error();
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
@@ -1274,11 +1318,45 @@ extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int3
   sta.T = T;
   sta.D = D;
 
-  const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(grad_y) && aligned16(grad_x);
+  const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(grad_y) && aligned16(grad_x) &&
+                   (!grad_x_in || aligned16(grad_x_in));
   switch (x_dtype) {
-    case MHC_DTYPE_BF16: return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, st);
-    case MHC_DTYPE_F16: return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, st);
-    case MHC_DTYPE_F32: return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, st);
+    case MHC_DTYPE_BF16:
+      return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, st);
+    case MHC_DTYPE_F16:
+      return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, st);
+    case MHC_DTYPE_F32:
+      return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: x dtype %d not supported", x_dtype);
+}
+
+extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                           const float* alpha, const float* base, const float* inv_rms,
+                           const float* mixes, const float* pre, const void* grad_y,
+                           const float* grad_post_out, const float* grad_comb_frag, float hc_eps,
+                           float clamp_min, float clamp_max, int32_t iter_times, void* grad_x,
+                           float* grad_phi, float* grad_alpha, float* grad_base, void* workspace,
+                           size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                           void* stream) {
+  return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                       grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, nullptr, grad_x, grad_phi,
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, stream);
+}
+
+extern "C" int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                               const float* alpha, const float* base, const float* inv_rms,
+                               const float* mixes, const float* pre, const void* grad_y,
+                               const float* grad_post_out, const float* grad_comb_frag, float hc_eps,
+                               float clamp_min, float clamp_max, int32_t iter_times, const void* grad_x_in,
+                               void* grad_x, float* grad_phi, float* grad_alpha, float* grad_base,
+                               void* workspace, size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                               void* stream) {
+  if (!grad_x_in && T > 0) {
+    clear_error();
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: null grad_x_in");
+  }
+  return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                       grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in, grad_x, grad_phi,
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, stream);
 }

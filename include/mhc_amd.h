@@ -114,6 +114,24 @@ int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dty
                 int32_t D, void* stream);
 
 /*
+ * mhc_pre_bwd that accumulates: grad_x = grad_x_in + dL/dx, in one pass for
+ * N = 4 bf16 with 16-byte aligned rows (other shapes add in a second kernel).
+ * No counterpart in the reference; it is for callers that sum the pre
+ * backward's grad_x with another gradient of the same x (the fused post + pre
+ * layer below: the residual-stream gradient reaching x_next), which otherwise
+ * takes a separate read-read-write pass.  grad_x_in: (T,N,D) `x_dtype`, may be
+ * grad_x itself.  Other arguments as in mhc_pre_bwd.
+ */
+int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                    const float* alpha, const float* base, const float* inv_rms,
+                    const float* mixes, const float* pre, const void* grad_y,
+                    const float* grad_post_out, const float* grad_comb_frag, float hc_eps,
+                    float clamp_min, float clamp_max, int32_t iter_times, const void* grad_x_in,
+                    void* grad_x, float* grad_phi, float* grad_alpha, float* grad_base,
+                    void* workspace, size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                    void* stream);
+
+/*
  * Fused forward of mhc_post (layer l) and mhc_pre_clamp_sinkhorn (layer l+1).
  * No single counterpart in the reference: it replaces the device work of
  * mhc_post (src/mhc_post.py:296-352) followed by mhc_pre_clamp_sinkhorn on its

@@ -134,6 +134,12 @@ def test_post_pre_autograd(D):
     y, p, c = m.mhc_pre_clamp_sinkhorn_fn(xn, b[4], b[5], b[6], **KW)
     loss(xn, y, p, c).backward()
     torch.cuda.synchronize()
+    # The fused backward rounds x_next's total gradient once (grad_x_next +
+    # dL/dx accumulated in fp32 inside the pre backward), the unfused chain
+    # twice (dL/dx to bf16, then autograd's bf16 add); h_res / h_post
+    # gradients are D-long sums over that gradient, so they get an absolute
+    # tolerance of 1% of their largest entry.
     for ta, tb, name in zip(a, b, ("x", "h_res", "h_out", "h_post", "phi", "alpha", "base")):
         w = _np(tb.grad)
-        assert_close(ta.grad.float(), w, 2e-2, 2e-2 + 2e-3 * np.abs(w).max(), name + ".grad")
+        atol = (1e-2 if name in ("h_res", "h_post") else 2e-3) * np.abs(w).max()
+        assert_close(ta.grad.float(), w, 2e-2, 2e-2 + atol, name + ".grad")

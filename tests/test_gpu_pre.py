@@ -201,6 +201,34 @@ def test_pre_bwd_parity(T, N, D, dtype, phi_dtype, recipe, clamp, iters):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T,N,D,dtype", [
+    (1000, 4, 1024, torch.bfloat16),    # LDS-pipelined kernel, grad_x_in accumulated in place
+    (4133, 4, 7168, torch.bfloat16),
+    (70, 8, 256, torch.bfloat16),       # streaming kernel + separate add
+    (40, 4, 100, torch.bfloat16),       # D % 8 != 0: generic kernel + separate add
+    (33, 4, 64, torch.float32),
+])
+def test_pre_bwd_accumulate(T, N, D, dtype):
+    """mhc_pre_bwd_acc: grad_x = grad_x_in + dL/dx (one rounding), the other
+    gradients bit-identical to mhc_pre_bwd."""
+    from FlagOS_mhc.mhc_pre_clamp_sinkhorn_backward import _pre_backward
+    print(f"[pre_bwd acc] T={T} N={N} D={D} {dtype}", flush=True)
+    x, phi, alpha, base, gy, gpost, gcomb = pre_inputs(T, N, D, dtype, dtype if dtype != torch.bfloat16 else torch.bfloat16)
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-10.0, clamp_max=10.0, iter_times=20)
+    out = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **kw)
+    gin = torch.randn(x.shape, device=DEV, generator=_gen(9)).to(dtype)
+    args = (x, phi, alpha, base, out["inv_rms"], out["mixes"], out["pre"], gy, gpost, gcomb,
+            kw["norm_eps"], kw["hc_eps"], kw["clamp_min"], kw["clamp_max"], kw["iter_times"])
+    gx, gphi, ga, gb = _pre_backward(*args)
+    gxa, gphia, gaa, gba = _pre_backward(*args, grad_x_in=gin)
+    torch.cuda.synchronize()
+    assert gxa.shape == x.shape and gxa.dtype == dtype
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert_close(gxa.float(), (gx.float() + gin.float()), tol, tol, "grad_x_in + grad_x")
+    for a, b, name in ((gphia, gphi, "phi"), (gaa, ga, "alpha"), (gba, gb, "base")):
+        assert torch.equal(a, b), name
+
+
 def test_pre_bwd_empty_batch():
     N, D = 4, 64
     x, phi, alpha, base, *_ = pre_inputs(1, N, D)

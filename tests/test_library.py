@@ -1,6 +1,6 @@
 """torch.library registration of the mHC operators (FlagOS_mhc.library).
 
-CPU: the five ops are registered, their shape functions give the real
+CPU: the six ops are registered, their shape functions give the real
 kernels' output shapes / dtypes on meta tensors, and the real implementations
 refuse CPU tensors (no CPU path).  GPU: torch.library.opcheck (schema,
 fake-tensor and autograd registration checks), compiled mHC layers (unfused
@@ -19,7 +19,7 @@ import FlagOS_mhc as m
 from FlagOS_mhc import library as L
 
 OPS = ("mhc_post", "mhc_post_backward", "mhc_pre_clamp_sinkhorn", "mhc_pre_clamp_sinkhorn_backward",
-       "mhc_post_pre_clamp_sinkhorn")
+       "mhc_pre_clamp_sinkhorn_backward_acc", "mhc_post_pre_clamp_sinkhorn")
 
 
 def test_ops_registered():
