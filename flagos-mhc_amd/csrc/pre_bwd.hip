@@ -1352,9 +1352,13 @@ extern "C" int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, 
                                void* grad_x, float* grad_phi, float* grad_alpha, float* grad_base,
                                void* workspace, size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
                                void* stream) {
-  if (!grad_x_in && T > 0) {
+  if (T > 0) {
     clear_error();
-    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: null grad_x_in");
+    if (!grad_x_in) return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: null grad_x_in");
+    const uintptr_t bytes = (uintptr_t)T * (uintptr_t)N * (uintptr_t)D * (x_dtype == MHC_DTYPE_F32 ? 4u : 2u);
+    const uintptr_t in = (uintptr_t)grad_x_in, out = (uintptr_t)grad_x;
+    if (grad_x && in < out + bytes && out < in + bytes)
+      return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: grad_x_in overlaps grad_x");
   }
   return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                        grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in, grad_x, grad_phi,

@@ -119,8 +119,8 @@ int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dty
  * No counterpart in the reference; it is for callers that sum the pre
  * backward's grad_x with another gradient of the same x (the fused post + pre
  * layer below: the residual-stream gradient reaching x_next), which otherwise
- * takes a separate read-read-write pass.  grad_x_in: (T,N,D) `x_dtype`, may be
- * grad_x itself.  Other arguments as in mhc_pre_bwd.
+ * takes a separate read-read-write pass.  grad_x_in: (T,N,D) `x_dtype`; it
+ * must not overlap grad_x.  Other arguments as in mhc_pre_bwd.
  */
 int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
                     const float* alpha, const float* base, const float* inv_rms,

@@ -83,6 +83,21 @@ def test_error_codes_without_device(lib):
     assert rc == -1 and b"workspace" in lib.mhc_last_error()
     # T == 0 is a no-op for the forward ops
     assert lib.mhc_post_fwd(dummy, dummy, dummy, dummy, dummy, 0, 4, 64, 1, None) == 0
+    # accumulating pre backward: grad_x_in is required and must not overlap grad_x
+    gx, gin_ok, gin_overlap = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x900000), ctypes.c_void_p(0x100400)
+    acc = lambda gin, out: lib.mhc_pre_bwd_acc(
+        dummy, 1, dummy, 1, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 1e-6, 0.0, 0.0, 20,
+        gin, out, dummy, dummy, dummy, dummy, 16, 16, 4, 64, None)
+    assert acc(None, gx) == -1 and b"null grad_x_in" in lib.mhc_last_error()
+    assert acc(gx, gx) == -1 and b"overlaps" in lib.mhc_last_error()
+    assert acc(gin_overlap, gx) == -1 and b"overlaps" in lib.mhc_last_error()   # 16*4*64*2 bytes
+    assert acc(gin_ok, gx) == -1 and b"workspace" in lib.mhc_last_error()       # passes to mhc_pre_bwd's checks
+    # fused post + pre forward: N outside {4, 8} and null pointers are rejected before any launch
+    fused = lambda x, n: lib.mhc_post_pre_fwd(
+        x, dummy, dummy, dummy, 1, dummy, 1, dummy, dummy, 1e-6, 1e-6, 0.0, 0.0, 20, dummy, dummy, dummy,
+        dummy, None, None, None, None, dummy, 256, 16, n, 64, None)
+    assert fused(dummy, 6) == -2 and b"N=6" in lib.mhc_last_error()
+    assert fused(None, 4) == -1 and b"null" in lib.mhc_last_error()
 
 
 def test_ops_refuse_cpu_tensors():
