@@ -29,6 +29,7 @@
 namespace mhc {
 
 constexpr int kFwdTile = 64;  // tokens per block
+constexpr size_t kPreFwdWsBase = 256;  // workspace bytes before the split-K area
 constexpr int kFwdThreads = 256;
 
 struct PreFwdArgs {
@@ -52,6 +53,13 @@ struct PreFwdArgs {
   float* x_scaled;
   int64_t T;
   int D;
+  // split-K form (few tiles): contraction stages per split and the partial
+  // sums [splits][T][M] / [splits][T], pre / inv_rms of every token for y
+  int split_stages;
+  float* part;
+  float* part_ssq;
+  float* pre_ws;
+  float* inv_ws;
 };
 
 template <int N, typename S, bool VEC, int P>
@@ -327,7 +335,9 @@ template <int N> struct FwdDmaCfg {
   static constexpr int S = N == 4 ? kFwdDmaStages : 3;  // slots (LDS: S * UNITS KB + mixes)
 };
 
-template <int N, bool XS>
+// SPLIT: block (tile, s) runs contraction stages [s * split_stages, ..) of
+// one tile and writes its partial sums; heads and y run in two more kernels.
+template <int N, bool XS, bool SPLIT>
 __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) {
   using C = FwdDmaCfg<N>;
   constexpr int M = PreDims<N>::M, MT = C::MT, L = N * N, TT = kFwdTile, S = C::S, UNITS = C::UNITS;
@@ -354,11 +364,15 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   const int64_t T = a.T;
   const int nst_c = (K + CW - 1) / CW;
   const int ncb = (D + YW - 1) / YW;
-  const int per_tile = nst_c + (TT / 4) * ncb;
   const int64_t ntiles = (T + TT - 1) / TT;
-  const int64_t my_tiles = (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
-  if (my_tiles <= 0) return;  // uniform over the block
-  const int64_t J = my_tiles * per_tile;
+  // stage range of this block within its tiles: [s_first, per_tile)
+  const int s_first = SPLIT ? (int)blockIdx.y * a.split_stages : 0;
+  const int per_tile = SPLIT ? (s_first + a.split_stages < nst_c ? s_first + a.split_stages : nst_c)
+                             : nst_c + (TT / 4) * ncb;
+  const int64_t my_tiles = SPLIT ? (blockIdx.x < ntiles ? 1 : 0)
+                                 : (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
+  if (my_tiles <= 0 || s_first >= per_tile) return;  // uniform over the block
+  const int64_t J = my_tiles * (per_tile - s_first);
   const bf16_t* __restrict__ x = static_cast<const bf16_t*>(a.x);
   const auto rphi = rows_rsrc(a.phi, (int64_t)M * K * 2);
 
@@ -370,7 +384,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
 
   // ---- loads of stage j --------------------------------------------------
   int64_t itile = blockIdx.x;  // tile and stage of the next issue
-  int is = 0;
+  int is = s_first;
   auto issue = [&](int64_t j) {
     const int64_t tb = itile * TT;
     const int nv = (int)(T - tb < TT ? T - tb : TT);
@@ -409,7 +423,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
         }
     }
     if (++is == per_tile) {
-      is = 0;
+      is = s_first;
       itile += gridDim.x;
     }
   };
@@ -421,13 +435,14 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float ssq = 0.f;
   int64_t ctile = blockIdx.x;
-  int cs = 0;  // stage of the current tile being consumed
+  int cs = s_first;  // stage of the current tile being consumed
   for (int64_t j = 0; j < J; ++j) {
     // this wave's loads of stage j have landed once at most V newer vector
     // memory operations are outstanding (windows of one stage kind get the
-    // exact count, mixed windows the smallest)
+    // exact count, mixed windows the smallest; a split block runs
+    // contraction stages only, which store nothing)
     if (j + S - 2 < J) {
-      if (cs >= S - 1 && cs + S - 2 < nst_c)
+      if (SPLIT || (cs >= S - 1 && cs + S - 2 < nst_c))
         wait_vmcnt<VM_C>();
       else if (cs >= nst_c + S - 1 && cs + S - 2 < per_tile)
         wait_vmcnt<VM_Y>();
@@ -514,7 +529,23 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
 
-      if (cs == nst_c - 1) {
+      if (SPLIT && cs == per_tile - 1) {
+        // ---- this split's partial sums of the tile --------------------------
+        // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; after
+        // the shuffles the lanes of row r hold this split's sum(x^2) of token
+        // 16*wave + r
+        ssq += __shfl_xor(ssq, 16, kWave);
+        ssq += __shfl_xor(ssq, 32, kWave);
+        const int64_t pbase = (int64_t)blockIdx.y * T;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t tok = tb + 16 * wave + 4 * q + v;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            if (tok < T && 16 * mt + r < M) a.part[(pbase + tok) * M + 16 * mt + r] = acc[mt][v];
+        }
+        if (q == 0 && tb + 16 * wave + r < T) a.part_ssq[pbase + tb + 16 * wave + r] = ssq;
+      } else if (!SPLIT && cs == nst_c - 1) {
         // ---- tile's mixes, heads and Sinkhorn -----------------------------
         // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; the
         // lane of row r (any q) holds sum(x^2) of token 16*wave + r
@@ -620,10 +651,136 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
       }
     }
     if (++cs == per_tile) {
-      cs = 0;
+      cs = s_first;
       ctile += gridDim.x;
     }
   }
+}
+
+// ---- split-K form, kernels 2 and 3 -----------------------------------------
+// Kernel 2: one N x N lane group per token sums the splits' partials in split
+// order, then computes inv_rms, mixes, heads, clamp and Sinkhorn exactly as
+// the single-kernel form does after its last contraction stage.
+template <int N>
+__global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArgs a, int nsplit) {
+  constexpr int M = PreDims<N>::M, L = N * N, TPP = kFwdThreads / L;
+  const int tid = threadIdx.x, e = tid % L;
+  const int64_t T = a.T;
+  const int64_t tok = (int64_t)blockIdx.x * TPP + tid / L;
+  const bool ok = tok < T;
+  const int64_t tk = ok ? tok : T - 1;  // lanes past T compute on the last token and store nothing
+  const float K = (float)(N * a.D);
+  float ssq = 0.f, acc_l = 0.f, acc_h = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t row = (int64_t)s * T + tk;
+    ssq += a.part_ssq[row];
+    acc_l += a.part[row * M + 2 * N + e];
+    if (e < 2 * N) acc_h += a.part[row * M + e];
+  }
+  const float inv = 1.0f / sqrtf(ssq / K + a.norm_eps);
+  const float mix_l = acc_l * inv, mix_h = acc_h * inv;
+  if (ok) {
+    if (a.mixes) {
+      a.mixes[tok * M + 2 * N + e] = mix_l;
+      if (e < 2 * N) a.mixes[tok * M + e] = mix_h;
+    }
+    if (e == 0) {
+      a.inv_ws[tok] = inv;
+      if (a.inv_rms) a.inv_rms[tok] = inv;
+    }
+  }
+  const float a0 = a.alpha[0], a1 = a.alpha[1], a2 = a.alpha[2];
+  const float logit = mix_l * a2 + a.base[2 * N + e];
+  const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
+  const float c = sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
+  if (ok) {
+    a.comb[tok * L + e] = c;
+    if (a.logits) a.logits[tok * L + e] = logit;
+  }
+  if (e < N) {
+    const float p = sigmoidf_(mix_h * a0 + a.base[e]) + a.hc_eps;
+    if (ok) {
+      a.pre_ws[tok * N + e] = p;
+      if (a.pre) a.pre[tok * N + e] = p;
+    }
+  } else if (e < 2 * N) {
+    const float po = 2.0f * sigmoidf_(mix_h * a1 + a.base[e]);
+    if (ok) a.post_out[tok * N + (e - N)] = po;
+  }
+}
+
+// Kernel 3: y[t, d] = sum_n pre[t, n] * x[t, n, d] (and x_scaled), a wave per
+// (token, 512-column block), 8 columns a lane, same FMA order as the y stages
+// of the single-kernel form.
+template <int N, bool XS>
+__global__ __launch_bounds__(kFwdThreads) void pre_fwd_y_kernel(PreFwdArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = (int64_t)blockIdx.x * (kFwdThreads / kWave) + (threadIdx.x >> 6);
+  const int D = a.D;
+  const int col = blockIdx.y * 512 + 8 * lane;
+  if (t >= a.T || col >= D) return;
+  const bf16_t* x = static_cast<const bf16_t*>(a.x) + t * N * D + col;
+  float p[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) p[n] = a.pre_ws[t * N + n];
+  u32x4 X[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) X[n] = ld16nt(x + (int64_t)n * D);
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      o[2 * w] = fmaf(p[n], __uint_as_float(X[n][w] << 16), o[2 * w]);
+      o[2 * w + 1] = fmaf(p[n], __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
+    }
+  u32x4 ov;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
+  st16nt(static_cast<bf16_t*>(a.y) + t * D + col, ov);
+  if constexpr (XS) {
+    const float inv = a.inv_ws[t];
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u32x4 xs;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const uint32_t xw = X[n][2 * h + w];
+          xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv);
+          xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv);
+        }
+        st16(a.x_scaled + (t * N + n) * (int64_t)D + col + 4 * h, xs);
+      }
+  }
+}
+
+// Split-K plan for few tiles: ntiles <= 256 splits K into up to 64 parts so
+// that about 512 blocks run the contraction; the plan depends on (T, N, D)
+// only, so results do not depend on the device.
+struct FwdSplitPlan {
+  int nsplit = 0, stages = 0;
+  size_t bytes = 0;  // workspace for partials, pre and inv_rms
+};
+
+static FwdSplitPlan fwd_split_plan(int64_t T, int N, int D) {
+  FwdSplitPlan p;
+  const int64_t ntiles = (T + kFwdTile - 1) / kFwdTile;
+  const int nst_c = (int)(((int64_t)N * D + 127) / 128);
+  if (T <= 0 || ntiles > 256) return p;
+  int64_t want = (512 + ntiles - 1) / ntiles;
+  if (want > nst_c / 4) want = nst_c / 4;
+  if (want > 64) want = 64;
+  if (want < 2) return p;
+  p.stages = (int)((nst_c + want - 1) / want);
+  p.nsplit = (nst_c + p.stages - 1) / p.stages;
+  const int M = 2 * N + N * N;
+  p.bytes = align256((size_t)p.nsplit * T * M * 4) + align256((size_t)p.nsplit * T * 4) +
+            align256((size_t)T * N * 4) + align256((size_t)T * 4);
+  return p;
 }
 
 // The LDS-pipelined kernel covers the bf16 fast path (N = 4, 8).  Buffer
@@ -634,7 +791,7 @@ static bool fwd_dma_usable(const PreFwdArgs& a, int N, bool bf16x, bool vec) {
 }
 
 template <int N>
-static int launch_pre_fwd_dma(const PreFwdArgs& a, hipStream_t st) {
+static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_bytes, hipStream_t st) {
   static int cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -642,11 +799,39 @@ static int launch_pre_fwd_dma(const PreFwdArgs& a, hipStream_t st) {
                     cus[dev] <= 0))
     cus[dev] = 256;
   const int64_t ntiles = (a.T + kFwdTile - 1) / kFwdTile;
+  const FwdSplitPlan plan = fwd_split_plan(a.T, N, a.D);
+  if (plan.nsplit >= 2 && workspace && workspace_bytes >= kPreFwdWsBase + plan.bytes) {
+    // few tiles: split K over blocks, then heads and y in their own kernels
+    char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
+    const int M = 2 * N + N * N;
+    a.split_stages = plan.stages;
+    a.part = reinterpret_cast<float*>(w);
+    w += align256((size_t)plan.nsplit * a.T * M * 4);
+    a.part_ssq = reinterpret_cast<float*>(w);
+    w += align256((size_t)plan.nsplit * a.T * 4);
+    a.pre_ws = reinterpret_cast<float*>(w);
+    w += align256((size_t)a.T * N * 4);
+    a.inv_ws = reinterpret_cast<float*>(w);
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false, true>), dim3((unsigned)ntiles, (unsigned)plan.nsplit),
+                       dim3(kFwdThreads), 0, st, a);
+    int rc = check_launch("pre_fwd_split");
+    if (rc) return rc;
+    constexpr int TPP = kFwdThreads / (N * N);
+    hipLaunchKernelGGL((pre_fwd_finalize_kernel<N>), dim3((unsigned)((a.T + TPP - 1) / TPP)), dim3(kFwdThreads),
+                       0, st, a, plan.nsplit);
+    if ((rc = check_launch("pre_fwd_finalize"))) return rc;
+    const dim3 gy((unsigned)((a.T + 3) / 4), (unsigned)((a.D + 511) / 512));
+    if (a.x_scaled)
+      hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), gy, dim3(kFwdThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((pre_fwd_y_kernel<N, false>), gy, dim3(kFwdThreads), 0, st, a);
+    return check_launch("pre_fwd_y");
+  }
   const int64_t grid = ntiles < cus[dev] ? ntiles : cus[dev];  // one block per CU (LDS ring)
   if (a.x_scaled)
-    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, true>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, true, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   return check_launch("pre_fwd_dma");
 }
 
@@ -684,11 +869,11 @@ static int dispatch_pre_fwd(int N, const PreFwdArgs& a, bool vec, hipStream_t st
 using namespace mhc;
 
 extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype) {
-  (void)T;
   if (N <= 0 || D <= 0) return 0;
   const int M = 2 * N + N * N;
   const int64_t K = (int64_t)N * D;
-  if (phi_dtype == MHC_DTYPE_BF16 && K % 8 == 0) return 256;  // used directly when aligned
+  if (phi_dtype == MHC_DTYPE_BF16 && K % 8 == 0)  // phi used directly; split-K partials for few tiles
+    return kPreFwdWsBase + fwd_split_plan(T, N, D).bytes;
   return align256(phi_planes_bytes(phi_dtype, M, K));
 }
 
@@ -735,7 +920,8 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   a.D = D;
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(y) && (!x_scaled || aligned16(x_scaled));
   if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec))
-    return N == 4 ? launch_pre_fwd_dma<4>(a, st) : launch_pre_fwd_dma<8>(a, st);
+    return N == 4 ? launch_pre_fwd_dma<4>(a, workspace, workspace_bytes, st)
+                  : launch_pre_fwd_dma<8>(a, workspace, workspace_bytes, st);
   switch (x_dtype) {
     case MHC_DTYPE_BF16: return dispatch_pre_fwd<bf16_t>(N, a, vec, st);
     case MHC_DTYPE_F16: return dispatch_pre_fwd<f16_t>(N, a, vec, st);
