@@ -6,7 +6,9 @@
 // <grad_y, y> + <grad_post_out, post_out> + <grad_comb_frag, comb_frag>.
 //
 // Kernel A (pre_bwd_small_kernel), a block per 16 tokens:
-//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token)
+//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token;
+//   for 4 < T < 16384 summed in fixed order from the partials of
+//   pre_bwd_gpre_kernel, a block per (token, 2048 columns))
 //   Sinkhorn / softmax / clamp / sigmoid-head VJP, lane per matrix element
 //   -> grad_mixes (T,M) and scale[t] = -inv^2 * <grad_mixes, mixes> / (N*D)
 //   (because <x, grad_mixes @ phi> = <grad_mixes, mixes> / inv), plus a
@@ -59,9 +61,54 @@ struct PreBwdSmallArgs {
   float* partial;  // (gridDim.x, 3 + M)
   float* sink_scratch;
   int64_t sink_stride;
+  const float* gpre_part;  // [T][gpre_chunks][N] grad_pre partials, or null
+  int gpre_chunks;
   int64_t T;
   int D;
 };
+
+// grad_pre partials for small T, where a block per 16 tokens leaves most of
+// the chip idle and each wave streams (N + 1) * D elements serially: a block
+// per (token, 2048-column chunk) writes part[t][chunk][n] =
+// sum over its columns of grad_y[t,d] * x[t,n,d] (per-thread FMA chain over
+// 8 columns, wave_sum, then the 4 waves in order).
+constexpr int kGpreCols = kBwdThreads * 8;
+
+template <int N, typename S, bool VEC>
+__global__ __launch_bounds__(kBwdThreads) void pre_bwd_gpre_kernel(const void* xv, const void* gyv, float* part,
+                                                                   int D) {
+  __shared__ float red[kBwdThreads / kWave][N];
+  const S* __restrict__ x = static_cast<const S*>(xv);
+  const S* __restrict__ gy = static_cast<const S*>(gyv);
+  const int64_t tok = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int64_t d = (int64_t)blockIdx.y * kGpreCols + tid * 8;
+  const bool ok = d < D;
+  float acc[N];
+  float g8[8];
+  load8f<S, VEC>(gy + tok * D, d, D, ok, g8);
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    float x8[8];
+    load8f<S, VEC>(x + (tok * N + n) * D, d, D, ok, x8);
+    acc[n] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
+  }
+#pragma unroll
+  for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
+  if (lane == 0) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) red[wave][n] = acc[n];
+  }
+  __syncthreads();
+  if (tid < N) {
+    float s = red[0][tid];
+#pragma unroll
+    for (int w = 1; w < kBwdThreads / kWave; ++w) s += red[w][tid];
+    part[(tok * gridDim.y + blockIdx.y) * N + tid] = s;
+  }
+}
 
 template <int N, typename S, bool VEC>
 __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallArgs a) {
@@ -78,31 +125,44 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t t0 = (int64_t)blockIdx.x * kBwdTile;
 
-  // ---- grad_pre: a wave per token ---------------------------------------
-  for (int q = 0; q < kBwdTile / 4; ++q) {
-    const int tt = wave + 4 * q;
-    const int64_t tok = t0 + tt;
-    float acc[N];
+  // ---- grad_pre: summed from the split kernel's partials, or a wave per token
+  if (a.gpre_part) {
+    if (tid < kBwdTile * N) {
+      const int tt = tid / N, n = tid % N;
+      const int64_t tok = t0 + tt;
+      float s = 0.f;
+      if (tok < a.T) {
+        const float* pp = a.gpre_part + tok * a.gpre_chunks * N + n;
+        for (int c = 0; c < a.gpre_chunks; ++c) s += pp[c * N];
+      }
+      gp_sh[tt][n] = s;
+    }
+  } else {
+    for (int q = 0; q < kBwdTile / 4; ++q) {
+      const int tt = wave + 4 * q;
+      const int64_t tok = t0 + tt;
+      float acc[N];
 #pragma unroll
-    for (int n = 0; n < N; ++n) acc[n] = 0.f;
-    if (tok < a.T) {
-      for (int64_t d = (int64_t)lane * 8; d < D; d += kWave * 8) {
-        float g8[8];
-        load8f<S, VEC>(gy + tok * D, d, D, true, g8);
+      for (int n = 0; n < N; ++n) acc[n] = 0.f;
+      if (tok < a.T) {
+        for (int64_t d = (int64_t)lane * 8; d < D; d += kWave * 8) {
+          float g8[8];
+          load8f<S, VEC>(gy + tok * D, d, D, true, g8);
 #pragma unroll
-        for (int n = 0; n < N; ++n) {
-          float x8[8];
-          load8f<S, VEC>(x + (tok * N + n) * D, d, D, true, x8);
+          for (int n = 0; n < N; ++n) {
+            float x8[8];
+            load8f<S, VEC>(x + (tok * N + n) * D, d, D, true, x8);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
+            for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
+          }
         }
       }
-    }
 #pragma unroll
-    for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
-    if (lane == 0) {
+      for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
+      if (lane == 0) {
 #pragma unroll
-      for (int n = 0; n < N; ++n) gp_sh[tt][n] = acc[n];
+        for (int n = 0; n < N; ++n) gp_sh[tt][n] = acc[n];
+      }
     }
   }
   __syncthreads();
@@ -968,14 +1028,22 @@ __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__
 // host side
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int M, L, C, P, MP, MP32, nsplit, chunks, DC;
+  int M, L, C, P, MP, MP32, nsplit, chunks, DC, gpre_chunks;
   int64_t K, nblkA, tok_per_split, ntiles;
-  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink;
+  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink, off_gpre;
   size_t off_gmP, off_gTw, off_coef, total;
 };
 
 // Token splits of the grad_phi partials: kMaxSplits for the split kernels,
 // more for the LDS-pipelined kernel when D has few 128-column blocks.
+// Between these token counts grad_pre comes from the split kernel: below
+// kGpreSplitMaxT kernel A's grid (a block per 16 tokens) leaves the chip
+// partly idle (measured on MI355X at D = 7168: T = 64 113 -> 52 us, T = 4096
+// 214 -> 170 us for the whole backward, even at 16384, 3% slower at 65536);
+// up to 4 tokens a wave per token streams them in parallel and the extra
+// launch costs more than it saves.
+constexpr int64_t kGpreSplitMinT = 5, kGpreSplitMaxT = 16384;
+
 static int64_t dma_max_splits(int D) {
   const int64_t ncb = (D + DmaCfg<4>::DW - 1) / DmaCfg<4>::DW;
   const int64_t s = kDmaMaxBlocks / ncb;
@@ -1026,6 +1094,9 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   off += align256((size_t)T * N * 16);
   b.off_sink = off;
   if (iters > kSinkRegIters) off += align256((size_t)(iters - 1) * b.nblkA * kBwdTile * b.L * 4);
+  b.gpre_chunks = (T >= kGpreSplitMinT && T < kGpreSplitMaxT) ? (int)((D + kGpreCols - 1) / kGpreCols) : 0;
+  b.off_gpre = off;
+  off += align256((size_t)T * b.gpre_chunks * N * 4);
   b.total = off;
   return b;
 }
@@ -1168,11 +1239,21 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
     sa.gTw = nullptr;
     sa.coef = nullptr;
   }
+  int rc;
+  if (sa.gpre_part) {
+    const dim3 gG((unsigned)sa.T, (unsigned)lay.gpre_chunks);
+    float* part = const_cast<float*>(sa.gpre_part);
+    if (vec)
+      hipLaunchKernelGGL((pre_bwd_gpre_kernel<N, S, true>), gG, bA, 0, st, sa.x, sa.gy, part, sa.D);
+    else
+      hipLaunchKernelGGL((pre_bwd_gpre_kernel<N, S, false>), gG, bA, 0, st, sa.x, sa.gy, part, sa.D);
+    if ((rc = check_launch("pre_bwd_gpre"))) return rc;
+  }
   if (vec)
     hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, true>), gA, bA, 0, st, sa);
   else
     hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, false>), gA, bA, 0, st, sa);
-  int rc = check_launch("pre_bwd_small");
+  rc = check_launch("pre_bwd_small");
   if (rc) return rc;
   if constexpr (N == 4) {
     if (streaming && dma_usable<N>(sta.D)) {
@@ -1284,6 +1365,8 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
   sa.partial = reinterpret_cast<float*>(ws + lay.off_partial);
   sa.sink_scratch = reinterpret_cast<float*>(ws + lay.off_sink);
   sa.sink_stride = lay.nblkA * kBwdTile * lay.L;
+  sa.gpre_part = lay.gpre_chunks ? reinterpret_cast<float*>(ws + lay.off_gpre) : nullptr;
+  sa.gpre_chunks = lay.gpre_chunks;
   sa.T = T;
   sa.D = D;
 
