@@ -79,9 +79,9 @@ def run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
 
 # operators that are one kernel launch at the bench shapes -> that kernel
 SINGLE_KERNEL_OPS = {
-    "pre_fwd": "pre_fwd_dma_kernel<4, false>",
-    "post_fwd": "post_fwd_dma_kernel<4>",
-    "post_bwd": "post_bwd_dma_kernel<4>",
+    "pre_fwd": "pre_fwd_dma_kernel<4, false, false>",
+    "post_fwd": "post_fwd_block_kernel<4, bf16_t, true>",
+    "post_bwd": "post_bwd_block_kernel<4, bf16_t, true>",
 }
 
 

@@ -1,4 +1,4 @@
-// mhc_post forward and backward: one wave64 per token, streaming over D.
+// mhc_post forward and backward: streaming kernels over tokens.
 //
 //   y[t,i,:]      = sum_j h_res[t,j,i] * x[t,j,:] + h_post[t,i] * h_out[t,:]
 //   grad_x[t,j,:] = sum_i h_res[t,j,i] * gy[t,i,:]
@@ -9,13 +9,15 @@
 // (src/mhc_post.py:344-352, src/mhc_post_backward.py:624-643).
 //
 // Layout: x, y, gy, grad_x are contiguous (T, N, D); h_out / grad_h_out are
-// (T, D); gates are fp32 (T, N, N) and (T, N).  A wave owns one token: the
-// N*N + N gates are wave-uniform scalar loads, every lane streams 16-byte
-// vectors of each of the N rows, accumulates in fp32 and stores with
-// round-to-nearest-even (streaming stores: outputs are not re-read here).
-// The backward's N*N + N dot products are reduced across the wave once per
-// token and written by plain stores (no atomics), so results are
-// deterministic.
+// (T, D); gates are fp32 (T, N, N) and (T, N).  Three forms, chosen by shape
+// (see kPostStreamMinT / kPostBlockMinD): a block of waves per token (the
+// waves split D), a wave per token (backward, N > 4), and for N = 4 bf16 an
+// LDS-pipelined wave per token.  In each, the N*N + N gates are uniform
+// scalar loads, every lane streams 16-byte vectors of each of the N rows,
+// accumulates in fp32 and stores with round-to-nearest-even (streaming
+// stores: outputs are not re-read here).  The backward's N*N + N dot products
+// are reduced across the wave (and the block) once per token and written by
+// plain stores (no atomics), so results are deterministic.
 #include <type_traits>
 
 #include "common.hpp"
@@ -25,62 +27,6 @@
 namespace mhc {
 
 constexpr int kPostWavesPerBlock = 4;
-
-template <int N, typename S, bool VECTOR>
-__global__ __launch_bounds__(256) void post_fwd_kernel(
-    const S* __restrict__ x, const float* __restrict__ h_res, const S* __restrict__ h_out,
-    const float* __restrict__ h_post, S* __restrict__ y, int64_t T, int D) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t t = (int64_t)blockIdx.x * kPostWavesPerBlock + wave;
-  if (t >= T) return;
-
-  float hr[N * N], hp[N];
-#pragma unroll
-  for (int i = 0; i < N * N; ++i) hr[i] = h_res[t * (N * N) + i];
-#pragma unroll
-  for (int i = 0; i < N; ++i) hp[i] = h_post[t * N + i];
-
-  const int64_t xrow = t * (int64_t)N * D;
-  const int64_t hrow = t * (int64_t)D;
-
-  if constexpr (VECTOR) {
-    constexpr int V = Store<S>::VEC;
-#pragma unroll 2
-    for (int d = lane * V; d < D; d += kWave * V) {
-      float xv[N][V], hv[V];
-#pragma unroll
-      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16(x + xrow + (int64_t)j * D + d), xv[j]);
-      Store<S>::unpack(ld16(h_out + hrow + d), hv);
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        float o[V];
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-          float acc = hp[i] * hv[e];
-#pragma unroll
-          for (int j = 0; j < N; ++j) acc = fmaf(hr[j * N + i], xv[j][e], acc);
-          o[e] = acc;
-        }
-        st16nt(y + xrow + (int64_t)i * D + d, Store<S>::pack(o));
-      }
-    }
-  } else {
-    for (int d = lane; d < D; d += kWave) {
-      float xv[N];
-#pragma unroll
-      for (int j = 0; j < N; ++j) xv[j] = load_elem(x, xrow + (int64_t)j * D + d);
-      const float hv = load_elem(h_out, hrow + d);
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        float acc = hp[i] * hv;
-#pragma unroll
-        for (int j = 0; j < N; ++j) acc = fmaf(hr[j * N + i], xv[j], acc);
-        store_elem(y, xrow + (int64_t)i * D + d, acc);
-      }
-    }
-  }
-}
 
 template <int N, typename S, bool VECTOR>
 __global__ __launch_bounds__(256) void post_bwd_kernel(
@@ -187,6 +133,177 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
     for (int i = 0; i < N; ++i) g_hpost[t * N + i] = acc_p[i];
   }
 }
+
+// ---------------------------------------------------------------------------
+// Block forms: a block of W = min(8, chunks) waves per token, the waves
+// splitting D into 64 * V-column chunks (wave w takes chunks w, w + W, ...),
+// so all of a token's loads are in flight at once.  With a wave per token a
+// call with few tokens runs a handful of waves, each streaming its whole
+// token serially (T = 1, N = 4, D = 7168: 11 us forward, 19 us backward,
+// against 3.3 and 6.4 us here).  At large T the block forms also beat the
+// LDS-pipelined kernels below for D >= 5120 (c5 width: backward 2.30 against
+// 2.50 ms, forward 1.58 against 1.60 ms on one MI355X): with one 8-wave block
+// per CU only 256 tokens are in flight, each read as a few contiguous
+// streams.  Every output element of the forward, grad_x and grad_h_out uses
+// the FMA order of the other kernels (bit-identical results); the backward's
+// N * N + N dot products are summed per lane over its chunks, across the wave
+// (wave_sum), then over the waves in order through LDS (no atomics).
+// ---------------------------------------------------------------------------
+constexpr int kPostBlockWaves = 8;
+
+template <int N, typename S, bool VECTOR>
+__global__ __launch_bounds__(kWave * kPostBlockWaves) void post_fwd_block_kernel(
+    const S* __restrict__ x, const float* __restrict__ h_res, const S* __restrict__ h_out,
+    const float* __restrict__ h_post, S* __restrict__ y, int D) {
+  constexpr int V = VECTOR ? Store<S>::VEC : 1, CW = kWave * V;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x / kWave;
+  const int64_t t = blockIdx.x;
+  float hr[N * N], hp[N];
+#pragma unroll
+  for (int i = 0; i < N * N; ++i) hr[i] = h_res[t * (N * N) + i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) hp[i] = h_post[t * N + i];
+  const int64_t xrow = t * (int64_t)N * D, hrow = t * (int64_t)D;
+  for (int d = wave * CW + lane * V; d < D; d += W * CW) {
+    float xv[N][V], hv[V];
+    if constexpr (VECTOR) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16(x + xrow + (int64_t)j * D + d), xv[j]);
+      Store<S>::unpack(ld16(h_out + hrow + d), hv);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) xv[j][0] = load_elem(x, xrow + (int64_t)j * D + d);
+      hv[0] = load_elem(h_out, hrow + d);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      float o[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float acc = hp[i] * hv[e];
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc = fmaf(hr[j * N + i], xv[j][e], acc);
+        o[e] = acc;
+      }
+      if constexpr (VECTOR)
+        st16nt(y + xrow + (int64_t)i * D + d, Store<S>::pack(o));
+      else
+        store_elem(y, xrow + (int64_t)i * D + d, o[0]);
+    }
+  }
+}
+
+template <int N, typename S, bool VECTOR>
+__global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel(
+    const S* __restrict__ gy, const S* __restrict__ x, const float* __restrict__ h_res,
+    const S* __restrict__ h_out, const float* __restrict__ h_post, S* __restrict__ gx,
+    float* __restrict__ g_hres, S* __restrict__ g_hout, float* __restrict__ g_hpost, int D) {
+  constexpr int V = VECTOR ? Store<S>::VEC : 1, CW = kWave * V, R = N * N + N;
+  __shared__ float red[kPostBlockWaves][R];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x / kWave;
+  const int64_t t = blockIdx.x;
+  float hr[N * N], hp[N];
+#pragma unroll
+  for (int i = 0; i < N * N; ++i) hr[i] = h_res[t * (N * N) + i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) hp[i] = h_post[t * N + i];
+  float acc_r[N * N], acc_p[N];
+#pragma unroll
+  for (int i = 0; i < N * N; ++i) acc_r[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc_p[i] = 0.f;
+  const int64_t xrow = t * (int64_t)N * D, hrow = t * (int64_t)D;
+  for (int d = wave * CW + lane * V; d < D; d += W * CW) {
+    float gv[N][V], xv[N][V], hv[V];
+    if constexpr (VECTOR) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) Store<S>::unpack(ld16(gy + xrow + (int64_t)i * D + d), gv[i]);
+#pragma unroll
+      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16(x + xrow + (int64_t)j * D + d), xv[j]);
+      Store<S>::unpack(ld16(h_out + hrow + d), hv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) gv[i][0] = load_elem(gy, xrow + (int64_t)i * D + d);
+#pragma unroll
+      for (int j = 0; j < N; ++j) xv[j][0] = load_elem(x, xrow + (int64_t)j * D + d);
+      hv[0] = load_elem(h_out, hrow + d);
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      float o[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) a = fmaf(hr[j * N + i], gv[i][e], a);
+        o[e] = a;
+      }
+      if constexpr (VECTOR)
+        st16nt(gx + xrow + (int64_t)j * D + d, Store<S>::pack(o));
+      else
+        store_elem(gx, xrow + (int64_t)j * D + d, o[0]);
+    }
+    float oh[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < N; ++i) a = fmaf(hp[i], gv[i][e], a);
+      oh[e] = a;
+    }
+    if constexpr (VECTOR)
+      st16nt(g_hout + hrow + d, Store<S>::pack(oh));
+    else
+      store_elem(g_hout, hrow + d, oh[0]);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+#pragma unroll
+      for (int j = 0; j < N; ++j)
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc_r[j * N + i] = fmaf(xv[j][e], gv[i][e], acc_r[j * N + i]);
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc_p[i] = fmaf(hv[e], gv[i][e], acc_p[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N * N; ++i) acc_r[i] = wave_sum(acc_r[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc_p[i] = wave_sum(acc_p[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < N * N; ++i) red[wave][i] = acc_r[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) red[wave][N * N + i] = acc_p[i];
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < R; r += blockDim.x) {  // R = 72 > 64 threads at N = 8, W = 1
+    float v = red[0][r];
+    for (int w = 1; w < W; ++w) v += red[w][r];
+    if (r < N * N)
+      g_hres[t * (N * N) + r] = v;
+    else
+      g_hpost[t * N + r - N * N] = v;
+  }
+}
+
+// Waves per block: one per 64 * V-column chunk, at most kPostBlockWaves.
+static inline int post_block_waves(int D, int V) {
+  const int chunks = (D + kWave * V - 1) / (kWave * V);
+  return chunks < kPostBlockWaves ? chunks : kPostBlockWaves;
+}
+
+// Kernel choice (measured on MI355X): the LDS-pipelined kernels (N = 4 bf16)
+// and the wave-per-token backward (other shapes) need at least
+// kPostStreamMinT tokens to fill the chip; for N = 4 bf16 the LDS-pipelined
+// kernels win only for D < kPostBlockMinD.  The wave-per-token backward stays
+// for N > 4 at large T (the block form needs 225 VGPRs at N = 8 and ran 1.5x
+// slower at D = 2048).
+constexpr int64_t kPostStreamMinT = 1024;
+constexpr int kPostBlockMinD = 5120;
 
 // ---------------------------------------------------------------------------
 // LDS-pipelined forms (bf16, 16-byte aligned rows, D % 8 == 0)
@@ -471,24 +588,24 @@ static int64_t post_dma_grid(K kernel, int64_t T) {
 template <int N, typename S>
 static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
                            const float* h_post, void* y, int64_t T, int D, hipStream_t st) {
-  const dim3 grid((unsigned)((T + kPostWavesPerBlock - 1) / kPostWavesPerBlock));
   const dim3 block(kWave * kPostWavesPerBlock);
   const bool vec = (D % Store<S>::VEC == 0) && aligned16(x) && aligned16(h_out) && aligned16(y);
   if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
-    if (vec && D % 8 == 0) {
+    if (vec && T >= kPostStreamMinT && D < kPostBlockMinD) {
       const int64_t g = post_dma_grid(post_fwd_dma_kernel<N>, T);
       hipLaunchKernelGGL((post_fwd_dma_kernel<N>), dim3((unsigned)g), block, 0, st, (const bf16_t*)x, h_res,
                          (const bf16_t*)h_out, h_post, (bf16_t*)y, T, D);
       return check_launch("post_fwd_dma");
     }
   }
+  const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1));
   if (vec)
-    hipLaunchKernelGGL((post_fwd_kernel<N, S, true>), grid, block, 0, st, (const S*)x, h_res,
-                       (const S*)h_out, h_post, (S*)y, T, D);
+    hipLaunchKernelGGL((post_fwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)x, h_res,
+                       (const S*)h_out, h_post, (S*)y, D);
   else
-    hipLaunchKernelGGL((post_fwd_kernel<N, S, false>), grid, block, 0, st, (const S*)x, h_res,
-                       (const S*)h_out, h_post, (S*)y, T, D);
-  return check_launch("post_fwd");
+    hipLaunchKernelGGL((post_fwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)x, h_res,
+                       (const S*)h_out, h_post, (S*)y, D);
+  return check_launch("post_fwd_block");
 }
 
 template <int N, typename S>
@@ -499,8 +616,22 @@ static int launch_post_bwd(const void* gy, const void* x, const float* h_res, co
   const dim3 block(kWave * kPostWavesPerBlock);
   const bool vec = (D % Store<S>::VEC == 0) && aligned16(gy) && aligned16(x) &&
                    aligned16(h_out) && aligned16(gx) && aligned16(g_hout);
+  bool block_form = T < kPostStreamMinT || N <= 4;
   if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
-    if (vec && D % 8 == 0) {
+    if (vec && T >= kPostStreamMinT && D < kPostBlockMinD) block_form = false;  // LDS-pipelined kernel
+  }
+  if (block_form) {
+    const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1));
+    if (vec)
+      hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                         h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D);
+    else
+      hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                         h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D);
+    return check_launch("post_bwd_block");
+  }
+  if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
+    if (vec) {
       const int64_t g = post_dma_grid(post_bwd_dma_kernel<N>, T);
       hipLaunchKernelGGL((post_bwd_dma_kernel<N>), dim3((unsigned)g), block, 0, st, (const bf16_t*)gy,
                          (const bf16_t*)x, h_res, (const bf16_t*)h_out, h_post, (bf16_t*)gx, g_hres,

@@ -133,6 +133,7 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
       float s = 0.f;
       if (tok < a.T) {
         const float* pp = a.gpre_part + tok * a.gpre_chunks * N + n;
+#pragma unroll 4
         for (int c = 0; c < a.gpre_chunks; ++c) s += pp[c * N];
       }
       gp_sh[tt][n] = s;

@@ -671,11 +671,15 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
   const int64_t tk = ok ? tok : T - 1;  // lanes past T compute on the last token and store nothing
   const float K = (float)(N * a.D);
   float ssq = 0.f, acc_l = 0.f, acc_h = 0.f;
+  // unconditional loads (lanes e >= 2N sum a column they never use), so the
+  // unrolled iterations issue together instead of waiting one by one
+  const int eh = e < 2 * N ? e : 0;
+#pragma unroll 8
   for (int s = 0; s < nsplit; ++s) {
     const int64_t row = (int64_t)s * T + tk;
     ssq += a.part_ssq[row];
     acc_l += a.part[row * M + 2 * N + e];
-    if (e < 2 * N) acc_h += a.part[row * M + e];
+    acc_h += a.part[row * M + eh];
   }
   const float inv = 1.0f / sqrtf(ssq / K + a.norm_eps);
   const float mix_l = acc_l * inv, mix_h = acc_h * inv;

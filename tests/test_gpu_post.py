@@ -124,6 +124,34 @@ def test_post_bwd_parity(T, N, D, dtype, gates):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("N,D,dtype", [
+    (4, 4096, torch.bfloat16),   # 1100 tokens: LDS-pipelined kernels (D < 5120)
+    (4, 2048, torch.bfloat16),
+    (8, 2048, torch.bfloat16),   # 1100 tokens: wave-per-token backward (N > 4)
+    (6, 264, torch.float32),
+    (6, 100, torch.bfloat16),    # element-wise path
+    (8, 40, torch.float32),      # one-wave blocks: N * N + N = 72 sums > 64 threads
+])
+def test_post_small_and_large_forms_agree(N, D, dtype):
+    """Below 1024 tokens a block of waves shares each token; the same tokens
+    inside a 1100-token call go through the LDS-pipelined or wave-per-token
+    kernels.  Element-wise outputs (y, grad_x, grad_h_out) use one FMA order
+    and must match bit for bit; the D-long dot products are summed in another
+    order (fp32 tolerance)."""
+    T, Ts = 1100, 1000
+    print(f"[post small/large] N={N} D={D} {dtype}", flush=True)
+    x, h_res, h_out, h_post, gy = post_inputs(T, N, D, dtype, gates="randn", seed=5)
+    big = m.mhc_post(x, h_res, h_out, h_post)[:Ts]
+    small = m.mhc_post(x[:Ts], h_res[:Ts], h_out[:Ts], h_post[:Ts])
+    assert torch.equal(small, big)
+    gb = [g[:Ts] for g in m.mhc_post_backward(gy, x, h_res, h_out, h_post)]
+    gs = m.mhc_post_backward(gy[:Ts], x[:Ts], h_res[:Ts], h_out[:Ts], h_post[:Ts])
+    torch.cuda.synchronize()
+    assert torch.equal(gs[0], gb[0]) and torch.equal(gs[2], gb[2])
+    for a, b, name in ((gs[1], gb[1], "grad_h_res"), (gs[3], gb[3], "grad_h_post")):
+        assert_close(a, _np(b), 1e-5, 1e-5 * float(b.abs().max()), name)
+
+
 def test_post_shapes_bsnd():
     B, S, N, D = 2, 8, 4, 64
     x, h_res, h_out, h_post, gy = post_inputs(B * S, N, D, torch.bfloat16, gates="randn")
