@@ -17,6 +17,7 @@ _LIB_NAME = "libmhc_amd.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+PRE_BWD_COMPENSATED = 1  # mhc_pre_bwd_ex flag (include/mhc_amd.h)
 
 _c = ctypes
 _vp, _i32, _i64, _f32, _sz = _c.c_void_p, _c.c_int32, _c.c_int64, _c.c_float, _c.c_size_t
@@ -34,6 +35,9 @@ _SIGNATURES = {
     "mhc_pre_bwd_acc": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _f32, _f32, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                    _i64, _i32, _i32, _vp]),
+    "mhc_pre_bwd_ex": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _f32, _f32, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _c.c_uint32, _vp,
+                                  _sz, _i64, _i32, _i32, _vp]),
     "mhc_post_pre_fwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "mhc_post_pre_fwd": (_c.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
                                     _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,

@@ -36,7 +36,8 @@ class MhcPreClampSinkhornFn(torch.autograd.Function):
     x_scaled (4*N*D bytes per token): the backward recomputes x * inv_rms."""
 
     @staticmethod
-    def forward(ctx, x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times):
+    def forward(ctx, x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+                compensated=False):
         out = _pre_forward(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
                            iter_times, need_backward=True, want_x_scaled=False)
         ctx.save_for_backward(x, phi, alpha, base, out["inv_rms"], out["mixes"], out["pre"])
@@ -45,6 +46,7 @@ class MhcPreClampSinkhornFn(torch.autograd.Function):
         ctx.clamp_min = clamp_min
         ctx.clamp_max = clamp_max
         ctx.iter_times = iter_times
+        ctx.compensated = bool(compensated)
         return out["y"], out["post_out"], out["comb_frag"]
 
     @staticmethod
@@ -62,9 +64,9 @@ class MhcPreClampSinkhornFn(torch.autograd.Function):
             x, phi, alpha, base, inv_rms, None, mixes, None, pre,
             grad_y.contiguous(), grad_post_out.contiguous(), grad_comb_frag.contiguous(),
             norm_eps=ctx.norm_eps, hc_eps=ctx.hc_eps, clamp_min=ctx.clamp_min,
-            clamp_max=ctx.clamp_max, iter_times=ctx.iter_times)
-        # (x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
-        return gx, gphi, galpha, gbase, None, None, None, None, None
+            clamp_max=ctx.clamp_max, iter_times=ctx.iter_times, compensated=ctx.compensated)
+        # (x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times, compensated)
+        return gx, gphi, galpha, gbase, None, None, None, None, None, None
 
 
 def mhc_pre_clamp_sinkhorn_fn(
@@ -72,10 +74,14 @@ def mhc_pre_clamp_sinkhorn_fn(
     norm_eps=1e-6, hc_eps=1e-6,
     clamp_min=0.0, clamp_max=0.0,
     iter_times=20,
+    *,
+    compensated=False,
 ):
-    """Autograd-aware mhc_pre_clamp_sinkhorn. Returns (y, post_out, comb_frag)."""
+    """Autograd-aware mhc_pre_clamp_sinkhorn. Returns (y, post_out, comb_frag).
+    ``compensated`` (beyond the reference) selects the backward's compensated
+    T-reductions (see mhc_pre_clamp_sinkhorn_backward)."""
     return MhcPreClampSinkhornFn.apply(
-        x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+        x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times, compensated)
 
 
 class MhcPostPreClampSinkhornFn(torch.autograd.Function):
@@ -86,13 +92,14 @@ class MhcPostPreClampSinkhornFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
-                clamp_max, iter_times):
+                clamp_max, iter_times, compensated=False):
         x_next, out = mhc_post_pre_clamp_sinkhorn(
             x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
             iter_times, need_backward=True)
         ctx.save_for_backward(x, h_res, h_out, h_post, phi, alpha, base, x_next, out["inv_rms"],
                               out["mixes"], out["pre"])
         ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+        ctx.compensated = bool(compensated)
         return x_next, out["y"], out["post_out"], out["comb_frag"]
 
     @staticmethod
@@ -109,9 +116,9 @@ class MhcPostPreClampSinkhornFn(torch.autograd.Function):
         g, gphi, galpha, gbase = _pre_backward(
             x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
             grad_post_out.contiguous(), grad_comb_frag.contiguous(), norm_eps, hc_eps, clamp_min,
-            clamp_max, iter_times, grad_x_in=grad_x_next)
+            clamp_max, iter_times, grad_x_in=grad_x_next, compensated=ctx.compensated)
         gx, ghres, ghout, ghpost = mhc_post_backward(g, x, h_res, h_out, h_post)
-        return gx, ghres, ghout, ghpost, gphi, galpha, gbase, None, None, None, None, None
+        return gx, ghres, ghout, ghpost, gphi, galpha, gbase, None, None, None, None, None, None
 
 
 def mhc_post_pre_clamp_sinkhorn_fn(
@@ -119,9 +126,12 @@ def mhc_post_pre_clamp_sinkhorn_fn(
     norm_eps=1e-6, hc_eps=1e-6,
     clamp_min=0.0, clamp_max=0.0,
     iter_times=20,
+    *,
+    compensated=False,
 ):
     """Autograd-aware fused mhc_post + mhc_pre_clamp_sinkhorn.  Returns
-    (x_next, y, post_out, comb_frag)."""
+    (x_next, y, post_out, comb_frag); ``compensated`` as in
+    mhc_pre_clamp_sinkhorn_fn."""
     return MhcPostPreClampSinkhornFn.apply(
         x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
-        iter_times)
+        iter_times, compensated)

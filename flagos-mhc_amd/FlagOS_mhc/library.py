@@ -90,8 +90,9 @@ _post.register_autograd(_post_grad, setup_context=_post_setup)
 
 @torch.library.custom_op(f"{NAMESPACE}::mhc_pre_clamp_sinkhorn", mutates_args=())
 def _pre(x: Tensor, phi: Tensor, alpha: Tensor, base: Tensor, norm_eps: float, hc_eps: float,
-         clamp_min: float, clamp_max: float,
-         iter_times: int) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+         clamp_min: float, clamp_max: float, iter_times: int,
+         compensated: bool = False) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    # compensated only selects the backward's reductions
     out = _pre_forward(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
                        need_backward=True, want_x_scaled=False)
     return (out["y"], out["post_out"], out["comb_frag"], out["inv_rms"], out["mixes"], out["pre"])
@@ -106,7 +107,8 @@ def _pre_dims(x):
 
 
 @_pre.register_fake
-def _pre_fake(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times):
+def _pre_fake(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+              compensated=False):
     T, N, D = _pre_dims(x)
     M = N * (N + 2)
     f32 = dict(dtype=torch.float32)
@@ -119,16 +121,17 @@ def _pre_fake(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_
 def _pre_bwd(x: Tensor, phi: Tensor, alpha: Tensor, base: Tensor, inv_rms: Tensor, mixes: Tensor,
              pre: Tensor, grad_y: Tensor, grad_post_out: Tensor, grad_comb_frag: Tensor,
              norm_eps: float, hc_eps: float, clamp_min: float, clamp_max: float,
-             iter_times: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+             iter_times: int, compensated: bool = False) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     return tuple(mhc_pre_clamp_sinkhorn_backward(
         x, phi, alpha, base, inv_rms, None, mixes, None, pre, grad_y, grad_post_out,
         grad_comb_frag, norm_eps=norm_eps, hc_eps=hc_eps, clamp_min=clamp_min,
-        clamp_max=clamp_max, iter_times=iter_times))
+        clamp_max=clamp_max, iter_times=iter_times, compensated=compensated))
 
 
 @_pre_bwd.register_fake
 def _pre_bwd_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
-                  grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times):
+                  grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+                  compensated=False):
     f32 = dict(dtype=torch.float32)
     return (x.new_empty(x.shape), phi.new_empty(phi.shape, **f32), alpha.new_empty((3,), **f32),
             base.new_empty((base.numel(),), **f32))
@@ -138,26 +141,27 @@ def _pre_bwd_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_ou
 def _pre_bwd_acc(x: Tensor, phi: Tensor, alpha: Tensor, base: Tensor, inv_rms: Tensor,
                  mixes: Tensor, pre: Tensor, grad_y: Tensor, grad_post_out: Tensor,
                  grad_comb_frag: Tensor, grad_x_in: Tensor, norm_eps: float, hc_eps: float,
-                 clamp_min: float, clamp_max: float,
-                 iter_times: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+                 clamp_min: float, clamp_max: float, iter_times: int,
+                 compensated: bool = False) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     return tuple(_pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                                grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
-                               grad_x_in=grad_x_in))
+                               grad_x_in=grad_x_in, compensated=compensated))
 
 
 @_pre_bwd_acc.register_fake
 def _pre_bwd_acc_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
-                      grad_comb_frag, grad_x_in, norm_eps, hc_eps, clamp_min, clamp_max, iter_times):
+                      grad_comb_frag, grad_x_in, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+                      compensated=False):
     return _pre_bwd_fake(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                          grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
 
 
 def _pre_setup(ctx, inputs, output):
-    x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times = inputs
+    x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times, *opt = inputs
     _, _, _, inv_rms, mixes, pre = output
     ctx.mark_non_differentiable(inv_rms, mixes, pre)
     ctx.save_for_backward(x, phi, alpha, base, inv_rms, mixes, pre)
-    ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+    ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times, bool(opt[0]) if opt else False)
 
 
 def _pre_grad(ctx, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes, _g_pre):
@@ -166,7 +170,7 @@ def _pre_grad(ctx, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes, _g_p
         x, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(), grad_post_out.contiguous(),
         grad_comb_frag.contiguous(), *ctx.args)
     return (gx, gphi.to(phi.dtype), galpha.reshape(alpha.shape).to(alpha.dtype),
-            gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None)
+            gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None, None)
 
 
 _pre.register_autograd(_pre_grad, setup_context=_pre_setup)
@@ -177,7 +181,8 @@ _pre.register_autograd(_pre_grad, setup_context=_pre_setup)
 @torch.library.custom_op(f"{NAMESPACE}::mhc_post_pre_clamp_sinkhorn", mutates_args=())
 def _post_pre(x: Tensor, h_res: Tensor, h_out: Tensor, h_post: Tensor, phi: Tensor, alpha: Tensor,
               base: Tensor, norm_eps: float, hc_eps: float, clamp_min: float, clamp_max: float,
-              iter_times: int) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+              iter_times: int,
+              compensated: bool = False) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     x_next, out = mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post, phi, alpha, base, norm_eps,
                                               hc_eps, clamp_min, clamp_max, iter_times,
                                               need_backward=True)
@@ -187,17 +192,17 @@ def _post_pre(x: Tensor, h_res: Tensor, h_out: Tensor, h_post: Tensor, phi: Tens
 
 @_post_pre.register_fake
 def _post_pre_fake(x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
-                   clamp_max, iter_times):
+                   clamp_max, iter_times, compensated=False):
     return (torch.empty_like(x, memory_format=torch.contiguous_format),) + tuple(
         _pre_fake(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times))
 
 
 def _post_pre_setup(ctx, inputs, output):
-    x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times = inputs
+    x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times, *opt = inputs
     x_next, _, _, _, inv_rms, mixes, pre = output
     ctx.mark_non_differentiable(inv_rms, mixes, pre)
     ctx.save_for_backward(x, h_res, h_out, h_post, phi, alpha, base, x_next, inv_rms, mixes, pre)
-    ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+    ctx.args = (norm_eps, hc_eps, clamp_min, clamp_max, iter_times, bool(opt[0]) if opt else False)
 
 
 def _post_pre_grad(ctx, grad_x_next, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes,
@@ -208,7 +213,7 @@ def _post_pre_grad(ctx, grad_x_next, grad_y, grad_post_out, grad_comb_frag, _g_i
         grad_post_out.contiguous(), grad_comb_frag.contiguous(), grad_x_next.contiguous(), *ctx.args)
     gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward(g, x, h_res, h_out, h_post)
     return (gx, ghres, ghout, ghpost, gphi.to(phi.dtype), galpha.reshape(alpha.shape).to(alpha.dtype),
-            gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None)
+            gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None, None)
 
 
 _post_pre.register_autograd(_post_pre_grad, setup_context=_post_pre_setup)
@@ -222,20 +227,22 @@ def mhc_post_op(x, h_res, h_out, h_post):
 
 
 def mhc_pre_clamp_sinkhorn_op(x, phi, alpha, base, norm_eps=1e-6, hc_eps=1e-6, clamp_min=0.0,
-                              clamp_max=0.0, iter_times=20):
+                              clamp_max=0.0, iter_times=20, *, compensated=False):
     """``mhc_pre_clamp_sinkhorn`` through the registered op: (y, post_out,
-    comb_frag), differentiable in x, phi, alpha and base."""
+    comb_frag), differentiable in x, phi, alpha and base; ``compensated``
+    selects the backward's compensated T-reductions."""
     y, post_out, comb, _, _, _ = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn(
         x, phi, alpha, base, float(norm_eps), float(hc_eps), float(clamp_min), float(clamp_max),
-        int(iter_times))
+        int(iter_times), bool(compensated))
     return y, post_out, comb
 
 
 def mhc_post_pre_clamp_sinkhorn_op(x, h_res, h_out, h_post, phi, alpha, base, norm_eps=1e-6,
-                                   hc_eps=1e-6, clamp_min=0.0, clamp_max=0.0, iter_times=20):
+                                   hc_eps=1e-6, clamp_min=0.0, clamp_max=0.0, iter_times=20, *,
+                                   compensated=False):
     """The fused mhc_post + mhc_pre_clamp_sinkhorn through the registered op:
     (x_next, y, post_out, comb_frag), differentiable in every tensor input."""
     x_next, y, post_out, comb, _, _, _ = torch.ops.flagos_mhc.mhc_post_pre_clamp_sinkhorn(
         x, h_res, h_out, h_post, phi, alpha, base, float(norm_eps), float(hc_eps), float(clamp_min),
-        float(clamp_max), int(iter_times))
+        float(clamp_max), int(iter_times), bool(compensated))
     return x_next, y, post_out, comb

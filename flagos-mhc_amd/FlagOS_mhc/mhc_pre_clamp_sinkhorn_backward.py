@@ -16,6 +16,13 @@ is reduced in a fixed order, as are grad_alpha and grad_base, so the result
 is deterministic.  The reference's x_scaled and h_res_logits arguments are
 accepted and not needed (x * inv_rms and the logits are recomputed), so
 passing None is fine.
+
+``compensated=True`` (keyword, beyond the reference's signature) selects the
+compensated T-reductions of the production AscendC operator's deterministic
+mode, which the reference lists as not replicated (README.md:197-204):
+grad_phi from exact 16-token products added with Neumaier's compensation
+(``mhc_pre_bwd_ex`` with ``MHC_PRE_BWD_COMPENSATED``), grad_alpha / grad_base
+likewise; grad_x is unchanged.  It costs one more read of x.
 """
 
 from __future__ import annotations
@@ -44,20 +51,25 @@ def mhc_pre_clamp_sinkhorn_backward(
     clamp_min: float = 0.0,
     clamp_max: float = 0.0,
     iter_times: int = 20,
+    *,
+    compensated: bool = False,
 ):
     """Returns (grad_x shaped like x in x's dtype, grad_phi (M, N*D) fp32,
     grad_alpha (3,) fp32, grad_base (M,) fp32)
     (src/mhc_pre_clamp_sinkhorn_backward.py:1292-1391)."""
     del x_scaled, h_res_logits  # recomputed
     return _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
-                         grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times)
+                         grad_comb_frag, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+                         compensated=compensated)
 
 
 def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out, grad_comb_frag,
-                  norm_eps, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in=None):
+                  norm_eps, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in=None,
+                  compensated=False):
     """mhc_pre_clamp_sinkhorn_backward; with ``grad_x_in`` (shaped and typed
     like x) the returned grad_x is grad_x_in + dL/dx, accumulated inside the
-    kernel (``mhc_pre_bwd_acc``)."""
+    kernel (``mhc_pre_bwd_acc``); ``compensated`` selects the compensated
+    T-reductions (``mhc_pre_bwd_ex``)."""
     del norm_eps  # folded into inv_rms
     _lib.require_device("mhc_pre_clamp_sinkhorn_backward", x, phi, alpha, base, inv_rms, mixes,
                         pre, grad_y, grad_post_out, grad_comb_frag, grad_x_in)
@@ -104,11 +116,14 @@ def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_ou
               float(clamp_max), int(iter_times))
     tail = (grad_x.data_ptr(), grad_phi.data_ptr(), grad_alpha.data_ptr(), grad_base.data_ptr(),
             ws.data_ptr(), ws_bytes, T, N, D, _lib.stream_of(xf))
+    gin = None if grad_x_in is None else grad_x_in.reshape(T, N * D).to(xf.dtype).contiguous()
     with torch.cuda.device(dev):
-        if grad_x_in is None:
+        if compensated:
+            rc = lib.mhc_pre_bwd_ex(*common, _lib.ptr(gin), *tail[:4], _lib.PRE_BWD_COMPENSATED,
+                                    *tail[4:])
+        elif gin is None:
             rc = lib.mhc_pre_bwd(*common, *tail)
         else:
-            gin = grad_x_in.reshape(T, N * D).to(xf.dtype).contiguous()
             rc = lib.mhc_pre_bwd_acc(*common, gin.data_ptr(), *tail)
     _lib.check(rc, "mhc_pre_clamp_sinkhorn_backward")
     return grad_x.view(*shape), grad_phi.reshape(phi.shape), grad_alpha, grad_base

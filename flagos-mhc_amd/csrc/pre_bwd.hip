@@ -63,9 +63,28 @@ struct PreBwdSmallArgs {
   int64_t sink_stride;
   const float* gpre_part;  // [T][gpre_chunks][N] grad_pre partials, or null
   int gpre_chunks;
+  int comp;                // compensated (Neumaier) sums of the block partials
   int64_t T;
   int D;
 };
+
+// Neumaier's compensated step: s + c tracks the exact sum of the added values
+// (the error of each rounded addition is collected in c).
+__device__ __forceinline__ void neumaier_add(float& s, float& c, float v) {
+  const float t = s + v;
+  c += fabsf(s) >= fabsf(v) ? (s - t) + v : (v - t) + s;
+  s = t;
+}
+
+// Kahan's step (4 operations; c is the negated running error, so the sum is
+// s - c): used per 32-token tile in the grad_phi kernel, where the VALU is the
+// bound and each added tile is the sum of many products.
+__device__ __forceinline__ void kahan_add(float& s, float& c, float v) {
+  const float y = v - c;
+  const float t = s + y;
+  c = (t - s) - y;
+  s = t;
+}
 
 // grad_pre partials for small T, where a block per 16 tokens leaves most of
 // the chip idle and each wave streams (N + 1) * D elements serially: a block
@@ -272,8 +291,15 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
 
   for (int c = tid; c < C; c += kBwdThreads) {
     float s = 0.f;
+    if (a.comp) {
+      float cc = 0.f;
 #pragma unroll
-    for (int tt = 0; tt < kBwdTile; ++tt) s += contrib[tt][c];
+      for (int tt = 0; tt < kBwdTile; ++tt) neumaier_add(s, cc, contrib[tt][c]);
+      s += cc;
+    } else {
+#pragma unroll
+      for (int tt = 0; tt < kBwdTile; ++tt) s += contrib[tt][c];
+    }
     a.partial[(int64_t)blockIdx.x * C + c] = s;
   }
 }
@@ -1002,21 +1028,297 @@ __global__ void sum_splits_kernel(const float* __restrict__ part, float* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Compensated grad_phi (opt-in, MHC_PRE_BWD_COMPENSATED)
+//
+// grad_phi[m,k] = sum_t g[t,m] * x[t,k] with g = grad_mixes * inv_rms (the
+// same fp32 product the streaming kernels use).  g is split into three bf16
+// planes (exact to 2^-26) and x into 1 (bf16), 2 (fp16, exact) or 3 (fp32)
+// planes, so the products on v_mfma_f32_16x16x32_bf16 (32 tokens deep) are
+// exact and only their fp32 additions round.  Each wave owns 16 * VC columns
+// of one token split and adds every 32-token tile's MFMA result into a
+// (sum, compensation) pair per output (Kahan); the splits' sums are added
+// with Neumaier's compensation in a fixed order.  Columns of the lane's
+// 8-token x VC-column block are transposed in registers into the MFMA B
+// operand, as in the streaming kernels; no LDS.
+// ---------------------------------------------------------------------------
+constexpr int kCompPlanesG = 3;
+constexpr int kCompTile = 32;  // tokens per MFMA (K of 16x16x32)
+
+// g planes in MFMA A-operand order: [ceil(T/32)][MT][64 lanes][3 planes][8
+// tokens] bf16, lane = m % 16 + 16 * q holding tokens 32 * tile + 8q + j.
+template <int N>
+__global__ void comp_gplanes_kernel(const float* __restrict__ gm, const float* __restrict__ inv,
+                                    uint16_t* __restrict__ gpl, int64_t T, int64_t ntiles) {
+  using PD = PreDims<N>;
+  constexpr int M = PD::M, MT = PD::MT;
+  const int64_t n = ntiles * MT * kWave;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i % kWave);
+    const int64_t tm = i / kWave;
+    const int mt = (int)(tm % MT);
+    const int64_t tile = tm / MT;
+    const int m = 16 * mt + (lane & 15);
+    uint32_t pl[kCompPlanesG][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t t = kCompTile * tile + 8 * (lane >> 4) + j;
+      float v = (t < T && m < M) ? gm[t * M + m] * inv[t] : 0.f;
+#pragma unroll
+      for (int p = 0; p < kCompPlanesG; ++p) {
+        pl[p][j] = f32_to_bf16_bits(v);
+        v -= bf16_bits_to_f32(pl[p][j]);
+      }
+    }
+    u32x4* dst = reinterpret_cast<u32x4*>(gpl + i * (kCompPlanesG * 8));
+#pragma unroll
+    for (int p = 0; p < kCompPlanesG; ++p) {
+      u32x4 v;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v[w] = pl[p][2 * w] | (pl[p][2 * w + 1] << 16);
+      dst[p] = v;
+    }
+  }
+}
+
+struct GphiCompArgs {
+  const void* x;         // (T, K) activations
+  const uint16_t* gpl;   // g planes, layout above
+  float* part;           // [2][nsplit][M][K]: sums, then compensations
+  int64_t T, K, tps;     // tps: tokens per split, a multiple of kCompTile
+  int nsplit;
+};
+
+template <typename S> struct XPlanes { static constexpr int P = 3; };                     // fp32
+template <> struct XPlanes<bf16_t> { static constexpr int P = 1; };
+template <> struct XPlanes<f16_t> { static constexpr int P = 2; };
+
+// Raw bits of VC consecutive elements of `row` from column k (zeros past K or
+// when !ok), as NW = VC * sizeof(S) / 4 words (2-byte types two per word, low
+// half first).  Kept raw so that the loads of the next tile stay in flight
+// while the current one is multiplied.
+template <typename S, int VC> struct XRaw {
+  static constexpr int NW = VC * (int)sizeof(S) / 4;
+};
+
+template <typename S, int VC, bool VEC>
+__device__ __forceinline__ void load_raw(const S* row, int64_t k, int64_t K, bool ok, uint32_t* w) {
+  constexpr int NW = XRaw<S, VC>::NW;
+  if constexpr (VEC) {
+    // K % VC == 0 and 16-byte aligned rows: the group is wholly in or out
+    const bool in = ok && k < K;
+    if constexpr (NW == 2) {
+      const uint2 v = in ? *reinterpret_cast<const uint2*>(row + k) : uint2{0u, 0u};
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+      static_assert(NW % 4 == 0, "16-byte groups");
+#pragma unroll
+      for (int i = 0; i < NW / 4; ++i) {
+        const u32x4 v = in ? ld16(reinterpret_cast<const char*>(row + k) + 16 * i) : zero4();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
+      }
+    }
+  } else if constexpr (sizeof(S) == 2) {
+    const uint16_t* r16 = reinterpret_cast<const uint16_t*>(row);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const uint32_t lo = (ok && k + 2 * i < K) ? r16[k + 2 * i] : 0u;
+      const uint32_t hi = (ok && k + 2 * i + 1 < K) ? r16[k + 2 * i + 1] : 0u;
+      w[i] = lo | (hi << 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = (ok && k + i < K) ? __float_as_uint(row[k + i]) : 0u;
+  }
+}
+
+// bf16 planes of element i of a raw group
+template <typename S, int PX>
+__device__ __forceinline__ void raw_planes(const uint32_t* w, int i, uint32_t* pl) {
+  if constexpr (std::is_same<S, bf16_t>::value) {
+    pl[0] = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+  } else {
+    float v;
+    if constexpr (sizeof(S) == 4)
+      v = __uint_as_float(w[i]);
+    else
+      v = Store<S>::to_f32((uint16_t)((w[i >> 1] >> (16 * (i & 1))) & 0xffffu));
+#pragma unroll
+    for (int p = 0; p < PX; ++p) {
+      pl[p] = f32_to_bf16_bits(v);
+      if (p + 1 < PX) v -= bf16_bits_to_f32(pl[p]);
+    }
+  }
+}
+
+template <int N, typename S, int VC, bool VEC>
+__global__ __launch_bounds__(kWave) void pre_bwd_gphi_comp_kernel(GphiCompArgs a) {
+  using PD = PreDims<N>;
+  constexpr int M = PD::M, MT = PD::MT, PX = XPlanes<S>::P, PG = kCompPlanesG, NW = XRaw<S, VC>::NW;
+  const int lane = threadIdx.x, r = lane & 15, q = lane >> 4;
+  const S* __restrict__ x = static_cast<const S*>(a.x);
+  const int64_t T = a.T, K = a.K;
+  const int64_t kl = (int64_t)blockIdx.x * (16 * VC) + (int64_t)VC * r;  // lane's first column
+  const int64_t tb0 = (int64_t)blockIdx.y * a.tps;
+  const int64_t tb1 = tb0 + a.tps < T ? tb0 + a.tps : T;
+
+  floatx4 sum[MT][VC], cmp[MT][VC];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int c = 0; c < VC; ++c) sum[mt][c] = cmp[mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // operands of 32-token tiles: g planes (A) and this lane's x rows (tokens
+  // tb + 8q + e, columns kl .. kl + VC - 1), in NS slots loaded NS tiles
+  // ahead of the one being multiplied (two slots measured no faster and
+  // cost registers)
+  constexpr int TT = kCompTile, NS = 1;
+  uint32_t xw[NS][8][NW];
+  u32x4 ga[NS][MT][PG];
+  auto load_tile = [&](int64_t tb, int slot) {
+    const u32x4* gp = reinterpret_cast<const u32x4*>(a.gpl) + ((tb / TT) * MT * kWave + lane) * PG;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < PG; ++p) ga[slot][mt][p] = gp[mt * kWave * PG + p];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t t = tb + 8 * q + e;
+      const bool ok = t < T;
+      load_raw<S, VC, VEC>(x + (ok ? t : 0) * K, kl, K, ok, xw[slot][e]);
+    }
+  };
+  auto multiply = [&](const uint32_t (&cw)[8][NW], const u32x4 (&cg)[MT][PG]) {
+#pragma unroll
+    for (int c = 0; c < VC; ++c) {
+      u32x4 xb[PX];
+      if constexpr (std::is_same<S, bf16_t>::value) {
+        // column c of tokens (2w, 2w + 1) straight from the raw words
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t lo = cw[2 * w][c >> 1], hi = cw[2 * w + 1][c >> 1];
+          xb[0][w] = (c & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+      } else {
+        uint32_t pl[8][PX];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) raw_planes<S, PX>(cw[e], c, pl[e]);
+#pragma unroll
+        for (int p = 0; p < PX; ++p)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) xb[p][w] = pl[2 * w][p] | (pl[2 * w + 1][p] << 16);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        floatx4 tile = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pg = 0; pg < PG; ++pg)
+#pragma unroll
+          for (int px = 0; px < PX; ++px)
+            if (pg + px <= 3) tile = mfma16x16x32(as_bf16x8(cg[mt][pg]), as_bf16x8(xb[px]), tile);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float sv = sum[mt][c][v], cv = cmp[mt][c][v];
+          kahan_add(sv, cv, tile[v]);
+          sum[mt][c][v] = sv;
+          cmp[mt][c][v] = cv;
+        }
+      }
+    }
+  };
+  // tile tb + j * TT lives in slot j % NS; a slot is refilled (NS tiles
+  // ahead) right after its contents are copied out
+  auto step = [&](int64_t tb, int slot) {
+    uint32_t cw[8][NW];
+    u32x4 cg[MT][PG];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int i = 0; i < NW; ++i) cw[e][i] = xw[slot][e][i];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int p = 0; p < PG; ++p) cg[mt][p] = ga[slot][mt][p];
+    if (tb + NS * TT < tb1) load_tile(tb + NS * TT, slot);
+    multiply(cw, cg);
+  };
+
+#pragma unroll
+  for (int j = 0; j < NS; ++j)
+    if (tb0 + j * TT < tb1) load_tile(tb0 + j * TT, j);
+  for (int64_t tb = tb0; tb < tb1; tb += NS * TT) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+      if (tb + j * TT < tb1) step(tb + j * TT, j);
+  }
+
+  const int64_t MK = (int64_t)M * K;
+  float* ps = a.part + (int64_t)blockIdx.y * MK;
+  float* pc = a.part + ((int64_t)a.nsplit + blockIdx.y) * MK;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 16 * mt + 4 * q + v;
+      if (m >= M) continue;
+#pragma unroll
+      for (int c = 0; c < VC; ++c) {
+        if (kl + c >= K) continue;
+        ps[(int64_t)m * K + kl + c] = sum[mt][c][v];
+        pc[(int64_t)m * K + kl + c] = -cmp[mt][c][v];  // Kahan's c is the negated error
+      }
+    }
+}
+
+// out[i] = compensated sum over the splits of sums[j][i], plus their
+// compensations
+__global__ void sum_splits_comp_kernel(const float* __restrict__ part, float* __restrict__ out, int64_t n,
+                                       int nsplit) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f, c = 0.f;
+    for (int j = 0; j < nsplit; ++j) {
+      neumaier_add(s, c, part[(int64_t)j * n + i]);
+      c += part[((int64_t)nsplit + j) * n + i];
+    }
+    out[i] = s + c;
+  }
+}
+
 // One block per column c of partial (rows x C): out = sum over rows.
+// comp: each thread sums its rows with Neumaier's compensation, then the 256
+// (sum, compensation) pairs are added pairwise with the exact error of each
+// addition (TwoSum) carried into the compensation.
 __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ partial,
                                                        int64_t rows, int C,
                                                        float* __restrict__ out_alpha,
-                                                       float* __restrict__ out_base) {
-  __shared__ float red[256];
+                                                       float* __restrict__ out_base, int comp) {
+  __shared__ float red[256], redc[256];
   const int c = blockIdx.x;
-  float s = 0.f;
-  for (int64_t i = threadIdx.x; i < rows; i += 256) s += partial[i * C + c];
+  float s = 0.f, cc = 0.f;
+  if (comp) {
+    for (int64_t i = threadIdx.x; i < rows; i += 256) neumaier_add(s, cc, partial[i * C + c]);
+  } else {
+    for (int64_t i = threadIdx.x; i < rows; i += 256) s += partial[i * C + c];
+  }
   red[threadIdx.x] = s;
+  redc[threadIdx.x] = cc;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    if ((int)threadIdx.x < w) {
+      const float a0 = red[threadIdx.x], b0 = red[threadIdx.x + w];
+      const float t = a0 + b0;
+      if (comp) {
+        const float bb = t - a0;
+        redc[threadIdx.x] += redc[threadIdx.x + w] + ((a0 - (t - bb)) + (b0 - bb));
+      }
+      red[threadIdx.x] = t;
+    }
     __syncthreads();
   }
+  if (threadIdx.x == 0 && comp) red[0] += redc[0];
   if (threadIdx.x == 0) {
     if (c < 3)
       out_alpha[c] = red[0];
@@ -1031,7 +1333,7 @@ __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__
 struct BwdLayout {
   int M, L, C, P, MP, MP32, nsplit, chunks, DC, gpre_chunks;
   int64_t K, nblkA, tok_per_split, ntiles;
-  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink, off_gpre;
+  size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink, off_gpre, off_gpl;
   size_t off_gmP, off_gTw, off_coef, total;
 };
 
@@ -1098,6 +1400,8 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   b.gpre_chunks = (T >= kGpreSplitMinT && T < kGpreSplitMaxT) ? (int)((D + kGpreCols - 1) / kGpreCols) : 0;
   b.off_gpre = off;
   off += align256((size_t)T * b.gpre_chunks * N * 4);
+  b.off_gpl = off;  // compensated mode: g planes, 3 bf16 per (token, padded m)
+  off += align256((size_t)((T + kCompTile - 1) / kCompTile) * kCompTile * b.MP * kCompPlanesG * 2);
   b.total = off;
   return b;
 }
@@ -1150,17 +1454,63 @@ static unsigned reduce_grid(int64_t n) {
 static int sum_alpha_base(const BwdLayout& lay, const PreBwdSmallArgs& sa, float* grad_alpha,
                           float* grad_base, hipStream_t st) {
   hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
-                     lay.nblkA, lay.C, grad_alpha, grad_base);
+                     lay.nblkA, lay.C, grad_alpha, grad_base, sa.comp);
   return check_launch("pre_bwd_sum_rows");
 }
 
-static int reduce_tail(const BwdLayout& lay, const PreBwdSmallArgs& sa, const float* gphi_part,
-                       int nsplit, float* grad_phi, float* grad_alpha, float* grad_base,
-                       hipStream_t st) {
-  const int64_t n = (int64_t)lay.M * lay.K;
-  hipLaunchKernelGGL(sum_splits_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, gphi_part, grad_phi, n,
-                     nsplit);
-  int rc = check_launch("pre_bwd_sum_splits");
+// Compensated grad_phi: g planes, then the split MFMA sums, then their
+// compensated fixed-order sum.  Reuses the grad_phi partial region (the plain
+// partials written there before are not read in this mode).
+template <int N, typename S, int VC, bool VEC>
+static int launch_comp_gphi_v(const BwdLayout& lay, const GphiCompArgs& ga, int64_t ncw, hipStream_t st) {
+  hipLaunchKernelGGL((pre_bwd_gphi_comp_kernel<N, S, VC, VEC>), dim3((unsigned)ncw, (unsigned)ga.nsplit),
+                     dim3(kWave), 0, st, ga);
+  return check_launch("pre_bwd_gphi_comp");
+}
+
+template <int N, typename S>
+static int launch_comp_gphi(const BwdLayout& lay, const PreBwdSmallArgs& sa, float* gphi_part, uint16_t* gpl,
+                            float* grad_phi, hipStream_t st) {
+  constexpr int VC = N == 4 ? 8 : 4;  // columns per lane: accumulators stay within the VGPR budget
+  const int64_t T = sa.T, K = lay.K, ntiles = (T + kCompTile - 1) / kCompTile;
+  hipLaunchKernelGGL((comp_gplanes_kernel<N>), dim3(reduce_grid(ntiles * PreDims<N>::MT * kWave)), dim3(256), 0,
+                     st, sa.gm, sa.inv_rms, gpl, T, ntiles);
+  int rc = check_launch("pre_bwd_comp_gplanes");
+  if (rc) return rc;
+  // token splits: about 2048 waves, within the partial region (2 floats per
+  // output and split)
+  const int64_t ncw = (K + 16 * VC - 1) / (16 * VC);
+  int64_t ns = (2048 + ncw - 1) / ncw;
+  const int64_t cap = dma_max_splits(sa.D) / 2;
+  if (ns > cap) ns = cap;
+  if (ns > ntiles) ns = ntiles;
+  if (ns < 1) ns = 1;
+  const int64_t tps = (ntiles + ns - 1) / ns * kCompTile;
+  ns = (T + tps - 1) / tps;
+  GphiCompArgs ga{sa.x, gpl, gphi_part, T, K, tps, (int)ns};
+  const bool vec = K % VC == 0 && aligned16(sa.x) && (K * (int64_t)sizeof(S)) % 16 == 0;
+  rc = vec ? launch_comp_gphi_v<N, S, VC, true>(lay, ga, ncw, st) : launch_comp_gphi_v<N, S, VC, false>(lay, ga, ncw, st);
+  if (rc) return rc;
+  const int64_t n = (int64_t)lay.M * K;
+  hipLaunchKernelGGL(sum_splits_comp_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, gphi_part, grad_phi, n,
+                     (int)ns);
+  return check_launch("pre_bwd_sum_splits_comp");
+}
+
+// grad_phi from the split partials (plain) or the compensated kernels, then
+// grad_alpha / grad_base
+template <int N, typename S>
+static int reduce_tail(const BwdLayout& lay, const PreBwdSmallArgs& sa, float* gphi_part, int nsplit,
+                       uint16_t* gpl, float* grad_phi, float* grad_alpha, float* grad_base, hipStream_t st) {
+  int rc;
+  if (sa.comp) {
+    rc = launch_comp_gphi<N, S>(lay, sa, gphi_part, gpl, grad_phi, st);
+  } else {
+    const int64_t n = (int64_t)lay.M * lay.K;
+    hipLaunchKernelGGL(sum_splits_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, gphi_part, grad_phi, n,
+                       nsplit);
+    rc = check_launch("pre_bwd_sum_splits");
+  }
   if (rc) return rc;
   return sum_alpha_base(lay, sa, grad_alpha, grad_base, st);
 }
@@ -1171,9 +1521,9 @@ static bool dma_usable(int D) {
   return N == 4 && (int64_t)DmaCfg<N>::TT * N * D * 2 < ((int64_t)1 << 31);
 }
 
+// Launches the LDS-pipelined kernel; *nsplit receives its token-split count.
 template <int N, int P>
-static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* grad_phi,
-                      hipStream_t st) {
+static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* nsplit, hipStream_t st) {
   constexpr int DW = DmaCfg<N>::DW;
   const int D = sta.D;
   const int64_t ncb = (D + DW - 1) / DW;
@@ -1204,12 +1554,8 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, float* 
   else
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages, false>), dim3((unsigned)ncb, (unsigned)ns),
                        dim3(64 * N), 0, st, da);
-  int rc = check_launch("pre_bwd_dma");
-  if (rc) return rc;
-  const int64_t n = (int64_t)lay.M * lay.K;
-  hipLaunchKernelGGL(sum_splits_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, sta.gphi_part, grad_phi, n,
-                     (int)ns);
-  return check_launch("pre_bwd_sum_splits");
+  *nsplit = (int)ns;
+  return check_launch("pre_bwd_dma");
 }
 
 // grad_x += grad_x_in for the kernels without an accumulating form
@@ -1229,11 +1575,11 @@ static int add_into(void* out, const void* in, int64_t n, hipStream_t st) {
 template <int N, typename S>
 static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwdMainArgs& ma,
                           PreBwdStreamArgs sta, float* grad_phi, float* grad_alpha,
-                          float* grad_base, bool vec, const void* gin, hipStream_t st) {
+                          float* grad_base, bool vec, const void* gin, uint16_t* gpl, hipStream_t st) {
   const dim3 gA((unsigned)lay.nblkA), bA(kBwdThreads);
   const bool streaming = vec && std::is_same<S, bf16_t>::value;
   if (streaming) {
-    sa.gm = nullptr;
+    if (!sa.comp) sa.gm = nullptr;  // the compensated grad_phi reads fp32 grad_mixes
     sa.scale = nullptr;
   } else {
     sa.gmP = nullptr;
@@ -1259,9 +1605,10 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
   if constexpr (N == 4) {
     if (streaming && dma_usable<N>(sta.D)) {
       sta.gin = static_cast<const bf16_t*>(gin);  // accumulated inside the kernel
-      rc = lay.P == 1 ? launch_dma<N, 1>(lay, sta, grad_phi, st) : launch_dma<N, 2>(lay, sta, grad_phi, st);
+      int ns = 0;
+      rc = lay.P == 1 ? launch_dma<N, 1>(lay, sta, &ns, st) : launch_dma<N, 2>(lay, sta, &ns, st);
       if (rc) return rc;
-      return sum_alpha_base(lay, sa, grad_alpha, grad_base, st);
+      return reduce_tail<N, S>(lay, sa, sta.gphi_part, ns, gpl, grad_phi, grad_alpha, grad_base, st);
     }
   }
   const int64_t nx = sta.T * N * (int64_t)sta.D;
@@ -1269,7 +1616,7 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
     rc = lay.P == 1 ? launch_stream<N, 1>(lay, sta, st) : launch_stream<N, 2>(lay, sta, st);
     if (rc) return rc;
     if (gin && (rc = add_into<S>(sta.gx, gin, nx, st))) return rc;
-    return reduce_tail(lay, sa, sta.gphi_part, sta.nsplit, grad_phi, grad_alpha, grad_base, st);
+    return reduce_tail<N, S>(lay, sa, sta.gphi_part, sta.nsplit, gpl, grad_phi, grad_alpha, grad_base, st);
   }
   const dim3 gB((unsigned)lay.chunks, (unsigned)lay.nsplit), bB(256);
   if (vec)
@@ -1279,16 +1626,17 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
   rc = check_launch("pre_bwd_main");
   if (rc) return rc;
   if (gin && (rc = add_into<S>(ma.gx, gin, nx, st))) return rc;
-  return reduce_tail(lay, sa, ma.gphi_part, lay.nsplit, grad_phi, grad_alpha, grad_base, st);
+  return reduce_tail<N, S>(lay, sa, ma.gphi_part, lay.nsplit, gpl, grad_phi, grad_alpha, grad_base, st);
 }
 
 template <typename S>
 static int dispatch_pre_bwd(int N, const BwdLayout& lay, const PreBwdSmallArgs& sa,
                             const PreBwdMainArgs& ma, const PreBwdStreamArgs& sta, float* gphi,
-                            float* galpha, float* gbase, bool vec, const void* gin, hipStream_t st) {
+                            float* galpha, float* gbase, bool vec, const void* gin, uint16_t* gpl,
+                            hipStream_t st) {
   switch (N) {
-    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, st);
-    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, st);
+    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, gpl, st);
+    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, gpl, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
 }
@@ -1315,8 +1663,10 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
                          const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
                          int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
                          float* grad_alpha, float* grad_base, void* workspace, size_t workspace_bytes,
-                         int64_t T, int32_t N, int32_t D, void* stream) {
+                         int64_t T, int32_t N, int32_t D, uint32_t flags, void* stream) {
   clear_error();
+  if (flags & ~(uint32_t)MHC_PRE_BWD_COMPENSATED)
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: unknown flags 0x%x", (unsigned)flags);
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
   if (N != 4 && N != 8) return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
@@ -1368,6 +1718,7 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
   sa.sink_stride = lay.nblkA * kBwdTile * lay.L;
   sa.gpre_part = lay.gpre_chunks ? reinterpret_cast<float*>(ws + lay.off_gpre) : nullptr;
   sa.gpre_chunks = lay.gpre_chunks;
+  sa.comp = (flags & MHC_PRE_BWD_COMPENSATED) ? 1 : 0;
   sa.T = T;
   sa.D = D;
 
@@ -1404,13 +1755,14 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
 
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(grad_y) && aligned16(grad_x) &&
                    (!grad_x_in || aligned16(grad_x_in));
+  uint16_t* gpl = reinterpret_cast<uint16_t*>(ws + lay.off_gpl);
   switch (x_dtype) {
     case MHC_DTYPE_BF16:
-      return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, st);
+      return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st);
     case MHC_DTYPE_F16:
-      return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, st);
+      return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st);
     case MHC_DTYPE_F32:
-      return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, st);
+      return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: x dtype %d not supported", x_dtype);
 }
@@ -1425,7 +1777,17 @@ extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int3
                            void* stream) {
   return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                        grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, nullptr, grad_x, grad_phi,
-                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, stream);
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, 0u, stream);
+}
+
+// grad_x_in (nullable) must not overlap grad_x
+static int check_gin(const void* grad_x_in, const void* grad_x, int64_t T, int32_t N, int32_t D, int32_t x_dtype,
+                     const char* who) {
+  if (T <= 0 || !grad_x_in || !grad_x) return MHC_OK;
+  const uintptr_t bytes = (uintptr_t)T * (uintptr_t)N * (uintptr_t)D * (x_dtype == MHC_DTYPE_F32 ? 4u : 2u);
+  const uintptr_t in = (uintptr_t)grad_x_in, out = (uintptr_t)grad_x;
+  if (in < out + bytes && out < in + bytes) return set_error(MHC_ERR_INVALID, "%s: grad_x_in overlaps grad_x", who);
+  return MHC_OK;
 }
 
 extern "C" int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
@@ -1436,15 +1798,24 @@ extern "C" int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, 
                                void* grad_x, float* grad_phi, float* grad_alpha, float* grad_base,
                                void* workspace, size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
                                void* stream) {
-  if (T > 0) {
-    clear_error();
-    if (!grad_x_in) return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: null grad_x_in");
-    const uintptr_t bytes = (uintptr_t)T * (uintptr_t)N * (uintptr_t)D * (x_dtype == MHC_DTYPE_F32 ? 4u : 2u);
-    const uintptr_t in = (uintptr_t)grad_x_in, out = (uintptr_t)grad_x;
-    if (grad_x && in < out + bytes && out < in + bytes)
-      return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: grad_x_in overlaps grad_x");
-  }
+  clear_error();
+  if (T > 0 && !grad_x_in) return set_error(MHC_ERR_INVALID, "mhc_pre_bwd_acc: null grad_x_in");
+  if (int rc = check_gin(grad_x_in, grad_x, T, N, D, x_dtype, "mhc_pre_bwd_acc")) return rc;
   return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                        grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in, grad_x, grad_phi,
-                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, stream);
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, 0u, stream);
+}
+
+extern "C" int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                              const float* alpha, const float* base, const float* inv_rms, const float* mixes,
+                              const float* pre, const void* grad_y, const float* grad_post_out,
+                              const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
+                              int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
+                              float* grad_alpha, float* grad_base, uint32_t flags, void* workspace,
+                              size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream) {
+  clear_error();
+  if (int rc = check_gin(grad_x_in, grad_x, T, N, D, x_dtype, "mhc_pre_bwd_ex")) return rc;
+  return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
+                       grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in, grad_x, grad_phi,
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, flags, stream);
 }

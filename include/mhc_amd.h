@@ -132,6 +132,29 @@ int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi
                     void* stream);
 
 /*
+ * mhc_pre_bwd with options.  grad_x_in may be NULL (then as mhc_pre_bwd) or
+ * as in mhc_pre_bwd_acc.  flags:
+ *   MHC_PRE_BWD_COMPENSATED  compensated T-reductions for grad_phi,
+ *       grad_alpha and grad_base: the production AscendC operator's
+ *       deterministic Kahan-summation mode, which the reference lists as not
+ *       replicated (README.md:197-204, "Deterministic mode and Kahan
+ *       compensated summation in mhc_pre_clamp_sinkhorn_backward").  grad_phi
+ *       is formed from exact 16-token products (grad_mixes * inv_rms in three
+ *       bf16 planes, x in one to three) added with Neumaier's compensation;
+ *       grad_alpha / grad_base partials likewise.  Results stay deterministic;
+ *       grad_x is unchanged.  Costs one more read of x.
+ * Unknown flag bits are an error.  Workspace: mhc_pre_bwd_workspace_size.
+ */
+#define MHC_PRE_BWD_COMPENSATED 1u
+int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                   const float* alpha, const float* base, const float* inv_rms, const float* mixes,
+                   const float* pre, const void* grad_y, const float* grad_post_out,
+                   const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
+                   int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
+                   float* grad_alpha, float* grad_base, uint32_t flags, void* workspace,
+                   size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream);
+
+/*
  * Fused forward of mhc_post (layer l) and mhc_pre_clamp_sinkhorn (layer l+1).
  * No single counterpart in the reference: it replaces the device work of
  * mhc_post (src/mhc_post.py:296-352) followed by mhc_pre_clamp_sinkhorn on its

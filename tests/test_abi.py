@@ -92,6 +92,14 @@ def test_error_codes_without_device(lib):
     assert acc(gx, gx) == -1 and b"overlaps" in lib.mhc_last_error()
     assert acc(gin_overlap, gx) == -1 and b"overlaps" in lib.mhc_last_error()   # 16*4*64*2 bytes
     assert acc(gin_ok, gx) == -1 and b"workspace" in lib.mhc_last_error()       # passes to mhc_pre_bwd's checks
+    # pre backward with options: unknown flag bits, overlap, then mhc_pre_bwd's checks
+    ex = lambda gin, flags: lib.mhc_pre_bwd_ex(
+        dummy, 1, dummy, 1, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 1e-6, 0.0, 0.0, 20,
+        gin, gx, dummy, dummy, dummy, flags, dummy, 16, 16, 4, 64, None)
+    assert ex(None, 2) == -1 and b"flags" in lib.mhc_last_error()
+    assert ex(gin_overlap, 1) == -1 and b"overlaps" in lib.mhc_last_error()
+    assert ex(None, 1) == -1 and b"workspace" in lib.mhc_last_error()
+    assert ex(gin_ok, 0) == -1 and b"workspace" in lib.mhc_last_error()
     # fused post + pre forward: N outside {4, 8} and null pointers are rejected before any launch
     fused = lambda x, n: lib.mhc_post_pre_fwd(
         x, dummy, dummy, dummy, 1, dummy, 1, dummy, dummy, 1e-6, 1e-6, 0.0, 0.0, 20, dummy, dummy, dummy,

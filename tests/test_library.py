@@ -104,9 +104,36 @@ def test_opcheck():
     torch.library.opcheck(torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn.default, leaves + args)
     y, post_out, comb, inv, mixes, pre = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn(
         x.detach(), phi.detach(), alpha, base, *args)
-    torch.library.opcheck(torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward.default,
-                          (x.detach(), phi.detach(), alpha, base, inv, mixes, pre, noise,
-                           torch.randn_like(post_out), torch.randn_like(comb)) + args)
+    bwd_args = (x.detach(), phi.detach(), alpha, base, inv, mixes, pre, noise,
+                torch.randn_like(post_out), torch.randn_like(comb)) + args
+    torch.library.opcheck(torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward.default, bwd_args)
+    # the compensated reductions (trailing bool) through the same ops
+    torch.library.opcheck(torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward.default, bwd_args + (True,))
+    torch.library.opcheck(torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn.default, leaves + args + (True,))
+
+
+@pytest.mark.gpu
+def test_registered_op_compensated_gradients():
+    """compensated=True through the registered op's autograd gives the
+    functional compensated backward's gradients, bit for bit."""
+    T, N, D = 300, 4, 512
+    print(f"[op compensated] T={T} N={N} D={D}", flush=True)
+    x, phi, alpha, base, noise, _ = _layer_inputs(T, N, D, seed=5)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(6)
+    gpost = torch.randn(T, N, device=DEV, generator=g)
+    gcomb = torch.randn(T, N, N, device=DEV, generator=g)
+    leaves = [t.clone().requires_grad_(True) for t in (x, phi, alpha, base)]
+    y, p, c = L.mhc_pre_clamp_sinkhorn_op(*leaves, **KW, compensated=True)
+    ((y.float() * noise.float()).sum() + (p * gpost).sum() + (c * gcomb).sum()).backward()
+    out = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **KW)
+    gx, gphi, ga, gb = m.mhc_pre_clamp_sinkhorn_backward(
+        x, phi, alpha, base, out["inv_rms"], None, out["mixes"], None, out["pre"], noise, gpost, gcomb,
+        **KW, compensated=True)
+    torch.cuda.synchronize()
+    assert torch.equal(leaves[0].grad, gx)
+    assert torch.equal(leaves[1].grad, gphi.to(phi.dtype))
+    assert torch.equal(leaves[2].grad, ga) and torch.equal(leaves[3].grad, gb)
 
 
 @pytest.mark.gpu
