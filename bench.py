@@ -129,6 +129,62 @@ def time_events(fn, reps, stream):
     return statistics.median(ts), sum(ts) / len(ts)
 
 
+def small_t_latency(m, _pre_forward, dev, kw, token_counts=(1, 64, 1024), reps=50, per_graph=20):
+    """Per-operator latency at few tokens (N=4, D=7168): GPU time per call from
+    replays of a HIP graph holding `per_graph` back-to-back calls (no host work
+    and one graph launch per `per_graph` calls inside the timed region) and,
+    for comparison, wall time per eager call (Python + launch included)."""
+    import torch
+
+    N, D = 4, 7168
+    res = {}
+    for T in token_counts:
+        x, phi, alpha, base, noise, gup = make_inputs(T, N, D, dev, seed=1)
+        o = _pre_forward(x, phi, alpha, base, need_backward=True, want_x_scaled=False, **kw)
+        h_out = o["y"] + noise
+        pb = m.mhc_post_backward(gup, x, o["comb_frag"], h_out, o["post_out"])
+        ops = {
+            "pre_fwd": lambda: _pre_forward(x, phi, alpha, base, need_backward=True,
+                                            want_x_scaled=False, **kw),
+            "post_fwd": lambda: m.mhc_post(x, o["comb_frag"], h_out, o["post_out"]),
+            "post_bwd": lambda: m.mhc_post_backward(gup, x, o["comb_frag"], h_out, o["post_out"]),
+            "pre_bwd": lambda: m.mhc_pre_clamp_sinkhorn_backward(
+                x, phi, alpha, base, o["inv_rms"], None, o["mixes"], None, o["pre"], pb[2], pb[3],
+                pb[1], **kw),
+        }
+        entry = {}
+        for name, fn in ops.items():
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                fn()  # warm-up outside capture
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(per_graph):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(reps // 10):
+                graph.replay()
+            e.record()
+            torch.cuda.synchronize()
+            gpu_us = s.elapsed_time(e) / (reps // 10 * per_graph) * 1e3
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            torch.cuda.synchronize()
+            eager_us = (time.perf_counter() - t0) / reps * 1e6
+            entry[name] = {"graph_us": round(gpu_us, 1), "eager_us": round(eager_us, 1)}
+            del graph
+        res[str(T)] = entry
+    return res
+
+
 def cpu_baselines(N, D, sample_tokens, ref_tokens):
     """Oracle chain (numpy float64, one thread) and the package's torch *_ref
     chain (fp32, all host threads) on bounded token samples of the workload."""
@@ -206,6 +262,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=3072, help="oracle tokens for cpu_baseline")
     ap.add_argument("--ref-sample", type=int, default=8192, help="torch *_ref tokens on CPU")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-small-t", action="store_true", help="skip the few-token latency block")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run one step and a 1 GiB copy (for rocprofv3 --pmc), no timing")
     args = ap.parse_args()
@@ -337,6 +394,8 @@ def main():
         "post_pre_fused": post_pre,
         "device": torch.cuda.get_device_name(0),
     }
+    if not args.no_small_t:
+        result["small_t_latency"] = small_t_latency(m, _pre_forward, dev, kw)
     if not args.no_cpu:
         cb, rb = cpu_baselines(N, D, args.cpu_sample, args.ref_sample)
         result["cpu_baseline"] = cb

@@ -7,7 +7,7 @@
 //
 // Kernel A (pre_bwd_small_kernel), a block per 16 tokens:
 //   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token;
-//   for 4 < T < 16384 summed in fixed order from the partials of
+//   for T < 16384 summed in fixed order from the partials of
 //   pre_bwd_gpre_kernel, a block per (token, 2048 columns))
 //   Sinkhorn / softmax / clamp / sigmoid-head VJP, lane per matrix element
 //   -> grad_mixes (T,M) and scale[t] = -inv^2 * <grad_mixes, mixes> / (N*D)
@@ -1339,13 +1339,13 @@ struct BwdLayout {
 
 // Token splits of the grad_phi partials: kMaxSplits for the split kernels,
 // more for the LDS-pipelined kernel when D has few 128-column blocks.
-// Between these token counts grad_pre comes from the split kernel: below
-// kGpreSplitMaxT kernel A's grid (a block per 16 tokens) leaves the chip
-// partly idle (measured on MI355X at D = 7168: T = 64 113 -> 52 us, T = 4096
-// 214 -> 170 us for the whole backward, even at 16384, 3% slower at 65536);
-// up to 4 tokens a wave per token streams them in parallel and the extra
-// launch costs more than it saves.
-constexpr int64_t kGpreSplitMinT = 5, kGpreSplitMaxT = 16384;
+// Below kGpreSplitMaxT tokens grad_pre comes from the split kernel: kernel
+// A's grid (a block per 16 tokens) leaves the chip partly idle (measured on
+// MI355X at D = 7168, eager calls: T = 64 113 -> 52 us, T = 4096 214 -> 170
+// us for the whole backward; even at 16384, 3% slower at 65536).  At T <= 4
+// the GPU time still drops (28.0 -> 24.9 us from graph replays) while an
+// eager call pays about 2 us more host time for the extra launch.
+constexpr int64_t kGpreSplitMinT = 1, kGpreSplitMaxT = 16384;
 
 static int64_t dma_max_splits(int D) {
   const int64_t ncb = (D + DmaCfg<4>::DW - 1) / DmaCfg<4>::DW;

@@ -164,8 +164,8 @@ BWD_CASES = [
     (17, 4, 40000, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     # few column blocks: many more token splits of the grad_phi partials
     (4000, 4, 256, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
-    # T <= 4 and T >= 16384 take grad_pre from a wave per token, the others
-    # from the split (token, 2048-column) partials
+    # T >= 16384 takes grad_pre from a wave per token, smaller T from the
+    # split (token, 2048-column) partials
     (3, 4, 7168, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (4, 8, 100, torch.float32, torch.float32, "baseline", 10.0, 20),
     (5, 4, 4100, torch.float16, torch.float16, "baseline", 10.0, 20),
