@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+
+#include <atomic>
 #include <stdint.h>
 #include <stdio.h>
 
@@ -15,6 +17,31 @@ int set_error(int code, const char* fmt, ...);
 void clear_error();
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Compute units of the current device, queried once per device (safe to call
+// from several host threads; a failed query reads as 256, the MI355X count).
+inline int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int cus = cache[dev].load(std::memory_order_relaxed);
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// Token counts above this are refused: several grids put one block (or one
+// per 16 tokens) in a 32-bit grid dimension, which must not wrap.
+constexpr int64_t kMaxTokens = 2147483647;
+
+inline int check_tokens(int64_t T, const char* who) {
+  if (T > kMaxTokens)
+    return set_error(MHC_ERR_UNSUPPORTED, "%s: T=%lld above the supported %lld tokens", who, (long long)T,
+                     (long long)kMaxTokens);
+  return MHC_OK;
+}
 
 // Reports a failed launch (bad configuration, missing code object, ...).
 inline int check_launch(const char* what) {

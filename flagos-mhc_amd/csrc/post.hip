@@ -567,17 +567,11 @@ __global__ __launch_bounds__(256) void post_bwd_dma_kernel(
 // bound the residency), at most one wave per token.
 template <typename K>
 static int64_t post_dma_grid(K kernel, int64_t T) {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (!cus[dev] && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-                    cus[dev] <= 0))
-    cus[dev] = 256;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWave * kPostWavesPerBlock, 0) != hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
-  const int64_t grid = (int64_t)cus[dev] * per_cu;
+  const int64_t grid = (int64_t)device_cu_count() * per_cu;
   const int64_t max_grid = (T + kPostWavesPerBlock - 1) / kPostWavesPerBlock;
   return grid < max_grid ? grid : max_grid;
 }
@@ -686,6 +680,7 @@ extern "C" int mhc_post_fwd(const void* x, const float* h_res, const void* h_out
                             int32_t dtype, void* stream) {
   clear_error();
   if (T < 0 || D <= 0) return set_error(MHC_ERR_INVALID, "mhc_post_fwd: bad shape T=%lld D=%d", (long long)T, D);
+  if (int rc = check_tokens(T, "mhc_post_fwd")) return rc;
   if (T == 0) return MHC_OK;
   if (!x || !h_res || !h_out || !h_post || !y) return set_error(MHC_ERR_INVALID, "mhc_post_fwd: null pointer");
   hipStream_t st = (hipStream_t)stream;
@@ -703,6 +698,7 @@ extern "C" int mhc_post_bwd(const void* grad_y, const void* x, const float* h_re
                             int32_t N, int32_t D, int32_t dtype, void* stream) {
   clear_error();
   if (T < 0 || D <= 0) return set_error(MHC_ERR_INVALID, "mhc_post_bwd: bad shape T=%lld D=%d", (long long)T, D);
+  if (int rc = check_tokens(T, "mhc_post_bwd")) return rc;
   if (T == 0) return MHC_OK;
   if (!grad_y || !x || !h_res || !h_out || !h_post || !grad_x || !grad_h_res || !grad_h_out || !grad_h_post)
     return set_error(MHC_ERR_INVALID, "mhc_post_bwd: null pointer");

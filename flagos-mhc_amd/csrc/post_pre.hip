@@ -489,16 +489,6 @@ bool post_pre_usable(const void* x, const void* h_out, const void* phi, const vo
          aligned16(x_next) && aligned16(y);
 }
 
-int device_cu_count() {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (!cus[dev] && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-                    cus[dev] <= 0))
-    cus[dev] = 256;
-  return cus[dev];
-}
-
 }  // namespace
 }  // namespace mhc
 
@@ -517,6 +507,7 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
   clear_error();
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
+  if (int rc = check_tokens(T, "mhc_post_pre_fwd")) return rc;
   if (N != 4 && N != 8)
     return set_error(MHC_ERR_UNSUPPORTED, "mhc_post_pre_fwd: N=%d not supported (4, 8)", N);
   if (T == 0) return MHC_OK;

@@ -1406,37 +1406,22 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   return b;
 }
 
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cache[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    cache[dev] = cus;
-  }
-  return cache[dev];
-}
-
 template <int N, int P>
 static int stream_blocks_per_cu() {
-  static int cache = 0;
-  if (!cache) {
-    int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pre_bwd_stream_kernel<N, P>, 64 * N, 0) != hipSuccess || nb <= 0)
-      nb = 1;
-    cache = nb;
-  }
-  return cache;
+  static std::atomic<int> cache{0};
+  int nb = cache.load(std::memory_order_relaxed);
+  if (nb > 0) return nb;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, pre_bwd_stream_kernel<N, P>, 64 * N, 0) != hipSuccess || nb <= 0)
+    nb = 1;
+  cache.store(nb, std::memory_order_relaxed);
+  return nb;
 }
 
 template <int N, int P>
 static int launch_stream(const BwdLayout& lay, PreBwdStreamArgs& sta, hipStream_t st) {
   constexpr int DW = StreamCfg<N>::DW;
   const int chunks = (int)((lay.K / N + DW - 1) / DW);
-  int64_t ns = (int64_t)device_cus() * stream_blocks_per_cu<N, P>() / chunks;
+  int64_t ns = (int64_t)device_cu_count() * stream_blocks_per_cu<N, P>() / chunks;
   if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns > lay.ntiles) ns = lay.ntiles;
   if (ns < 1) ns = 1;
@@ -1529,7 +1514,7 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* ns
   const int64_t ncb = (D + DW - 1) / DW;
   // one block per CU (the ring fills the LDS); as many token splits as fit
   // next to the column blocks in one wave of blocks
-  int64_t ns = device_cus() / ncb;
+  int64_t ns = device_cu_count() / ncb;
   if (ns > dma_max_splits(D)) ns = dma_max_splits(D);
   if (ns > lay.ntiles) ns = lay.ntiles;
   if (ns < 1) ns = 1;
@@ -1669,6 +1654,7 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: unknown flags 0x%x", (unsigned)flags);
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
+  if (int rc = check_tokens(T, "mhc_pre_bwd")) return rc;
   if (N != 4 && N != 8) return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
   if (!phi || !alpha || !base || !grad_phi || !grad_alpha || !grad_base)
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: null pointer");

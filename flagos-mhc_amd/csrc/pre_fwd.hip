@@ -796,12 +796,6 @@ static bool fwd_dma_usable(const PreFwdArgs& a, int N, bool bf16x, bool vec) {
 
 template <int N>
 static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (!cus[dev] && (hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-                    cus[dev] <= 0))
-    cus[dev] = 256;
   const int64_t ntiles = (a.T + kFwdTile - 1) / kFwdTile;
   const FwdSplitPlan plan = fwd_split_plan(a.T, N, a.D);
   if (plan.nsplit >= 2 && workspace && workspace_bytes >= kPreFwdWsBase + plan.bytes) {
@@ -831,7 +825,8 @@ static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_by
       hipLaunchKernelGGL((pre_fwd_y_kernel<N, false>), gy, dim3(kFwdThreads), 0, st, a);
     return check_launch("pre_fwd_y");
   }
-  const int64_t grid = ntiles < cus[dev] ? ntiles : cus[dev];  // one block per CU (LDS ring)
+  const int64_t cus = device_cu_count();
+  const int64_t grid = ntiles < cus ? ntiles : cus;  // one block per CU (LDS ring)
   if (a.x_scaled)
     hipLaunchKernelGGL((pre_fwd_dma_kernel<N, true, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   else
@@ -891,6 +886,7 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   clear_error();
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_fwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
+  if (int rc = check_tokens(T, "mhc_pre_fwd")) return rc;
   if (N != 4 && N != 8) return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_fwd: N=%d not supported (4, 8)", N);
   if (T == 0) return MHC_OK;
   if (!x || !phi || !alpha || !base || !y || !post_out || !comb_frag)

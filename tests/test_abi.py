@@ -81,6 +81,18 @@ def test_error_codes_without_device(lib):
                          dummy, 1e-6, 0.0, 0.0, 20, dummy, dummy, dummy, dummy, dummy, 16,
                          16, 4, 64, None)
     assert rc == -1 and b"workspace" in lib.mhc_last_error()
+    # token counts beyond 32-bit grids are refused, not wrapped
+    big = 1 << 32
+    rc = lib.mhc_post_fwd(dummy, dummy, dummy, dummy, dummy, big, 4, 64, 1, None)
+    assert rc == -2 and b"above the supported" in lib.mhc_last_error()
+    rc = lib.mhc_post_bwd(dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, big, 4, 64, 1, None)
+    assert rc == -2 and b"above the supported" in lib.mhc_last_error()
+    rc = lib.mhc_pre_fwd(dummy, 1, dummy, 1, dummy, dummy, 1e-6, 1e-6, 0.0, 0.0, 20,
+                         dummy, dummy, dummy, None, None, None, None, None, dummy, 1 << 20, big, 4, 64, None)
+    assert rc == -2 and b"above the supported" in lib.mhc_last_error()
+    rc = lib.mhc_pre_bwd(dummy, 1, dummy, 1, dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                         dummy, 1e-6, 0.0, 0.0, 20, dummy, dummy, dummy, dummy, dummy, 16, big, 4, 64, None)
+    assert rc == -2 and b"above the supported" in lib.mhc_last_error()
     # T == 0 is a no-op for the forward ops
     assert lib.mhc_post_fwd(dummy, dummy, dummy, dummy, dummy, 0, 4, 64, 1, None) == 0
     # accumulating pre backward: grad_x_in is required and must not overlap grad_x
