@@ -13,9 +13,10 @@
 // (see kPostStreamMinT / kPostBlockMinD): a block of waves per token (the
 // waves split D), a wave per token (backward, N > 4), and for N = 4 bf16 an
 // LDS-pipelined wave per token.  In each, the N*N + N gates are uniform
-// scalar loads, every lane streams 16-byte vectors of each of the N rows,
-// accumulates in fp32 and stores with round-to-nearest-even (streaming
-// stores: outputs are not re-read here).  The backward's N*N + N dot products
+// scalar loads, every lane streams 16-byte vectors of each of the N rows
+// (non-temporal loads: each input is read once), accumulates in fp32 and
+// stores with round-to-nearest-even (streaming stores: outputs are not
+// re-read here).  The backward's N*N + N dot products
 // are reduced across the wave (and the block) once per token and written by
 // plain stores (no atomics), so results are deterministic.
 #include <type_traits>
@@ -59,10 +60,10 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
     for (int d = lane * V; d < D; d += kWave * V) {
       float gv[N][V], xv[N][V], hv[V];
 #pragma unroll
-      for (int i = 0; i < N; ++i) Store<S>::unpack(ld16(gy + xrow + (int64_t)i * D + d), gv[i]);
+      for (int i = 0; i < N; ++i) Store<S>::unpack(ld16nt(gy + xrow + (int64_t)i * D + d), gv[i]);
 #pragma unroll
-      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16(x + xrow + (int64_t)j * D + d), xv[j]);
-      Store<S>::unpack(ld16(h_out + hrow + d), hv);
+      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16nt(x + xrow + (int64_t)j * D + d), xv[j]);
+      Store<S>::unpack(ld16nt(h_out + hrow + d), hv);
 #pragma unroll
       for (int j = 0; j < N; ++j) {
         float o[V];
@@ -135,24 +136,26 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Block forms: a block of W = min(8, chunks) waves per token, the waves
-// splitting D into 64 * V-column chunks (wave w takes chunks w, w + W, ...),
-// so all of a token's loads are in flight at once.  With a wave per token a
-// call with few tokens runs a handful of waves, each streaming its whole
-// token serially (T = 1, N = 4, D = 7168: 11 us forward, 19 us backward,
-// against 3.3 and 6.4 us here).  At large T the block forms also beat the
-// LDS-pipelined kernels below for D >= 5120 (c5 width: backward 2.30 against
-// 2.50 ms, forward 1.58 against 1.60 ms on one MI355X): with one 8-wave block
-// per CU only 256 tokens are in flight, each read as a few contiguous
-// streams.  Every output element of the forward, grad_x and grad_h_out uses
+// Block forms: a block of W = min(16 forward / 8 backward, chunks) waves per
+// token, the waves splitting D into 64 * V-column chunks (wave w takes chunks
+// w, w + W, ...), so all of a token's loads are in flight at once.  With a
+// wave per token a call with few tokens runs a handful of waves, each
+// streaming its whole token serially (T = 1, N = 4, D = 7168: 11 us forward,
+// 19 us backward, against 3.3 and 6.4 us here).  At large T the block forms
+// also beat the LDS-pipelined kernels below for D >= 5120 (c5 width on one
+// MI355X: backward 2.23 against 2.50 ms, forward 1.48 against 1.60 ms): only
+// a few tokens per CU are in flight, each read as a few long contiguous
+// streams.  Inputs are read once, so loads are non-temporal (measured 3-7%
+// faster than default loads here).  Every output element of the forward, grad_x and grad_h_out uses
 // the FMA order of the other kernels (bit-identical results); the backward's
 // N * N + N dot products are summed per lane over its chunks, across the wave
 // (wave_sum), then over the waves in order through LDS (no atomics).
 // ---------------------------------------------------------------------------
-constexpr int kPostBlockWaves = 8;
+constexpr int kPostBlockWaves = 8;     // backward: 132 VGPRs at N = 4 allow 8 waves
+constexpr int kPostFwdBlockWaves = 16;  // forward: 68 VGPRs
 
 template <int N, typename S, bool VECTOR>
-__global__ __launch_bounds__(kWave * kPostBlockWaves) void post_fwd_block_kernel(
+__global__ __launch_bounds__(kWave * kPostFwdBlockWaves) void post_fwd_block_kernel(
     const S* __restrict__ x, const float* __restrict__ h_res, const S* __restrict__ h_out,
     const float* __restrict__ h_post, S* __restrict__ y, int D) {
   constexpr int V = VECTOR ? Store<S>::VEC : 1, CW = kWave * V;
@@ -170,8 +173,8 @@ __global__ __launch_bounds__(kWave * kPostBlockWaves) void post_fwd_block_kernel
     float xv[N][V], hv[V];
     if constexpr (VECTOR) {
 #pragma unroll
-      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16(x + xrow + (int64_t)j * D + d), xv[j]);
-      Store<S>::unpack(ld16(h_out + hrow + d), hv);
+      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16nt(x + xrow + (int64_t)j * D + d), xv[j]);
+      Store<S>::unpack(ld16nt(h_out + hrow + d), hv);
     } else {
 #pragma unroll
       for (int j = 0; j < N; ++j) xv[j][0] = load_elem(x, xrow + (int64_t)j * D + d);
@@ -221,10 +224,10 @@ __global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel
     float gv[N][V], xv[N][V], hv[V];
     if constexpr (VECTOR) {
 #pragma unroll
-      for (int i = 0; i < N; ++i) Store<S>::unpack(ld16(gy + xrow + (int64_t)i * D + d), gv[i]);
+      for (int i = 0; i < N; ++i) Store<S>::unpack(ld16nt(gy + xrow + (int64_t)i * D + d), gv[i]);
 #pragma unroll
-      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16(x + xrow + (int64_t)j * D + d), xv[j]);
-      Store<S>::unpack(ld16(h_out + hrow + d), hv);
+      for (int j = 0; j < N; ++j) Store<S>::unpack(ld16nt(x + xrow + (int64_t)j * D + d), xv[j]);
+      Store<S>::unpack(ld16nt(h_out + hrow + d), hv);
     } else {
 #pragma unroll
       for (int i = 0; i < N; ++i) gv[i][0] = load_elem(gy, xrow + (int64_t)i * D + d);
@@ -290,10 +293,10 @@ __global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel
   }
 }
 
-// Waves per block: one per 64 * V-column chunk, at most kPostBlockWaves.
-static inline int post_block_waves(int D, int V) {
+// Waves per block: one per 64 * V-column chunk, at most `cap`.
+static inline int post_block_waves(int D, int V, int cap) {
   const int chunks = (D + kWave * V - 1) / (kWave * V);
-  return chunks < kPostBlockWaves ? chunks : kPostBlockWaves;
+  return chunks < cap ? chunks : cap;
 }
 
 // Kernel choice (measured on MI355X): the LDS-pipelined kernels (N = 4 bf16)
@@ -592,7 +595,7 @@ static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
       return check_launch("post_fwd_dma");
     }
   }
-  const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1));
+  const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1, kPostFwdBlockWaves));
   if (vec)
     hipLaunchKernelGGL((post_fwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)x, h_res,
                        (const S*)h_out, h_post, (S*)y, D);
@@ -615,7 +618,7 @@ static int launch_post_bwd(const void* gy, const void* x, const float* h_res, co
     if (vec && T >= kPostStreamMinT && D < kPostBlockMinD) block_form = false;  // LDS-pipelined kernel
   }
   if (block_form) {
-    const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1));
+    const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1, kPostBlockWaves));
     if (vec)
       hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
                          h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D);
