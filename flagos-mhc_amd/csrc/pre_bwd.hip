@@ -339,13 +339,13 @@ __device__ __forceinline__ void copy8_to_lds(const S* src, int64_t lim, bool ok,
   typedef typename Raw<S>::type R;
   if constexpr (VEC) {
     if constexpr (sizeof(S) == 2) {
-      const u32x4 v = (ok && lim >= 8) ? ld16(src) : zero4();
+      const u32x4 v = (ok && lim >= 8) ? ld16nt(src) : zero4();
       st16(dst, v);
     } else {
       u32x4 v0 = zero4(), v1 = zero4();
       if (ok && lim >= 8) {
-        v0 = ld16(src);
-        v1 = ld16(src + 4);
+        v0 = ld16nt(src);
+        v1 = ld16nt(src + 4);
       }
       st16(dst, v0);
       st16(dst + 4, v1);
@@ -1115,7 +1115,7 @@ __device__ __forceinline__ void load_raw(const S* row, int64_t k, int64_t K, boo
       static_assert(NW % 4 == 0, "16-byte groups");
 #pragma unroll
       for (int i = 0; i < NW / 4; ++i) {
-        const u32x4 v = in ? ld16(reinterpret_cast<const char*>(row + k) + 16 * i) : zero4();
+        const u32x4 v = in ? ld16nt(reinterpret_cast<const char*>(row + k) + 16 * i) : zero4();
 #pragma unroll
         for (int j = 0; j < 4; ++j) w[4 * i + j] = v[j];
       }
