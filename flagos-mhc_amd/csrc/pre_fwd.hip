@@ -299,23 +299,23 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_kernel(PreFwdArgs a) {
 // LDS-pipelined form: N = 4 or 8, bf16 x and phi (phi used in place),
 // D % 8 == 0, 16-byte aligned rows.
 //
-// A persistent block per CU walks its 64-token tiles; every tile is two
-// streams of stages through one ring of S stage slots in LDS, filled by
+// A persistent block per CU walks its 64-token tiles; every tile is a stream
+// of contraction stages through one ring of S stage slots in LDS, filled by
 // direct-to-LDS loads issued S-1 stages ahead (no registers held by loads
-// in flight):
-//   contraction stages (128 columns of K each): x[64 tokens][128] (16 KB)
-//     and phi[32 rows][128] (8 KB, rows >= M zero).  Wave w multiplies row
-//     block w (tokens 16w..16w+15) by all of phi: no cross-wave reduction.
-//   y stages (4 tokens x 512 columns of d): x[4][4 streams][512] (16 KB);
-//     wave w forms y of token w, lane l its 8 columns 8l.. locally
-//     (y = sum_n pre[n] * x[n]), so a y store moves 1 KB of one row.
-// A contraction load instruction moves 4 rows x 256 contiguous bytes, a y
-// load one row x 1 KB.  In a contraction slot a row is 256 bytes with its
-// 16-byte chunks XOR-swizzled
-// by (row & 15), so the MFMA operand reads (16 rows, one chunk each) hit 16
-// different chunk positions: conflict-free.  After the last contraction
-// stage the wave's accumulators give mixes; heads and Sinkhorn run as in
-// the generic kernel while the first y stages are already loading.
+// in flight): 128 columns of K each, x[64 tokens][128] (16 KB) and
+// phi[32 rows][128] (8 KB, rows >= M zero).  Wave w multiplies row block w
+// (tokens 16w..16w+15) by all of phi: no cross-wave reduction.  A load
+// instruction moves 4 rows x 256 contiguous bytes.  In a slot a row is 256
+// bytes with its 16-byte chunks XOR-swizzled by (row & 15), so the MFMA
+// operand reads (16 rows, one chunk each) hit 16 different chunk positions:
+// conflict-free.  After the last contraction stage the wave's accumulators
+// give mixes; heads and Sinkhorn run as in the generic kernel while the next
+// tile's first stages are already loading, and pre / inv_rms go to the
+// workspace for the y kernel (pre_fwd_y_kernel, a block per token), which
+// reads x a second time.  The y pass used to run as stages of this kernel
+// (4 tokens x 512 columns each); as its own block-per-token kernel it moves
+// its 4.7 GB at c5 in 0.78 ms instead of sharing the ring (pre forward
+// 1.57 -> 1.44 ms on one MI355X).
 // ---------------------------------------------------------------------------
 constexpr int kFwdDmaStages = 4;
 
@@ -325,50 +325,44 @@ __device__ __forceinline__ u32x4 pre_sh4(uint32_t a) {
   asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
   return v;
 }
-// Slot geometry per N: a contraction slot holds 16 units of x and 4*MT of phi
-// (MT 16-row m blocks), a y slot 4 tokens x N streams; 1 KB units.
+// Slot geometry per N: 16 units of x and 4*MT of phi (MT 16-row m blocks);
+// 1 KB units.
 template <int N> struct FwdDmaCfg {
   static constexpr int MT = PreDims<N>::MT;
-  static constexpr int CU = 16 + 4 * MT;              // contraction units
-  static constexpr int YU = 4 * N;                    // y units
-  static constexpr int UNITS = CU > YU ? CU : YU;
+  static constexpr int UNITS = 16 + 4 * MT;
   static constexpr int S = N == 4 ? kFwdDmaStages : 3;  // slots (LDS: S * UNITS KB + mixes)
 };
 
 // SPLIT: block (tile, s) runs contraction stages [s * split_stages, ..) of
 // one tile and writes its partial sums; heads and y run in two more kernels.
-template <int N, bool XS, bool SPLIT>
+// Otherwise a persistent block runs all stages of its tiles and the heads.
+template <int N, bool SPLIT>
 __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) {
   using C = FwdDmaCfg<N>;
   constexpr int M = PreDims<N>::M, MT = C::MT, L = N * N, TT = kFwdTile, S = C::S, UNITS = C::UNITS;
   constexpr int CW = 128;                  // K columns per contraction stage
-  constexpr int YW = 512;                  // d columns per y stage
-  constexpr int CI = 4 + MT;               // loads per wave and contraction stage
-  constexpr int YI = N;                    // loads per wave and y stage
-  constexpr int YST = XS ? 1 + 2 * N : 1;  // buffer stores per lane and y stage
-  constexpr int VM_C = (S - 2) * CI;       // window of contraction stages only
-  constexpr int VM_Y = (S - 2) * YI + (S - 1) * YST;  // window of y stages only
-  constexpr int VM_MIN = (S - 2) * (CI < YI ? CI : YI);  // any window: fewest loads per stage
-  static_assert(N % 4 == 0 && VM_Y < 64 && VM_C < 64, "vmcnt range");
+  constexpr int CI = 4 + MT;               // loads per wave and stage
+  // Stage j's loads have landed once at most VM_C newer vector memory
+  // operations are outstanding: the loads of the S - 2 stages issued after
+  // it.  The heads' stores after a tile's last stage only add newer
+  // operations, so the same bound then waits a little longer than needed.
+  constexpr int VM_C = (S - 2) * CI;
+  static_assert(N % 4 == 0 && VM_C < 64, "vmcnt range");
   __shared__ u32x4 ring[S * UNITS * kWave];
   __shared__ float mix_sh[TT][M + 1];
-  __shared__ __align__(16) float pre_sh[TT][N];
   __shared__ __align__(16) float inv_sh[TT];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int D = a.D;
-  static_assert(sizeof(pre_sh[0]) % 16 == 0, "pre of a token is whole 16-byte LDS reads");
   const int K = N * D;
   const int64_t T = a.T;
   const int nst_c = (K + CW - 1) / CW;
-  const int ncb = (D + YW - 1) / YW;
   const int64_t ntiles = (T + TT - 1) / TT;
   // stage range of this block within its tiles: [s_first, per_tile)
   const int s_first = SPLIT ? (int)blockIdx.y * a.split_stages : 0;
-  const int per_tile = SPLIT ? (s_first + a.split_stages < nst_c ? s_first + a.split_stages : nst_c)
-                             : nst_c + (TT / 4) * ncb;
+  const int per_tile = SPLIT ? (s_first + a.split_stages < nst_c ? s_first + a.split_stages : nst_c) : nst_c;
   const int64_t my_tiles = SPLIT ? (blockIdx.x < ntiles ? 1 : 0)
                                  : (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
   if (my_tiles <= 0 || s_first >= per_tile) return;  // uniform over the block
@@ -390,37 +384,20 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
     const int nv = (int)(T - tb < TT ? T - tb : TT);
     const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * UNITS * 1024);
     const auto rx = rows_rsrc(x + tb * K, (int64_t)nv * K * 2);
-    if (is < nst_c) {
-      const int k0 = is * CW;
-      // units 0..15: x rows 4u..4u+3 (u = wave + 4i, i < 4); 16..: phi rows
-      // 4(u-16)..+3 (u = 16 + wave + 4(i-4)); chunks XOR-swizzled by row & 15
+    const int k0 = is * CW;
+    // units 0..15: x rows 4u..4u+3 (u = wave + 4i, i < 4); 16..: phi rows
+    // 4(u-16)..+3 (u = 16 + wave + 4(i-4)); chunks XOR-swizzled by row & 15
 #pragma unroll
-      for (int i = 0; i < CI; ++i) {
-        const int u = wave + 4 * i;
-        const int row = 4 * (wave + 4 * (i < 4 ? i : i - 4)) + q;
-        const int k = k0 + 8 * (r ^ (row & 15));
-        const uint32_t off = k < K ? (uint32_t)(((int64_t)row * K + k) * 2) : kBufferOob;
-        lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
-        if (i < 4)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2 /* nt */);
-        else
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, off, 0, 0, 0);
-      }
-    } else {
-      // unit n + N*i: token 4*tg + i, stream n (this wave: n = wave, wave + 4, ..),
-      // columns cb*512 + 8*lane
-      const int sy = is - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
-      const int col = cb * YW + 8 * lane;
-#pragma unroll
-      for (int nn = 0; nn < N; nn += 4)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = nn + wave;
-          lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + (n + N * i) * 1024);
-          const uint32_t off =
-              col < D ? (uint32_t)((((int64_t)(4 * tg + i) * N + n) * D + col) * 2) : kBufferOob;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2);
-        }
+    for (int i = 0; i < CI; ++i) {
+      const int u = wave + 4 * i;
+      const int row = 4 * (wave + 4 * (i < 4 ? i : i - 4)) + q;
+      const int k = k0 + 8 * (r ^ (row & 15));
+      const uint32_t off = k < K ? (uint32_t)(((int64_t)row * K + k) * 2) : kBufferOob;
+      lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
+      if (i < 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2 /* nt */);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, off, 0, 0, 0);
     }
     if (++is == per_tile) {
       is = s_first;
@@ -437,218 +414,160 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   int64_t ctile = blockIdx.x;
   int cs = s_first;  // stage of the current tile being consumed
   for (int64_t j = 0; j < J; ++j) {
-    // this wave's loads of stage j have landed once at most V newer vector
-    // memory operations are outstanding (windows of one stage kind get the
-    // exact count, mixed windows the smallest; a split block runs
-    // contraction stages only, which store nothing)
-    if (j + S - 2 < J) {
-      if (SPLIT || (cs >= S - 1 && cs + S - 2 < nst_c))
-        wait_vmcnt<VM_C>();
-      else if (cs >= nst_c + S - 1 && cs + S - 2 < per_tile)
-        wait_vmcnt<VM_Y>();
-      else
-        wait_vmcnt<VM_MIN>();
-    } else {
+    // this wave's loads of stage j have landed (see VM_C); near the end
+    // fewer stages follow it and everything is waited for
+    if (j + S - 2 < J)
+      wait_vmcnt<VM_C>();
+    else
       wait_vmcnt<0>();
-    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * UNITS * 1024);
     const int64_t tb = ctile * TT;
 
-    if (cs < nst_c) {
-      // ---- contraction stage: row block `wave` x all of phi ----------------
-      if (j + S - 1 < J) issue(j + S - 1);
-      // chunk 4g+q of x row 16*wave + r and of phi rows 16*mt + r: the
-      // swizzled positions differ per g, so each read has its own address;
-      // phi row 16*mt + r sits mt*4 KB after row r
-      u32x4 A[4], B[MT][4];
-      const uint32_t ca = slot + (16 * wave + r) * 256, cb0 = slot + 16 * 1024 + r * 256;
-      uint32_t sw[4];
+    // ---- contraction stage: row block `wave` x all of phi ----------------
+    if (j + S - 1 < J) issue(j + S - 1);
+    // chunk 4g+q of x row 16*wave + r and of phi rows 16*mt + r: the
+    // swizzled positions differ per g, so each read has its own address;
+    // phi row 16*mt + r sits mt*4 KB after row r
+    u32x4 A[4], B[MT][4];
+    const uint32_t ca = slot + (16 * wave + r) * 256, cb0 = slot + 16 * 1024 + r * 256;
+    uint32_t sw[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) sw[g] = ((4 * g + q) ^ r) << 4;
+    for (int g = 0; g < 4; ++g) sw[g] = ((4 * g + q) ^ r) << 4;
+    asm volatile(
+        "ds_read_b128 %0, %12\n\t"
+        "ds_read_b128 %1, %13\n\t"
+        "ds_read_b128 %2, %14\n\t"
+        "ds_read_b128 %3, %15\n\t"
+        "ds_read_b128 %4, %16\n\t"
+        "ds_read_b128 %5, %17\n\t"
+        "ds_read_b128 %6, %18\n\t"
+        "ds_read_b128 %7, %19\n\t"
+        "ds_read_b128 %8, %16 offset:4096\n\t"
+        "ds_read_b128 %9, %17 offset:4096\n\t"
+        "ds_read_b128 %10, %18 offset:4096\n\t"
+        "ds_read_b128 %11, %19 offset:4096\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0][0]), "=&v"(B[0][1]),
+          "=&v"(B[0][2]), "=&v"(B[0][3]), "=&v"(B[1][0]), "=&v"(B[1][1]), "=&v"(B[1][2]), "=&v"(B[1][3])
+        : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
+          "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
+        : "memory");
+    if constexpr (MT == 5) {  // N = 8: phi rows 32..79
       asm volatile(
-          "ds_read_b128 %0, %12\n\t"
-          "ds_read_b128 %1, %13\n\t"
-          "ds_read_b128 %2, %14\n\t"
-          "ds_read_b128 %3, %15\n\t"
-          "ds_read_b128 %4, %16\n\t"
-          "ds_read_b128 %5, %17\n\t"
-          "ds_read_b128 %6, %18\n\t"
-          "ds_read_b128 %7, %19\n\t"
-          "ds_read_b128 %8, %16 offset:4096\n\t"
-          "ds_read_b128 %9, %17 offset:4096\n\t"
-          "ds_read_b128 %10, %18 offset:4096\n\t"
-          "ds_read_b128 %11, %19 offset:4096\n\t"
+          "ds_read_b128 %0, %12 offset:8192\n\t"
+          "ds_read_b128 %1, %13 offset:8192\n\t"
+          "ds_read_b128 %2, %14 offset:8192\n\t"
+          "ds_read_b128 %3, %15 offset:8192\n\t"
+          "ds_read_b128 %4, %12 offset:12288\n\t"
+          "ds_read_b128 %5, %13 offset:12288\n\t"
+          "ds_read_b128 %6, %14 offset:12288\n\t"
+          "ds_read_b128 %7, %15 offset:12288\n\t"
+          "ds_read_b128 %8, %12 offset:16384\n\t"
+          "ds_read_b128 %9, %13 offset:16384\n\t"
+          "ds_read_b128 %10, %14 offset:16384\n\t"
+          "ds_read_b128 %11, %15 offset:16384\n\t"
           "s_waitcnt lgkmcnt(0)"
-          : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0][0]), "=&v"(B[0][1]),
-            "=&v"(B[0][2]), "=&v"(B[0][3]), "=&v"(B[1][0]), "=&v"(B[1][1]), "=&v"(B[1][2]), "=&v"(B[1][3])
-          : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
-            "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
+          : "=&v"(B[2][0]), "=&v"(B[2][1]), "=&v"(B[2][2]), "=&v"(B[2][3]), "=&v"(B[3][0]), "=&v"(B[3][1]),
+            "=&v"(B[3][2]), "=&v"(B[3][3]), "=&v"(B[4][0]), "=&v"(B[4][1]), "=&v"(B[4][2]), "=&v"(B[4][3])
+          : "v"(cb0 + sw[0]), "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
           : "memory");
-      if constexpr (MT == 5) {  // N = 8: phi rows 32..79
-        asm volatile(
-            "ds_read_b128 %0, %12 offset:8192\n\t"
-            "ds_read_b128 %1, %13 offset:8192\n\t"
-            "ds_read_b128 %2, %14 offset:8192\n\t"
-            "ds_read_b128 %3, %15 offset:8192\n\t"
-            "ds_read_b128 %4, %12 offset:12288\n\t"
-            "ds_read_b128 %5, %13 offset:12288\n\t"
-            "ds_read_b128 %6, %14 offset:12288\n\t"
-            "ds_read_b128 %7, %15 offset:12288\n\t"
-            "ds_read_b128 %8, %12 offset:16384\n\t"
-            "ds_read_b128 %9, %13 offset:16384\n\t"
-            "ds_read_b128 %10, %14 offset:16384\n\t"
-            "ds_read_b128 %11, %15 offset:16384\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(B[2][0]), "=&v"(B[2][1]), "=&v"(B[2][2]), "=&v"(B[2][3]), "=&v"(B[3][0]), "=&v"(B[3][1]),
-              "=&v"(B[3][2]), "=&v"(B[3][3]), "=&v"(B[4][0]), "=&v"(B[4][1]), "=&v"(B[4][2]), "=&v"(B[4][3])
-            : "v"(cb0 + sw[0]), "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
-            : "memory");
-      } else {
-        static_assert(MT == 2, "phi row blocks read above");
-      }
-      // The stage's 128 columns go through a fresh 4-step MFMA chain that is
-      // then added to the running sums with round-to-nearest-even adds: a
-      // single MFMA accumulator chain over all of K (up to ~900 steps) drifts
-      // measurably (2e-5 relative at K = 16384).
-      floatx4 part[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) part[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float lo = __uint_as_float(A[g][i] << 16), hi = __uint_as_float(A[g][i] & 0xffff0000u);
-          ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) part[mt] = mfma16x16x32(as_bf16x8(A[g]), as_bf16x8(B[mt][g]), part[mt]);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
-
-      if (SPLIT && cs == per_tile - 1) {
-        // ---- this split's partial sums of the tile --------------------------
-        // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; after
-        // the shuffles the lanes of row r hold this split's sum(x^2) of token
-        // 16*wave + r
-        ssq += __shfl_xor(ssq, 16, kWave);
-        ssq += __shfl_xor(ssq, 32, kWave);
-        const int64_t pbase = (int64_t)blockIdx.y * T;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t tok = tb + 16 * wave + 4 * q + v;
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            if (tok < T && 16 * mt + r < M) a.part[(pbase + tok) * M + 16 * mt + r] = acc[mt][v];
-        }
-        if (q == 0 && tb + 16 * wave + r < T) a.part_ssq[pbase + tb + 16 * wave + r] = ssq;
-      } else if (!SPLIT && cs == nst_c - 1) {
-        // ---- tile's mixes, heads and Sinkhorn -----------------------------
-        // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; the
-        // lane of row r (any q) holds sum(x^2) of token 16*wave + r
-        ssq += __shfl_xor(ssq, 16, kWave);
-        ssq += __shfl_xor(ssq, 32, kWave);
-        const float inv_row = 1.0f / sqrtf(ssq / (float)K + a.norm_eps);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float inv = __shfl(inv_row, 4 * q + v, kWave);
-          const int tt = 16 * wave + 4 * q + v;
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            if (16 * mt + r < M) mix_sh[tt][16 * mt + r] = acc[mt][v] * inv;
-        }
-        if (q == 0) inv_sh[16 * wave + r] = inv_row;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        ssq = 0.f;
-        __syncthreads();
-        if (a.mixes) {
-          for (int idx = tid; idx < TT * M; idx += kFwdThreads) {
-            const int tt = idx / M, m = idx - (idx / M) * M;
-            if (tb + tt < T) a.mixes[(tb + tt) * M + m] = mix_sh[tt][m];
-          }
-        }
-        if (a.inv_rms && tid < TT && tb + tid < T) a.inv_rms[tb + tid] = inv_sh[tid];
-        constexpr int TPP = kFwdThreads / L;
-#pragma unroll 1
-        for (int ps = 0; ps < TT / TPP; ++ps) {
-          const int tt = ps * TPP + tid / L;
-          const int64_t tok = tb + tt;
-          const bool ok = tok < T;
-          const float logit = mix_sh[tt][2 * N + e] * a2 + base_l;
-          const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
-          const float c = sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
-          if (ok) {
-            a.comb[tok * L + e] = c;
-            if (a.logits) a.logits[tok * L + e] = logit;
-          }
-          if (e < N) {
-            const float p = sigmoidf_(mix_sh[tt][e] * a0 + base_h) + a.hc_eps;
-            pre_sh[tt][e] = p;
-            if (ok && a.pre) a.pre[tok * N + e] = p;
-          } else if (e < 2 * N) {
-            const float po = 2.0f * sigmoidf_(mix_sh[tt][e] * a1 + base_h);
-            if (ok) a.post_out[tok * N + (e - N)] = po;
-          }
-        }
-        __syncthreads();
-      }
     } else {
-      // ---- y stage: wave w -> token 4*tg + w, lane -> 8 columns ------------
-      const int sy = cs - nst_c, tg = sy / ncb, cb = sy - tg * ncb;
-      const int t = 4 * tg + wave;  // token within the tile
-      if (j + S - 1 < J) issue(j + S - 1);
-      u32x4 X[N], P[N / 4], I = zero4();
+      static_assert(MT == 2, "phi row blocks read above");
+    }
+    // The stage's 128 columns go through a fresh 4-step MFMA chain that is
+    // then added to the running sums with round-to-nearest-even adds: a
+    // single MFMA accumulator chain over all of K (up to ~900 steps) drifts
+    // measurably (2e-5 relative at K = 16384).
+    floatx4 part[MT];
 #pragma unroll
-      for (int nn = 0; nn < N; nn += 4)  // streams nn..nn+3 of token t (units n + N*wave)
-        lds_read4<1024>(*reinterpret_cast<u32x4(*)[4]>(&X[nn]), slot + ((nn + N * wave) * kWave + lane) * 16);
-      // pre (and inv_rms) of token t: the same address on every lane, a broadcast
+    for (int mt = 0; mt < MT; ++mt) part[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int nn = 0; nn < N; nn += 4) P[nn / 4] = pre_sh4(lds_addr(&pre_sh[t][nn]));
-      if constexpr (XS) I = pre_sh4(lds_addr(&inv_sh[t]) & ~15u);
-      const int nv = (int)(T - tb < TT ? T - tb : TT);
-      const int col = cb * YW + 8 * lane;
-      float o[8];
+    for (int g = 0; g < 4; ++g) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(A[g][i] << 16), hi = __uint_as_float(A[g][i] & 0xffff0000u);
+        ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
+      }
 #pragma unroll
-      for (int n = 0; n < N; ++n) {
-        const float p = __uint_as_float(P[n / 4][n % 4]);
+      for (int mt = 0; mt < MT; ++mt) part[mt] = mfma16x16x32(as_bf16x8(A[g]), as_bf16x8(B[mt][g]), part[mt]);
+    }
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          o[2 * w] = fmaf(p, __uint_as_float(X[n][w] << 16), o[2 * w]);
-          o[2 * w + 1] = fmaf(p, __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
+    for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
+
+    if (SPLIT && cs == per_tile - 1) {
+      // ---- this split's partial sums of the tile --------------------------
+      // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; after
+      // the shuffles the lanes of row r hold this split's sum(x^2) of token
+      // 16*wave + r
+      ssq += __shfl_xor(ssq, 16, kWave);
+      ssq += __shfl_xor(ssq, 32, kWave);
+      const int64_t pbase = (int64_t)blockIdx.y * T;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t tok = tb + 16 * wave + 4 * q + v;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          if (tok < T && 16 * mt + r < M) a.part[(pbase + tok) * M + 16 * mt + r] = acc[mt][v];
+      }
+      if (q == 0 && tb + 16 * wave + r < T) a.part_ssq[pbase + tb + 16 * wave + r] = ssq;
+    } else if (!SPLIT && cs == nst_c - 1) {
+      // ---- tile's mixes, heads and Sinkhorn -----------------------------
+      // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; the
+      // lane of row r (any q) holds sum(x^2) of token 16*wave + r
+      ssq += __shfl_xor(ssq, 16, kWave);
+      ssq += __shfl_xor(ssq, 32, kWave);
+      const float inv_row = 1.0f / sqrtf(ssq / (float)K + a.norm_eps);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float inv = __shfl(inv_row, 4 * q + v, kWave);
+        const int tt = 16 * wave + 4 * q + v;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          if (16 * mt + r < M) mix_sh[tt][16 * mt + r] = acc[mt][v] * inv;
+      }
+      if (q == 0) inv_sh[16 * wave + r] = inv_row;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      ssq = 0.f;
+      __syncthreads();
+      if (a.mixes) {
+        for (int idx = tid; idx < TT * M; idx += kFwdThreads) {
+          const int tt = idx / M, m = idx - (idx / M) * M;
+          if (tb + tt < T) a.mixes[(tb + tt) * M + m] = mix_sh[tt][m];
         }
       }
-      u32x4 ov;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
-      // rows >= nv fall outside the range and are dropped, as are columns >= D
-      const auto ry = rows_rsrc(static_cast<bf16_t*>(a.y) + tb * D, (int64_t)nv * D * 2);
-      __builtin_amdgcn_raw_buffer_store_b128(ov, ry, col < D ? (uint32_t)(((int64_t)t * D + col) * 2) : kBufferOob,
-                                             0, 2 /* nt */);
-      if constexpr (XS) {
-        const float inv = __uint_as_float(I[t & 3]);
-        const auto rs = rows_rsrc(a.x_scaled + tb * K, (int64_t)nv * K * 4);
-#pragma unroll
-        for (int n = 0; n < N; ++n)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            u32x4 xs;
-#pragma unroll
-            for (int w = 0; w < 2; ++w) {
-              const uint32_t xw = X[n][2 * h + w];
-              xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv);
-              xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv);
-            }
-            const uint32_t off =
-                col < D ? (uint32_t)(((((int64_t)t * N + n) * D) + col + 4 * h) * 4) : kBufferOob;
-            __builtin_amdgcn_raw_buffer_store_b128(xs, rs, off, 0, 0);
-          }
+      if (tid < TT && tb + tid < T) {
+        a.inv_ws[tb + tid] = inv_sh[tid];
+        if (a.inv_rms) a.inv_rms[tb + tid] = inv_sh[tid];
       }
+      constexpr int TPP = kFwdThreads / L;
+#pragma unroll 1
+      for (int ps = 0; ps < TT / TPP; ++ps) {
+        const int tt = ps * TPP + tid / L;
+        const int64_t tok = tb + tt;
+        const bool ok = tok < T;
+        const float logit = mix_sh[tt][2 * N + e] * a2 + base_l;
+        const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
+        const float c = sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
+        if (ok) {
+          a.comb[tok * L + e] = c;
+          if (a.logits) a.logits[tok * L + e] = logit;
+        }
+        if (e < N) {
+          const float p = sigmoidf_(mix_sh[tt][e] * a0 + base_h) + a.hc_eps;
+          if (ok) {
+            a.pre_ws[tok * N + e] = p;
+            if (a.pre) a.pre[tok * N + e] = p;
+          }
+        } else if (e < 2 * N) {
+          const float po = 2.0f * sigmoidf_(mix_sh[tt][e] * a1 + base_h);
+          if (ok) a.post_out[tok * N + (e - N)] = po;
+        }
+      }
+      __syncthreads();
     }
     if (++cs == per_tile) {
       cs = s_first;
@@ -713,62 +632,80 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
   }
 }
 
-// Kernel 3: y[t, d] = sum_n pre[t, n] * x[t, n, d] (and x_scaled), a wave per
-// (token, 512-column block), 8 columns a lane, same FMA order as the y stages
-// of the single-kernel form.
+// y[t, d] = sum_n pre[t, n] * x[t, n, d] (and x_scaled = x * inv_rms): a
+// block per token of W = min(16, ceil(D / 512)) waves, wave w taking the
+// 512-column chunks w, w + W, .. (8 columns a lane), so a token's rows are read
+// as a few long contiguous streams (the order that lets the post kernels
+// move mixed traffic fastest); x is read once here (non-temporal), y and
+// x_scaled are written once (streaming stores).  Same FMA order as the
+// generic kernel's y.
+constexpr int kFwdYWaves = 16;
+
 template <int N, bool XS>
-__global__ __launch_bounds__(kFwdThreads) void pre_fwd_y_kernel(PreFwdArgs a) {
+__global__ __launch_bounds__(kWave * kFwdYWaves) void pre_fwd_y_kernel(PreFwdArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = (int64_t)blockIdx.x * (kFwdThreads / kWave) + (threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x / kWave;
+  const int64_t t = blockIdx.x;
   const int D = a.D;
-  const int col = blockIdx.y * 512 + 8 * lane;
-  if (t >= a.T || col >= D) return;
-  const bf16_t* x = static_cast<const bf16_t*>(a.x) + t * N * D + col;
   float p[N];
 #pragma unroll
   for (int n = 0; n < N; ++n) p[n] = a.pre_ws[t * N + n];
-  u32x4 X[N];
+  const float inv = XS ? a.inv_ws[t] : 0.f;
+  for (int col = wave * 512 + 8 * lane; col < D; col += W * 512) {
+    const bf16_t* x = static_cast<const bf16_t*>(a.x) + t * N * D + col;
+    u32x4 X[N];
 #pragma unroll
-  for (int n = 0; n < N; ++n) X[n] = ld16nt(x + (int64_t)n * D);
-  float o[8];
+    for (int n = 0; n < N; ++n) X[n] = ld16nt(x + (int64_t)n * D);
+    float o[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = 0.f;
-#pragma unroll
-  for (int n = 0; n < N; ++n)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      o[2 * w] = fmaf(p[n], __uint_as_float(X[n][w] << 16), o[2 * w]);
-      o[2 * w + 1] = fmaf(p[n], __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
-    }
-  u32x4 ov;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
-  st16nt(static_cast<bf16_t*>(a.y) + t * D + col, ov);
-  if constexpr (XS) {
-    const float inv = a.inv_ws[t];
+    for (int i = 0; i < 8; ++i) o[i] = 0.f;
 #pragma unroll
     for (int n = 0; n < N; ++n)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        u32x4 xs;
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-          const uint32_t xw = X[n][2 * h + w];
-          xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv);
-          xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv);
-        }
-        st16(a.x_scaled + (t * N + n) * (int64_t)D + col + 4 * h, xs);
+      for (int w = 0; w < 4; ++w) {
+        o[2 * w] = fmaf(p[n], __uint_as_float(X[n][w] << 16), o[2 * w]);
+        o[2 * w + 1] = fmaf(p[n], __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
       }
+    u32x4 ov;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
+    st16nt(static_cast<bf16_t*>(a.y) + t * D + col, ov);
+    if constexpr (XS) {
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          u32x4 xs;
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const uint32_t xw = X[n][2 * h + w];
+            xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv);
+            xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv);
+          }
+          st16nt(a.x_scaled + (t * N + n) * (int64_t)D + col + 4 * h, xs);
+        }
+    }
   }
 }
 
-// Split-K plan for few tiles: ntiles <= 256 splits K into up to 64 parts so
-// that about 512 blocks run the contraction; the plan depends on (T, N, D)
-// only, so results do not depend on the device.
+template <int N>
+static int launch_pre_fwd_y(const PreFwdArgs& a, hipStream_t st) {
+  const int chunks = (a.D + 511) / 512;
+  const dim3 grid((unsigned)a.T), block(kWave * (chunks < kFwdYWaves ? chunks : kFwdYWaves));
+  if (a.x_scaled)
+    hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((pre_fwd_y_kernel<N, false>), grid, block, 0, st, a);
+  return check_launch("pre_fwd_y");
+}
+
 struct FwdSplitPlan {
   int nsplit = 0, stages = 0;
   size_t bytes = 0;  // workspace for partials, pre and inv_rms
 };
+
+// pre (T, N) and inv_rms (T,) handed to the y kernel
+static size_t fwd_y_ws_bytes(int64_t T, int N) { return align256((size_t)T * N * 4) + align256((size_t)T * 4); }
 
 static FwdSplitPlan fwd_split_plan(int64_t T, int N, int D) {
   FwdSplitPlan p;
@@ -810,7 +747,7 @@ static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_by
     a.pre_ws = reinterpret_cast<float*>(w);
     w += align256((size_t)a.T * N * 4);
     a.inv_ws = reinterpret_cast<float*>(w);
-    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false, true>), dim3((unsigned)ntiles, (unsigned)plan.nsplit),
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, true>), dim3((unsigned)ntiles, (unsigned)plan.nsplit),
                        dim3(kFwdThreads), 0, st, a);
     int rc = check_launch("pre_fwd_split");
     if (rc) return rc;
@@ -818,20 +755,18 @@ static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_by
     hipLaunchKernelGGL((pre_fwd_finalize_kernel<N>), dim3((unsigned)((a.T + TPP - 1) / TPP)), dim3(kFwdThreads),
                        0, st, a, plan.nsplit);
     if ((rc = check_launch("pre_fwd_finalize"))) return rc;
-    const dim3 gy((unsigned)((a.T + 3) / 4), (unsigned)((a.D + 511) / 512));
-    if (a.x_scaled)
-      hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), gy, dim3(kFwdThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((pre_fwd_y_kernel<N, false>), gy, dim3(kFwdThreads), 0, st, a);
-    return check_launch("pre_fwd_y");
+    return launch_pre_fwd_y<N>(a, st);
   }
+  // contraction and heads in one persistent kernel, then y
+  char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
+  a.pre_ws = reinterpret_cast<float*>(w);
+  a.inv_ws = reinterpret_cast<float*>(w + align256((size_t)a.T * N * 4));
   const int64_t cus = device_cu_count();
   const int64_t grid = ntiles < cus ? ntiles : cus;  // one block per CU (LDS ring)
-  if (a.x_scaled)
-    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, true, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
-  return check_launch("pre_fwd_dma");
+  hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+  int rc = check_launch("pre_fwd_dma");
+  if (rc) return rc;
+  return launch_pre_fwd_y<N>(a, st);
 }
 
 template <int N, typename S, int P>
@@ -871,8 +806,11 @@ extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, in
   if (N <= 0 || D <= 0) return 0;
   const int M = 2 * N + N * N;
   const int64_t K = (int64_t)N * D;
-  if (phi_dtype == MHC_DTYPE_BF16 && K % 8 == 0)  // phi used directly; split-K partials for few tiles
-    return kPreFwdWsBase + fwd_split_plan(T, N, D).bytes;
+  if (phi_dtype == MHC_DTYPE_BF16 && K % 8 == 0) {  // phi used directly: pre / inv_rms for the y
+    const size_t split = fwd_split_plan(T, N, D).bytes;  // kernel, split-K partials for few tiles
+    const size_t y = fwd_y_ws_bytes(T < 0 ? 0 : T, N);
+    return kPreFwdWsBase + (split > y ? split : y);
+  }
   return align256(phi_planes_bytes(phi_dtype, M, K));
 }
 
@@ -919,7 +857,8 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   a.T = T;
   a.D = D;
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(y) && (!x_scaled || aligned16(x_scaled));
-  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec))
+  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec) && workspace &&
+      workspace_bytes >= kPreFwdWsBase + fwd_y_ws_bytes(T, N))
     return N == 4 ? launch_pre_fwd_dma<4>(a, workspace, workspace_bytes, st)
                   : launch_pre_fwd_dma<8>(a, workspace, workspace_bytes, st);
   switch (x_dtype) {
