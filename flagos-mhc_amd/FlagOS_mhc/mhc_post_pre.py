@@ -8,9 +8,10 @@ Between two sublayers the reference's model code runs
 
 ``mhc_post_pre_clamp_sinkhorn`` returns the same ``(x_next, out)`` from the
 gfx950 entry point ``mhc_post_pre_fwd``: for N = 4 bf16 with D % 64 == 0 and
-D >= 3136 one kernel reads x once, writes x_next once (bit-identical to
+D >= 256 one kernel reads x once, writes x_next once (bit-identical to
 ``mhc_post``) and feeds the same values to the pre contraction, saving one
-full read of the residual streams; other shapes run the two kernels in turn.
+full read of the residual streams (the y pass then reads x_next back); other
+shapes run the two kernels in turn.
 The reference has no fused operator; argument meanings, shapes, dtypes and
 errors are those of the two operators it replaces.  With ``need_backward``
 the dict carries inv_rms, mixes, h_res_logits and pre, and ``x_scaled`` is

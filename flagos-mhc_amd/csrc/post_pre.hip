@@ -5,12 +5,15 @@
 // writes x_next, then the pre kernel reads x_next twice (contraction, then y).
 // Here the contraction stages compute x_next from x and h_out on the fly,
 // write it once and feed the same bf16 values to the MFMA contraction; only
-// the y stages read x_next back.  Per token that saves one full read of the
-// N streams (N*D*2 bytes, a quarter of the pair's traffic).
+// the y pass (the pre forward's y kernel, run afterwards) reads x_next back.
+// Per token that saves one full read of the N streams (N*D*2 bytes, a
+// quarter of the pair's traffic).
 //
-// Shape: N = 4, bf16 x / h_out / phi, D a multiple of 64 and >= 3136 (see
-// the read-after-write argument below); the C entry point runs mhc_post then
-// mhc_pre_clamp_sinkhorn for every other shape.
+// Shape: N = 4, bf16 x / h_out / phi, D a multiple of 64 and >= 256; the C
+// entry point runs mhc_post then mhc_pre_clamp_sinkhorn for every other
+// shape.  (The tile's gates sit in one LDS buffer that wave 0 refills when it
+// issues the next tile's first stage, S - 1 stages ahead: a tile must span
+// at least S stages, D >= 64 * S, so that it has read its gates by then.)
 //
 // A block (8 waves, two per SIMD so that one wave's waits overlap the other's
 // work) owns a tile of 32 tokens.  Wave w handles row block rb = w & 1
@@ -34,21 +37,14 @@
 // second halves through a DPP row rotation first.  The four waves of a row
 // block hold partial sums over their streams; they are added in a fixed order
 // through LDS after the tile's last contraction stage, followed by heads and
-// Sinkhorn exactly as in the pre kernel.  y stages then read x_next back (8
-// tokens x 4 streams x 512 columns per stage, a token per wave).
-//
-// Read-after-write of x_next: a lane's stores of stage s were issued after
-// its loads for stage s + S - 1, so they have completed once the wave's wait
-// at stage s + S returns (vector memory operations complete in issue order),
-// and the barrier that follows makes them visible to loads any wave issues
-// from then on.  The y stage (tg, cb) reads columns stored by contraction
-// stages up to s_max = min(8cb + 7, nst_c - 1) (nst_c = D/64) and its loads
-// are issued at stage nst_c + tg*ncb + cb - (S - 1) >= nst_c + cb - S + 1.
-// That is >= s_max + S when cb >= 2S - 2 (s_max <= nst_c - 1) and, for
-// cb <= 2S - 3, when nst_c >= 7cb + 2S + 6 (s_max <= 8cb + 7): both hold for
-// every cb once nst_c >= 16S - 15, i.e. D >= 3136 for S = 4.
+// Sinkhorn exactly as in the pre kernel; pre goes to the workspace for the y
+// kernel.  The y pass used to run as stages of this kernel (8 tokens x 4
+// streams x 512 columns each, which needed D >= 3136 so that a y stage's
+// loads followed the stores of its columns); as the block-per-token kernel
+// it is faster (c5: 2.55 -> 2.26 ms for the fused forward on one MI355X).
 #include "mhc_launch.hpp"
 #include "pre_common.hpp"
+#include "pre_host.hpp"
 #include "sinkhorn.hpp"
 
 namespace mhc {
@@ -63,17 +59,12 @@ constexpr int kPPWaves = 8;
 constexpr int kPPThreads = kPPWaves * kWave;
 constexpr int kPPStages = 4;                  // ring slots
 constexpr int kPPCW = 64;                     // d columns per contraction stage
-constexpr int kPPYW = 512;                    // d columns per y stage
-constexpr int kPPYT = 8;                      // tokens per y stage (one per wave)
-constexpr int kPPMinD = kPPCW * (16 * kPPStages - 15);  // 3136: the y loads follow the stores
 constexpr int kUH = 16, kUP = 20;             // first h_out / phi unit of a contraction slot
-constexpr int kPPUnits = 36;                  // 1 KB units per slot (y stages use 32)
+constexpr int kPPUnits = 36;                  // 1 KB units per slot
 constexpr int kPPCImax = (kPPUnits + kPPWaves - 1) / kPPWaves;  // 5: loads of waves 0..3
 constexpr int kPPCImin = kPPUnits / kPPWaves;                   // 4: loads of waves 4..7
-constexpr int kPPYI = 4;                      // loads per wave and y stage
 constexpr int kPPCST = 2;                     // x_next stores per lane and contraction stage
-constexpr int kPPYST = 1;                     // y stores per lane and y stage
-static_assert(kPPYT * kPPN <= kPPUnits && kPPYT == kPPWaves, "y slot layout");
+constexpr int kPPMinD = kPPCW * kPPStages;    // 256: a tile spans at least S stages (gates buffer)
 
 struct PostPreArgs {
   const bf16_t* x;       // (T, 4, D)
@@ -94,6 +85,7 @@ struct PostPreArgs {
   float* mixes;
   float* logits;
   float* pre;
+  float* pre_ws;         // (T, 4) pre for the y kernel
   int64_t T;
   int D;
 };
@@ -106,17 +98,18 @@ __device__ __forceinline__ u32x4 lds_read1(uint32_t a) {
 
 __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a) {
   constexpr int N = kPPN, M = kPPM, MT = kPPMT, L = N * N, TT = kPPTile, S = kPPStages;
-  // windows of one stage kind get the count of the wave issuing fewest
-  // operations; mixed windows the smallest of both kinds
+  // Stage j's loads have landed once at most V newer vector memory
+  // operations are outstanding.  Issued after them: the loads of the S - 2
+  // next stages (at least kPPCImin per wave each) and, from stage S - 1 on,
+  // the x_next stores of the S - 1 previous stages (kPPCST each; the heads'
+  // stores only add).  The first S - 1 stages of a block count loads only.
+  constexpr int VM_START = (S - 2) * kPPCImin;
   constexpr int VM_C = (S - 2) * kPPCImin + (S - 1) * kPPCST;
-  constexpr int VM_Y = (S - 2) * kPPYI + (S - 1) * kPPYST;
-  constexpr int VM_MIN = (S - 2) * (kPPCImin < kPPYI ? kPPCImin : kPPYI) + (S - 1) * (kPPCST < kPPYST ? kPPCST : kPPYST);
-  static_assert(VM_C < 64 && VM_Y < 64 && VM_MIN <= VM_C && VM_MIN <= VM_Y, "vmcnt range");
+  static_assert(VM_C < 64, "vmcnt range");
   __shared__ u32x4 ring[S * kPPUnits * kWave];
   __shared__ u32x4 gates[3 * kWave];  // h_res rows of the 32 tokens (2 units), h_post (1 unit)
   __shared__ float red_ssq[2][3][16];
   __shared__ float mix_sh[TT][M + 1];
-  __shared__ __align__(16) float pre_sh[TT][N];
   __shared__ __align__(16) float inv_sh[TT];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -128,8 +121,7 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
   const int64_t K = (int64_t)N * D;
   const int64_t T = a.T;
   const int nst_c = D / kPPCW;
-  const int ncb = (D + kPPYW - 1) / kPPYW;
-  const int per_tile = nst_c + (TT / kPPYT) * ncb;
+  const int per_tile = nst_c;
   const int64_t ntiles = (T + TT - 1) / TT;
   const int64_t my_tiles = (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
   if (my_tiles <= 0) return;  // uniform over the block
@@ -143,8 +135,8 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
   const float base_h = e < 2 * N ? a.base[e] : 0.f;
 
   // Per-lane byte offsets of this wave's contraction-stage units (u = wave +
-  // 8i) at d0 = 0 (a stage adds 2*d0), of its x_next stores and of its y
-  // loads; rows >= M of phi are out of range.
+  // 8i) at d0 = 0 (a stage adds 2*d0) and of its x_next stores; rows >= M of
+  // phi are out of range.
   const int nci = wave < kPPUnits - kPPCImin * kPPWaves ? kPPCImax : kPPCImin;
   // DMA lane L of an x / h_out unit: row i = L >> 3 of its half, chunk
   // (L & 7) ^ f(i, g)
@@ -181,62 +173,44 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
     const int c = 4 * h + q, ri = r & 7;
     rpos[h] = (uint32_t)(hi * 1024 + (ri * 8 + (c ^ ((ri >> 1) ^ (hi << 2)))) * 16);
   }
-  // y loads: unit 4w + n = token 8tg + w, stream n, columns cb*512 + 8*lane
-  const uint32_t ybase = (uint32_t)(((int64_t)wave * N * D) * 2 + 16 * lane);
 
   // ---- loads of stage j (issued S - 1 stages ahead) ------------------------
   int64_t itile = blockIdx.x;
-  int is = 0, itg = 0, icb = 0;  // stage of the next issue; its y token group / column block
+  int is = 0;  // stage of the next issue
   auto issue = [&](int64_t j) {
     const int64_t tb = itile * TT;
     const int nv = (int)(T - tb < TT ? T - tb : TT);
     const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * kPPUnits * 1024);
-    if (is < nst_c) {
-      if (is == 0 && wave == 0) {
-        // the tile's gates: h_res rows (64 bytes a token), h_post (16 bytes)
-        const auto rg = rows_rsrc(a.h_res + tb * L, (int64_t)nv * L * 4);
+    if (is == 0 && wave == 0) {
+      // the tile's gates: h_res rows (64 bytes a token), h_post (16 bytes)
+      const auto rg = rows_rsrc(a.h_res + tb * L, (int64_t)nv * L * 4);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(uintptr_t)(gates_lds + u * 1024), 16,
-                                                   (uint32_t)((16 * u + (lane >> 2)) * 64 + (lane & 3) * 16), 0,
-                                                   0, 0);
-        const auto rp = rows_rsrc(a.h_post + tb * N, (int64_t)nv * N * 4);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void_t*)(uintptr_t)(gates_lds + 2048), 16,
-                                                 lane < TT ? (uint32_t)(lane * 16) : kBufferOob, 0, 0, 0);
-      }
-      const uint32_t d2 = (uint32_t)(is * kPPCW * 2);
-      const auto rx = rows_rsrc(a.x + tb * K, (int64_t)nv * K * 2);
-      const auto rh = rows_rsrc(a.h_out + tb * D, (int64_t)nv * D * 2);
+      for (int u = 0; u < 2; ++u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(uintptr_t)(gates_lds + u * 1024), 16,
+                                                 (uint32_t)((16 * u + (lane >> 2)) * 64 + (lane & 3) * 16), 0,
+                                                 0, 0);
+      const auto rp = rows_rsrc(a.h_post + tb * N, (int64_t)nv * N * 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void_t*)(uintptr_t)(gates_lds + 2048), 16,
+                                               lane < TT ? (uint32_t)(lane * 16) : kBufferOob, 0, 0, 0);
+    }
+    const uint32_t d2 = (uint32_t)(is * kPPCW * 2);
+    const auto rx = rows_rsrc(a.x + tb * K, (int64_t)nv * K * 2);
+    const auto rh = rows_rsrc(a.h_out + tb * D, (int64_t)nv * D * 2);
 #pragma unroll
-      for (int i = 0; i < kPPCImax; ++i) {
-        if (i < nci) {
-          const int u = wave + kPPWaves * i;
-          lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
-          if (u < kUH)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, cbase[i] + d2, 0, 0, 2 /* nt */);
-          else if (u < kUP)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, dst, 16, cbase[i] + d2, 0, 0, 2);
-          else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, cbase[i] + d2, 0, 0, 0);
-        }
-      }
-    } else {
-      // columns >= D read zero
-      const bool colok = icb * kPPYW + 8 * lane < D;
-      const uint32_t yo = ybase + (uint32_t)(((int64_t)kPPYT * itg * N * D + icb * kPPYW) * 2);
-      const auto rxn = rows_rsrc(a.x_next + tb * K, (int64_t)nv * K * 2);
-#pragma unroll
-      for (int n = 0; n < N; ++n)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rxn, (lds_void_t*)(uintptr_t)(slot + (N * wave + n) * 1024), 16,
-                                                 colok ? yo + (uint32_t)(n * D * 2) : kBufferOob, 0, 0, 2);
-      if (++icb == ncb) {
-        icb = 0;
-        ++itg;
+    for (int i = 0; i < kPPCImax; ++i) {
+      if (i < nci) {
+        const int u = wave + kPPWaves * i;
+        lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
+        if (u < kUH)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, cbase[i] + d2, 0, 0, 2 /* nt */);
+        else if (u < kUP)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, dst, 16, cbase[i] + d2, 0, 0, 2);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, cbase[i] + d2, 0, 0, 0);
       }
     }
     if (++is == per_tile) {
       is = 0;
-      itg = 0;
       itile += gridDim.x;
     }
   };
@@ -251,17 +225,15 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
 #pragma unroll
   for (int jj = 0; jj < N; ++jj) hr[jj] = 0.f;
   int64_t ctile = blockIdx.x;
-  int cs = 0, ctg = 0, ccb = 0;  // stage being consumed; its y token group / column block
+  int cs = 0;  // stage being consumed
   for (int64_t j = 0; j < J; ++j) {
-    // this wave's loads of stage j have landed once at most V newer vector
-    // memory operations are outstanding
+    // this wave's loads of stage j have landed (see VM_C); near the end
+    // fewer stages follow it and everything is waited for
     if (j + S - 2 < J) {
-      if (cs >= S - 1 && cs + S - 2 < nst_c)
+      if (j >= S - 1)
         wait_vmcnt<VM_C>();
-      else if (cs >= nst_c + S - 1 && cs + S - 2 < per_tile)
-        wait_vmcnt<VM_Y>();
       else
-        wait_vmcnt<VM_MIN>();
+        wait_vmcnt<VM_START>();
     } else {
       wait_vmcnt<0>();
     }
@@ -433,8 +405,10 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
           }
           if (e < N) {
             const float p = sigmoidf_(mix_sh[tt][e] * a0 + base_h) + a.hc_eps;
-            pre_sh[tt][e] = p;
-            if (ok && a.pre) a.pre[tok * N + e] = p;
+            if (ok) {
+              a.pre_ws[tok * N + e] = p;
+              if (a.pre) a.pre[tok * N + e] = p;
+            }
           } else if (e < 2 * N) {
             const float po = 2.0f * sigmoidf_(mix_sh[tt][e] * a1 + base_h);
             if (ok) a.post_out[tok * N + (e - N)] = po;
@@ -442,40 +416,9 @@ __global__ __launch_bounds__(kPPThreads) void post_pre_fwd_kernel(PostPreArgs a)
         }
         __syncthreads();
       }
-    } else {
-      // ---- y stage: wave w -> token 8tg + w, lane -> 8 columns --------------
-      const int t = kPPYT * ctg + wave, cb = ccb;
-      if (++ccb == ncb) {
-        ccb = 0;
-        ++ctg;
-      }
-      if (j + S - 1 < J) issue(j + S - 1);
-      u32x4 X[N];
-      lds_read4<1024>(X, slot + ((N * wave) * kWave + lane) * 16);
-      const u32x4 P = lds_read1(lds_addr(&pre_sh[t][0]));
-      const int col = cb * kPPYW + 8 * lane;
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = 0.f;
-#pragma unroll
-      for (int n = 0; n < N; ++n) {
-        const float p = __uint_as_float(P[n]);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          o[2 * w] = fmaf(p, __uint_as_float(X[n][w] << 16), o[2 * w]);
-          o[2 * w + 1] = fmaf(p, __uint_as_float(X[n][w] & 0xffff0000u), o[2 * w + 1]);
-        }
-      }
-      u32x4 ov;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
-      const auto ry = rows_rsrc(a.y + tb * D, (int64_t)nv * D * 2);
-      __builtin_amdgcn_raw_buffer_store_b128(ov, ry, col < D ? (uint32_t)(((int64_t)t * D + col) * 2) : kBufferOob,
-                                             0, 2 /* nt */);
     }
     if (++cs == per_tile) {
       cs = 0;
-      ctg = 0;
       ctile += gridDim.x;
     }
   }
@@ -513,7 +456,8 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
   if (T == 0) return MHC_OK;
   if (!x || !h_res || !h_out || !h_post || !phi || !alpha || !base || !x_next || !y || !post_out || !comb_frag)
     return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: null pointer");
-  if (!post_pre_usable(x, h_out, phi, x_next, y, x_dtype, phi_dtype, N, D)) {
+  if (!post_pre_usable(x, h_out, phi, x_next, y, x_dtype, phi_dtype, N, D) || !workspace ||
+      workspace_bytes < fwd_y_ws_bytes(T, N)) {
     // every other shape: the two operators one after the other
     int rc = mhc_post_fwd(x, h_res, h_out, h_post, x_next, T, N, D, x_dtype, stream);
     if (rc) return rc;
@@ -543,11 +487,13 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
   a.mixes = mixes;
   a.logits = h_res_logits;
   a.pre = pre;
+  a.pre_ws = static_cast<float*>(workspace);
   a.T = T;
   a.D = D;
   const int64_t ntiles = (T + kPPTile - 1) / kPPTile;
   const int64_t cus = device_cu_count();
   const int64_t grid = ntiles < cus ? ntiles : cus;  // one block per CU (LDS ring)
   hipLaunchKernelGGL(post_pre_fwd_kernel, dim3((unsigned)grid), dim3(kPPThreads), 0, (hipStream_t)stream, a);
-  return check_launch("post_pre_fwd");
+  if (int rc = check_launch("post_pre_fwd")) return rc;
+  return launch_pre_y_pass(x_next, a.pre_ws, y, T, N, D, (hipStream_t)stream);
 }

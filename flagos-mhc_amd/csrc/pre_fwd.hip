@@ -701,13 +701,23 @@ static int launch_pre_fwd_y(const PreFwdArgs& a, hipStream_t st) {
   return check_launch("pre_fwd_y");
 }
 
+int launch_pre_y_pass(const void* x, const float* pre, void* y, int64_t T, int N, int D, hipStream_t st) {
+  PreFwdArgs a{};
+  a.x = x;
+  a.pre_ws = const_cast<float*>(pre);
+  a.y = y;
+  a.T = T;
+  a.D = D;
+  if (N == 4) return launch_pre_fwd_y<4>(a, st);
+  if (N == 8) return launch_pre_fwd_y<8>(a, st);
+  return set_error(MHC_ERR_UNSUPPORTED, "pre y pass: N=%d not supported (4, 8)", N);
+}
+
 struct FwdSplitPlan {
   int nsplit = 0, stages = 0;
   size_t bytes = 0;  // workspace for partials, pre and inv_rms
 };
 
-// pre (T, N) and inv_rms (T,) handed to the y kernel
-static size_t fwd_y_ws_bytes(int64_t T, int N) { return align256((size_t)T * N * 4) + align256((size_t)T * 4); }
 
 static FwdSplitPlan fwd_split_plan(int64_t T, int N, int D) {
   FwdSplitPlan p;

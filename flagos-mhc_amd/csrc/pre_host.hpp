@@ -30,6 +30,16 @@ inline size_t phiT_planes_bytes(int32_t phi_dtype, int M, int64_t K) {
   return (size_t)phi_bwd_planes(phi_dtype) * (size_t)K * (size_t)round_up(M, 32) * 2;
 }
 
+// y = sum_n pre[t, n] * x[t, n, :] for bf16 x (T, N, D), D % 8 == 0 and
+// 16-byte aligned rows (the pre forward's y kernel, a block per token); pre
+// (T, N) fp32 in device memory.  The fused post + pre forward runs it on
+// x_next.
+int launch_pre_y_pass(const void* x, const float* pre, void* y, int64_t T, int N, int D, hipStream_t st);
+
+// Bytes the pre forward (and the fused post + pre forward) keep per call for
+// pre (T, N) and inv_rms (T,) between their contraction and y kernels.
+inline size_t fwd_y_ws_bytes(int64_t T, int N) { return align256((size_t)T * N * 4) + align256((size_t)T * 4); }
+
 // Makes phi available as bf16 planes [P][M][ld].  bf16 phi with K % 8 == 0
 // and a 16-byte aligned base is used in place; anything else is converted
 // into `ws` (which must hold phi_planes_bytes).

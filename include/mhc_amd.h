@@ -165,9 +165,9 @@ int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_
  * Outputs: x_next = mhc_post(x, h_res, h_out, h_post) (T,N,D) `x_dtype`,
  * bit-identical to mhc_post_fwd; y, post_out, comb_frag and the optional
  * inv_rms, mixes, h_res_logits, pre of mhc_pre_fwd applied to x_next (no
- * x_scaled).  N = 4 with bf16 x, h_out and phi, D % 64 == 0, D >= 3136 and
- * 16-byte aligned rows runs one kernel that reads x once and writes x_next
- * once; every other shape runs mhc_post_fwd then mhc_pre_fwd.
+ * x_scaled).  N = 4 with bf16 x, h_out and phi, D % 64 == 0, D >= 256 and
+ * 16-byte aligned rows reads x once and writes x_next once (then reads
+ * x_next back for y); every other shape runs mhc_post_fwd then mhc_pre_fwd.
  */
 size_t mhc_post_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype);
 int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,

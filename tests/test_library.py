@@ -138,7 +138,7 @@ def test_registered_op_compensated_gradients():
 
 @pytest.mark.gpu
 def test_opcheck_post_pre():
-    T, N, D = 40, 4, 3136   # the fused kernel (D >= 3136, D % 64 == 0)
+    T, N, D = 40, 4, 3136   # the fused kernel (D >= 256, D % 64 == 0)
     print(f"[opcheck post_pre] T={T} N={N} D={D}", flush=True)
     x, phi, alpha, base, noise, upstream = _layer_inputs(T, N, D)
     g = torch.Generator(device=DEV)
