@@ -32,6 +32,28 @@ inline int device_cu_count() {
   return cus;
 }
 
+// Dynamic LDS bytes that keep a kernel at one block per CU: just over half
+// of a CU's LDS (a kernel that uses no LDS of its own then never shares its
+// CU with a second block).  The streaming kernels that read a token's rows
+// as contiguous runs are faster with fewer tokens in flight per CU.  Queried
+// once per device; 0 if the device does not report its LDS sizes.
+inline size_t one_block_per_cu_lds() {
+  static std::atomic<long long> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  long long v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return (size_t)(v - 1);
+  int per_cu = 0, per_block = 0;
+  size_t pad = 0;
+  if (hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess &&
+      hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      per_cu > 0 && per_block > per_cu / 2)
+    pad = (size_t)(per_cu / 2 + 1024);
+  if (pad > (size_t)per_block) pad = 0;
+  cache[dev].store((long long)pad + 1, std::memory_order_relaxed);
+  return pad;
+}
+
 // Token counts above this are refused: several grids put one block (or one
 // per 16 tokens) in a 32-bit grid dimension, which must not wrap.
 constexpr int64_t kMaxTokens = 2147483647;

@@ -596,11 +596,12 @@ static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
     }
   }
   const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1, kPostFwdBlockWaves));
+  const size_t lds = one_block_per_cu_lds();  // one token per CU at a time: 2.6% faster at c5
   if (vec)
-    hipLaunchKernelGGL((post_fwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)x, h_res,
+    hipLaunchKernelGGL((post_fwd_block_kernel<N, S, true>), gs, bs, lds, st, (const S*)x, h_res,
                        (const S*)h_out, h_post, (S*)y, D);
   else
-    hipLaunchKernelGGL((post_fwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)x, h_res,
+    hipLaunchKernelGGL((post_fwd_block_kernel<N, S, false>), gs, bs, lds, st, (const S*)x, h_res,
                        (const S*)h_out, h_post, (S*)y, D);
   return check_launch("post_fwd_block");
 }

@@ -694,10 +694,11 @@ template <int N>
 static int launch_pre_fwd_y(const PreFwdArgs& a, hipStream_t st) {
   const int chunks = (a.D + 511) / 512;
   const dim3 grid((unsigned)a.T), block(kWave * (chunks < kFwdYWaves ? chunks : kFwdYWaves));
+  const size_t lds = one_block_per_cu_lds();  // one token per CU at a time: 2% faster at c5
   if (a.x_scaled)
-    hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), grid, block, lds, st, a);
   else
-    hipLaunchKernelGGL((pre_fwd_y_kernel<N, false>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((pre_fwd_y_kernel<N, false>), grid, block, lds, st, a);
   return check_launch("pre_fwd_y");
 }
 
