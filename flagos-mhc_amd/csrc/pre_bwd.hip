@@ -648,14 +648,29 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   // until compute_tile: a clamped x row meets zero columns of g (kernel A
   // zero-fills the padding tokens of the last tile), clamped gm rows and
   // coefficients only reach outputs of tokens >= T, which are not stored.
-  auto load_tile = [&](int64_t tile, Tile& tl) {
+  // With one phi plane the x / grad_y rows (HBM) are loaded one tile ahead,
+  // after the current tile's workspace operands (L2): vector loads complete
+  // in issue order, so waiting for those operands leaves the next rows in
+  // flight (N = 8, D = 2048: 1.49 -> 1.34 ms for the backward on MI355X).  A
+  // whole second tile of operands would not fit the 256 VGPRs of two waves
+  // per SIMD; with two phi planes even the rows spill (1.78 -> 2.14 ms), so
+  // that form loads a tile and then computes it.
+  auto load_rows = [&](int64_t tile, Row* xr, Row* gr) {
+    const int64_t tg = tile * TT + 4 * q;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t t = tg + e;
+      const int64_t tc = t < T ? t : T - 1;
+      xr[e] = __builtin_nontemporal_load(reinterpret_cast<const Row*>(a.x + (tc * N + n) * D + dlc));
+      gr[e] = *reinterpret_cast<const Row*>(a.gy + tc * D + dlc);
+    }
+  };
+  auto load_operands = [&](int64_t tile, Tile& tl) {
     const int64_t tb = tile * TT, tg = tb + 4 * q;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t t = tg + e;
       const int64_t tc = t < T ? t : T - 1;
-      tl.xr[e] = __builtin_nontemporal_load(reinterpret_cast<const Row*>(a.x + (tc * N + n) * D + dlc));
-      tl.gr[e] = *reinterpret_cast<const Row*>(a.gy + tc * D + dlc);
       tl.cf[e] = a.coef[tc * N + n];
     }
     const int64_t ts = tb + r;  // token of MFMA row r in the gs product
@@ -722,10 +737,27 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   };
 
   const int64_t ntiles = (T + TT - 1) / TT;
-  Tile A;
-  for (int64_t tile = blockIdx.y; tile < ntiles; tile += a.nsplit) {
-    load_tile(tile, A);
-    compute_tile(tile, A);
+  if constexpr (P == 1) {
+    Row xn[4], gn[4];  // rows of the next tile
+    if (blockIdx.y < ntiles) load_rows(blockIdx.y, xn, gn);
+    for (int64_t tile = blockIdx.y; tile < ntiles; tile += a.nsplit) {
+      Tile A;
+      load_operands(tile, A);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        A.xr[e] = xn[e];
+        A.gr[e] = gn[e];
+      }
+      if (tile + a.nsplit < ntiles) load_rows(tile + a.nsplit, xn, gn);
+      compute_tile(tile, A);
+    }
+  } else {
+    for (int64_t tile = blockIdx.y; tile < ntiles; tile += a.nsplit) {
+      Tile A;
+      load_rows(tile, A.xr, A.gr);
+      load_operands(tile, A);
+      compute_tile(tile, A);
+    }
   }
 
   if (!colok) return;

@@ -328,11 +328,16 @@ __device__ __forceinline__ u32x4 pre_sh4(uint32_t a) {
 // 1 KB units.
 // N = 4: two blocks per CU, each with a 3-slot ring (2 x 79 KB of LDS),
 // measured 2% faster than one block with 4 slots; N = 8 fits one block.
+// N = 8 (80 phi rows, 36 KB slots, one block per CU): the tile's mixes go
+// into the slot of its last stage instead of a buffer of their own, which
+// leaves room for a fourth slot (3 stages of x in flight instead of 2).
 template <int N> struct FwdDmaCfg {
   static constexpr int MT = PreDims<N>::MT;
   static constexpr int UNITS = 16 + 4 * MT;
-  static constexpr int S = 3;                       // slots (LDS: S * UNITS KB + mixes)
+  static constexpr bool MIX_IN_RING = N != 4;
+  static constexpr int S = MIX_IN_RING ? 4 : 3;      // slots (LDS: S * UNITS KB [+ mixes])
   static constexpr int BLOCKS_PER_CU = N == 4 ? 2 : 1;
+  static_assert(!MIX_IN_RING || PreDims<N>::M + 1 <= UNITS * 1024 / 4 / 64, "mixes fit a slot");
 };
 
 // SPLIT: block (tile, s) runs contraction stages [s * split_stages, ..) of
@@ -351,7 +356,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   constexpr int VM_C = (S - 2) * CI;
   static_assert(N % 4 == 0 && VM_C < 64, "vmcnt range");
   __shared__ u32x4 ring[S * UNITS * kWave];
-  __shared__ float mix_sh[TT][M + 1];
+  __shared__ float mix_own[C::MIX_IN_RING ? 1 : TT][M + 1];
   __shared__ __align__(16) float inv_sh[TT];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -522,6 +527,13 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
       ssq += __shfl_xor(ssq, 16, kWave);
       ssq += __shfl_xor(ssq, 32, kWave);
       const float inv_row = 1.0f / sqrtf(ssq / (float)K + a.norm_eps);
+      float(*mix_sh)[M + 1] = mix_own;
+      if constexpr (C::MIX_IN_RING) {
+        // this stage's slot, once every wave has read its operands from it;
+        // the next loads into it are issued after the closing barrier
+        __syncthreads();
+        mix_sh = reinterpret_cast<float(*)[M + 1]>(ring + (size_t)(j % S) * UNITS * kWave);
+      }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float inv = __shfl(inv_row, 4 * q + v, kWave);
