@@ -328,16 +328,19 @@ __device__ __forceinline__ u32x4 pre_sh4(uint32_t a) {
 // 1 KB units.
 // N = 4: two blocks per CU, each with a 3-slot ring (2 x 79 KB of LDS),
 // measured 2% faster than one block with 4 slots; N = 8 fits one block.
-// N = 8 (80 phi rows, 36 KB slots, one block per CU): the tile's mixes go
-// into the slot of its last stage instead of a buffer of their own, which
-// leaves room for a fourth slot (3 stages of x in flight instead of 2).
+// N = 8 (80 phi rows, 36 KB slots, one block per CU): heads and Sinkhorn of
+// a 64-token tile take 16 passes of 4 tokens (a wave per 8 x 8 token), which
+// stalled the block's ring for a third of its time (contraction 400 -> 254
+// us without them at D = 2048, T = 32768).  The persistent kernel therefore
+// writes each tile's sums to the workspace and the split form's token-
+// parallel finalize kernel runs heads and Sinkhorn over all tokens; without
+// the mixes buffer a fourth ring slot fits (3 stages of x in flight).
 template <int N> struct FwdDmaCfg {
   static constexpr int MT = PreDims<N>::MT;
   static constexpr int UNITS = 16 + 4 * MT;
-  static constexpr bool MIX_IN_RING = N != 4;
-  static constexpr int S = MIX_IN_RING ? 4 : 3;      // slots (LDS: S * UNITS KB [+ mixes])
+  static constexpr bool HEADS_APART = N != 4;
+  static constexpr int S = HEADS_APART ? 4 : 3;      // slots (LDS: S * UNITS KB [+ mixes])
   static constexpr int BLOCKS_PER_CU = N == 4 ? 2 : 1;
-  static_assert(!MIX_IN_RING || PreDims<N>::M + 1 <= UNITS * 1024 / 4 / 64, "mixes fit a slot");
 };
 
 // SPLIT: block (tile, s) runs contraction stages [s * split_stages, ..) of
@@ -356,7 +359,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   constexpr int VM_C = (S - 2) * CI;
   static_assert(N % 4 == 0 && VM_C < 64, "vmcnt range");
   __shared__ u32x4 ring[S * UNITS * kWave];
-  __shared__ float mix_own[C::MIX_IN_RING ? 1 : TT][M + 1];
+  __shared__ float mix_sh[C::HEADS_APART ? 1 : TT][M + 1];
   __shared__ __align__(16) float inv_sh[TT];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -504,8 +507,9 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] += part[mt];
 
-    if (SPLIT && cs == per_tile - 1) {
-      // ---- this split's partial sums of the tile --------------------------
+    if ((SPLIT || C::HEADS_APART) && cs == per_tile - 1) {
+      // ---- this split's partial sums of the tile (or, persistent with
+      // HEADS_APART, the tile's sums: blockIdx.y = 0) ----------------------
       // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; after
       // the shuffles the lanes of row r hold this split's sum(x^2) of token
       // 16*wave + r
@@ -520,20 +524,18 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
           if (tok < T && 16 * mt + r < M) a.part[(pbase + tok) * M + 16 * mt + r] = acc[mt][v];
       }
       if (q == 0 && tb + 16 * wave + r < T) a.part_ssq[pbase + tb + 16 * wave + r] = ssq;
-    } else if (!SPLIT && cs == nst_c - 1) {
+      if constexpr (!SPLIT) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ssq = 0.f;
+      }
+    } else if (!SPLIT && !C::HEADS_APART && cs == nst_c - 1) {
       // ---- tile's mixes, heads and Sinkhorn -----------------------------
       // acc: lane (r, q) holds token 16*wave + 4q + v, m = 16*mt + r; the
       // lane of row r (any q) holds sum(x^2) of token 16*wave + r
       ssq += __shfl_xor(ssq, 16, kWave);
       ssq += __shfl_xor(ssq, 32, kWave);
       const float inv_row = 1.0f / sqrtf(ssq / (float)K + a.norm_eps);
-      float(*mix_sh)[M + 1] = mix_own;
-      if constexpr (C::MIX_IN_RING) {
-        // this stage's slot, once every wave has read its operands from it;
-        // the next loads into it are issued after the closing barrier
-        __syncthreads();
-        mix_sh = reinterpret_cast<float(*)[M + 1]>(ring + (size_t)(j % S) * UNITS * kWave);
-      }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const float inv = __shfl(inv_row, 4 * q + v, kWave);
@@ -732,6 +734,14 @@ struct FwdSplitPlan {
 };
 
 
+// Workspace of the persistent form when heads run in the finalize kernel
+// (N = 8): the tiles' sums [T][M] and sum(x^2) [T], then pre and inv_rms.
+static size_t heads_apart_bytes(int64_t T, int N) {
+  if (N == 4 || T <= 0) return 0;
+  const int M = 2 * N + N * N;
+  return align256((size_t)T * M * 4) + align256((size_t)T * 4) + fwd_y_ws_bytes(T, N);
+}
+
 static FwdSplitPlan fwd_split_plan(int64_t T, int N, int D) {
   FwdSplitPlan p;
   const int64_t ntiles = (T + kFwdTile - 1) / kFwdTile;
@@ -782,8 +792,16 @@ static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_by
     if ((rc = check_launch("pre_fwd_finalize"))) return rc;
     return launch_pre_fwd_y<N>(a, st);
   }
-  // contraction and heads in one persistent kernel, then y
+  // contraction and heads in one persistent kernel (N = 8: contraction, then
+  // heads in the finalize kernel), then y
   char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
+  if constexpr (FwdDmaCfg<N>::HEADS_APART) {  // the caller checked heads_apart_bytes
+    const int M = 2 * N + N * N;
+    a.part = reinterpret_cast<float*>(w);
+    w += align256((size_t)a.T * M * 4);
+    a.part_ssq = reinterpret_cast<float*>(w);
+    w += align256((size_t)a.T * 4);
+  }
   a.pre_ws = reinterpret_cast<float*>(w);
   a.inv_ws = reinterpret_cast<float*>(w + align256((size_t)a.T * N * 4));
   const int64_t cus = device_cu_count();
@@ -792,6 +810,12 @@ static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_by
   hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   int rc = check_launch("pre_fwd_dma");
   if (rc) return rc;
+  if constexpr (FwdDmaCfg<N>::HEADS_APART) {
+    constexpr int TPP = kFwdThreads / (N * N);
+    hipLaunchKernelGGL((pre_fwd_finalize_kernel<N>), dim3((unsigned)((a.T + TPP - 1) / TPP)), dim3(kFwdThreads),
+                       0, st, a, 1);
+    if ((rc = check_launch("pre_fwd_finalize"))) return rc;
+  }
   return launch_pre_fwd_y<N>(a, st);
 }
 
@@ -834,7 +858,9 @@ extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, in
   const int64_t K = (int64_t)N * D;
   if (phi_dtype == MHC_DTYPE_BF16 && K % 8 == 0) {  // phi used directly: pre / inv_rms for the y
     const size_t split = fwd_split_plan(T, N, D).bytes;  // kernel, split-K partials for few tiles
-    const size_t y = fwd_y_ws_bytes(T < 0 ? 0 : T, N);
+    size_t y = fwd_y_ws_bytes(T < 0 ? 0 : T, N);
+    const size_t ha = heads_apart_bytes(T, N);           // N = 8: tile sums for the finalize kernel
+    if (ha > y) y = ha;
     return kPreFwdWsBase + (split > y ? split : y);
   }
   return align256(phi_planes_bytes(phi_dtype, M, K));
@@ -883,8 +909,9 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   a.T = T;
   a.D = D;
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(y) && (!x_scaled || aligned16(x_scaled));
-  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec) && workspace &&
-      workspace_bytes >= kPreFwdWsBase + fwd_y_ws_bytes(T, N))
+  const size_t y_ws = fwd_y_ws_bytes(T, N), ha_ws = heads_apart_bytes(T, N);
+  const size_t dma_ws = kPreFwdWsBase + (ha_ws > y_ws ? ha_ws : y_ws);
+  if (fwd_dma_usable(a, N, x_dtype == MHC_DTYPE_BF16, vec) && workspace && workspace_bytes >= dma_ws)
     return N == 4 ? launch_pre_fwd_dma<4>(a, workspace, workspace_bytes, st)
                   : launch_pre_fwd_dma<8>(a, workspace, workspace_bytes, st);
   switch (x_dtype) {
