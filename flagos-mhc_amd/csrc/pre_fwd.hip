@@ -707,8 +707,12 @@ __global__ __launch_bounds__(kWave * kFwdYWaves) void pre_fwd_y_kernel(PreFwdArg
 template <int N>
 static int launch_pre_fwd_y(const PreFwdArgs& a, hipStream_t st) {
   const int chunks = (a.D + 511) / 512;
-  const dim3 grid((unsigned)a.T), block(kWave * (chunks < kFwdYWaves ? chunks : kFwdYWaves));
-  const size_t lds = one_block_per_cu_lds();  // one token per CU at a time: 2% faster at c5
+  const int waves = chunks < kFwdYWaves ? chunks : kFwdYWaves;
+  const dim3 grid((unsigned)a.T), block(kWave * waves);
+  // Blocks of 12 or more waves run one token per CU at a time (D = 6144 /
+  // 7168: 1.5% / 2% faster); narrower ones faster several to a CU (D = 4096:
+  // 267 -> 247 us for the operator at T = 16384; D = 5120: 2%).
+  const size_t lds = waves >= 12 ? one_block_per_cu_lds() : 0;
   if (a.x_scaled)
     hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), grid, block, lds, st, a);
   else
