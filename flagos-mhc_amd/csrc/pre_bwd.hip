@@ -774,19 +774,21 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 }
 
 // ---------------------------------------------------------------------------
-// Kernel B, LDS-pipelined form (N = 4, bf16 activations, 16-byte rows)
+// Kernel B, LDS-pipelined form (N = 4 / 8, bf16 activations, 16-byte rows)
 //
 // Same per-lane arithmetic as the streaming form, but the operands of a
 // 16-token tile reach the lanes through a ring of S stages in LDS filled by
 // direct-to-LDS loads (buffer_load ... lds / global_load_lds): a tile's
 // loads are issued S-1 tiles before it is computed and cost no registers
-// while in flight, so one block of N waves per CU keeps ~(S-1) x 25 KB of
-// reads outstanding.  Each direct load moves 16 bytes per lane to
-// LDS[unit + 16*lane]; a lane later reads back exactly what the same lane
-// index loaded, so every LDS read is a conflict-free 16-byte row.
+// while in flight, so one block of 4 waves per CU keeps ~(S-1) x 25 KB
+// (N = 4) / 32 KB (N = 8) of reads outstanding.  Each direct load moves 16
+// bytes per lane to LDS[unit + 16*lane]; a lane later reads back exactly what
+// the same lane index loaded, so every LDS read is a conflict-free 16-byte
+// row (the coefficients unit excepted: 4 tokens x 4 streams per 64 bytes).
 //
-// Block (cb, split) owns the DW = 128 columns cb*DW.. of every stream and
-// the tiles split, split + nsplit, ...; blocks of one split read
+// Block (cb, group, split) owns the DW = 128 columns cb*DW.. of the 4
+// streams of its group and the tiles split, split + nsplit, ...; blocks of
+// one split read
 // neighbouring columns of the same token rows at about the same time, which
 // measured faster than giving every block an equal contiguous share of the
 // (column block, tile) items.
@@ -802,25 +804,32 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 // loads); grad_mixes rows and coefficients of tokens >= T load from the
 // clamped last token and only reach outputs that are not stored.
 // ---------------------------------------------------------------------------
+// A block owns G = 4 streams (a wave each): N = 8 runs two stream groups
+// per column block (blockIdx.x = cb * NG + group), which keeps the phi^T
+// operands (VC x MK x P registers) and grad_phi accumulators (MT x VC) of a
+// wave within one wave per SIMD.
 template <int N> struct DmaCfg {
   using PD = PreDims<N>;
+  static constexpr int G = 4, NG = N / G;
   static constexpr int VC = 8, VD = 4, DW = 128, TT = 16;
   static constexpr int MK = PD::MK, MT = PD::MT;
   // 1 KB units of one stage (16 bytes per lane)
-  static constexpr int X = 0;              // [N][4]  x rows: stream n, tokens 4q+e
-  static constexpr int GY = X + 4 * N;     // [4]     grad_y rows, tokens 4q+e
+  static constexpr int X = 0;              // [G][4]  x rows: stream G*group + w, tokens 4q+e
+  static constexpr int GY = X + 4 * G;     // [4]     grad_y rows, tokens 4q+e
   static constexpr int GA = GY + 4;        // [MK][2] grad_mixes rows (A of gs), hi/lo
   static constexpr int GT = GA + 2 * MK;   // [MT]    g^T blocks (A of grad_phi), both planes
-  static constexpr int CF = GT + MT;       // [N/4]   coefficients of 16 tokens x N streams
-  static constexpr int UNITS = CF + N / 4;
-  static constexpr int GI = UNITS;               // [N][4]  grad_x_in rows (accumulating form)
-  static constexpr int UNITS_ACC = GI + 4 * N;
+  static constexpr int CF = GT + MT;       // [1]     coefficients of 16 tokens x G streams
+  static constexpr int UNITS = CF + 1;
+  static constexpr int GI = UNITS;               // [G][4]  grad_x_in rows (accumulating form)
+  static constexpr int UNITS_ACC = GI + 4 * G;
   static constexpr int SHARED = UNITS - GY;      // units loaded once per block, split over waves
-  static constexpr int LMIN = 4 + SHARED / N;    // fewest loads a wave issues per tile
+  static constexpr int LMIN = 4 + SHARED / G;    // fewest loads a wave issues per tile
+  static constexpr int RA = (2 * MK + MT + 3) / 4 * 4;  // units from GA read per tile (4 at a time)
+  static constexpr int STAGES = N == 4 ? 5 : 4;  // ring: 125 KB (N = 4) / 128 KB (N = 8) of LDS
+  static_assert(N % G == 0 && GA + RA <= UNITS, "stream groups; reads stay in the slot");
 };
 
-constexpr int kDmaStages = 5;                  // 125 KB of LDS: one block per CU
-constexpr int kDmaAccStages = 3;               // accumulating form: 3 x 41 KB
+constexpr int kDmaAccStages = 3;               // accumulating form: 3 x 41 KB (N = 4) / 48 KB (N = 8)
 constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
 
 struct PreBwdDmaArgs {
@@ -841,7 +850,7 @@ struct PreBwdDmaArgs {
 };
 
 template <int N, int P, int S, bool ACC>
-__global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
+__global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
   using C = DmaCfg<N>;
   using PD = PreDims<N>;
   constexpr int M = PD::M, MT = PD::MT, MK = PD::MK, MP32 = PD::MP32;
@@ -850,18 +859,20 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
   constexpr int LMIN = C::LMIN + (ACC ? 4 : 0);             // grad_x_in: 4 more loads a wave
   constexpr int VM_START = (S - 2) * LMIN;                  // before any grad_x store
   constexpr int VM_STEADY = (S - 2) * LMIN + (S - 1) * 4;
-  static_assert(N == 4 && S >= 2 && VM_STEADY < 64, "pipeline shape");
+  static_assert(S >= 2 && VM_STEADY < 64, "pipeline shape");
   __shared__ u32x4 ring[S * UNITS * kWave];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int n = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave: stream of the group
+  const int grp = (int)(blockIdx.x % C::NG), cb = (int)(blockIdx.x / C::NG);
+  const int n = grp * C::G + w;
   const int r = lane & 15, q = lane >> 4;
   const int D = a.D;
   const int64_t T = a.T, K = (int64_t)N * D, ntiles = a.ntiles;
   const int64_t tstep = gridDim.y;
   const int64_t cnt = (ntiles - blockIdx.y + tstep - 1) / tstep;
   if (cnt <= 0) return;  // uniform over the block
-  const int dl = blockIdx.x * DW + VC * r;  // first column of this lane
+  const int dl = cb * DW + VC * r;  // first column of this lane
   const bool colok = dl < D;
 
   int64_t itile = blockIdx.y;  // next tile to load
@@ -874,7 +885,7 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(st + (C::X + 4 * n + e) * kWave), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(st + (C::X + 4 * w + e) * kWave), 16,
                                                off, 0, 0, 2 /* nt */);
     }
     if constexpr (ACC) {
@@ -882,11 +893,11 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ri, (lds_void_t*)(st + (C::GI + 4 * n + e) * kWave), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ri, (lds_void_t*)(st + (C::GI + 4 * w + e) * kWave), 16,
                                                  off, 0, 0, 2 /* nt */);
       }
     }
-    for (int u = n; u < C::SHARED; u += N) {
+    for (int u = w; u < C::SHARED; u += C::G) {
       const int unit = C::GY + u;
       lds_void_t* dst = (lds_void_t*)(st + unit * kWave);
       if (unit < C::GA) {
@@ -903,9 +914,8 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
         const int mt = unit - C::GT;
         __builtin_amdgcn_global_load_lds((glb_void_t*)(a.gTw + ((tile * MT + mt) * kWave + lane) * 8), dst,
                                          16, 0, 0);
-      } else {
-        const int i = unit - C::CF;
-        int64_t idx = tb * N + i * kWave + lane;
+      } else {  // token lane / G, stream G * group + lane % G
+        int64_t idx = (tb + lane / C::G) * N + grp * C::G + lane % C::G;
         if (idx > T * N - 1) idx = T * N - 1;
         __builtin_amdgcn_global_load_lds((glb_void_t*)(a.coef + idx), dst, 16, 0, 0);
       }
@@ -960,21 +970,24 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
 
     const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
     const uint32_t la = sbase + lane * 16;
-    static_assert(MK == 1 && MT == 2 && C::GY + 4 == C::GA && C::GA + 2 == C::GT, "unit order read below");
     u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
-    lds_read4<1024>(xr, la + (C::X + 4 * n) * 1024);  // x rows of stream n, tokens 4q+e
+    lds_read4<1024>(xr, la + (C::X + 4 * w) * 1024);  // x rows of stream n, tokens 4q+e
     lds_read4<1024>(gr, la + C::GY * 1024);           // grad_y rows
     {
-      u32x4 ag[4];                                    // grad_mixes hi, lo; g^T blocks mt = 0, 1
-      lds_read4<1024>(ag, la + C::GA * 1024);
-      gA[0][0] = ag[0];
-      gA[0][1] = ag[1];
-      gt[0] = ag[2];
-      gt[1] = ag[3];
+      u32x4 ag[C::RA / 4][4];  // units GA.. four at a time: grad_mixes hi, lo per mk, then g^T blocks
+#pragma unroll
+      for (int i = 0; i < C::RA / 4; ++i) lds_read4<1024>(ag[i], la + (C::GA + 4 * i) * 1024);
+#pragma unroll
+      for (int mk = 0; mk < MK; ++mk) {
+        gA[mk][0] = ag[(2 * mk) / 4][(2 * mk) % 4];
+        gA[mk][1] = ag[(2 * mk + 1) / 4][(2 * mk + 1) % 4];
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) gt[mt] = ag[(2 * MK + mt) / 4][(2 * MK + mt) % 4];
     }
-    lds_read4<N * 16>(cfu, sbase + C::CF * 1024 + (4 * q * N + n) * 16);  // tokens 4q+e, stream n
+    lds_read4<C::G * 16>(cfu, sbase + C::CF * 1024 + (4 * q * C::G + w) * 16);  // tokens 4q+e, stream n
     u32x4 gi[4];
-    if constexpr (ACC) lds_read4<1024>(gi, la + (C::GI + 4 * n) * 1024);  // grad_x_in rows, tokens 4q+e
+    if constexpr (ACC) lds_read4<1024>(gi, la + (C::GI + 4 * w) * 1024);  // grad_x_in rows, tokens 4q+e
 
     const int64_t tb = ctile * TT;
     const int nv = (int)(T - tb < TT ? T - tb : TT);
@@ -1535,18 +1548,18 @@ static int reduce_tail(const BwdLayout& lay, const PreBwdSmallArgs& sa, float* g
 // Buffer ranges are 32-bit: one tile of x rows (16 * N * D bf16) must fit.
 template <int N>
 static bool dma_usable(int D) {
-  return N == 4 && (int64_t)DmaCfg<N>::TT * N * D * 2 < ((int64_t)1 << 31);
+  return (N == 4 || N == 8) && (int64_t)DmaCfg<N>::TT * N * D * 2 < ((int64_t)1 << 31);
 }
 
 // Launches the LDS-pipelined kernel; *nsplit receives its token-split count.
 template <int N, int P>
 static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* nsplit, hipStream_t st) {
-  constexpr int DW = DmaCfg<N>::DW;
+  constexpr int DW = DmaCfg<N>::DW, NG = DmaCfg<N>::NG;
   const int D = sta.D;
   const int64_t ncb = (D + DW - 1) / DW;
   // one block per CU (the ring fills the LDS); as many token splits as fit
-  // next to the column blocks in one wave of blocks
-  int64_t ns = device_cu_count() / ncb;
+  // next to the (column block, stream group) blocks in one wave of blocks
+  int64_t ns = device_cu_count() / (ncb * NG);
   if (ns > dma_max_splits(D)) ns = dma_max_splits(D);
   if (ns > lay.ntiles) ns = lay.ntiles;
   if (ns < 1) ns = 1;
@@ -1565,12 +1578,11 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* ns
   da.T = sta.T;
   da.D = D;
   da.ntiles = lay.ntiles;
+  const dim3 grid((unsigned)(ncb * NG), (unsigned)ns), block(64 * DmaCfg<N>::G);
   if (sta.gin)
-    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), dim3((unsigned)ncb, (unsigned)ns),
-                       dim3(64 * N), 0, st, da);
+    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), grid, block, 0, st, da);
   else
-    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaStages, false>), dim3((unsigned)ncb, (unsigned)ns),
-                       dim3(64 * N), 0, st, da);
+    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, DmaCfg<N>::STAGES, false>), grid, block, 0, st, da);
   *nsplit = (int)ns;
   return check_launch("pre_bwd_dma");
 }
@@ -1619,14 +1631,12 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
     hipLaunchKernelGGL((pre_bwd_small_kernel<N, S, false>), gA, bA, 0, st, sa);
   rc = check_launch("pre_bwd_small");
   if (rc) return rc;
-  if constexpr (N == 4) {
-    if (streaming && dma_usable<N>(sta.D)) {
-      sta.gin = static_cast<const bf16_t*>(gin);  // accumulated inside the kernel
-      int ns = 0;
-      rc = lay.P == 1 ? launch_dma<N, 1>(lay, sta, &ns, st) : launch_dma<N, 2>(lay, sta, &ns, st);
-      if (rc) return rc;
-      return reduce_tail<N, S>(lay, sa, sta.gphi_part, ns, gpl, grad_phi, grad_alpha, grad_base, st);
-    }
+  if (streaming && dma_usable<N>(sta.D)) {
+    sta.gin = static_cast<const bf16_t*>(gin);  // accumulated inside the kernel
+    int ns = 0;
+    rc = lay.P == 1 ? launch_dma<N, 1>(lay, sta, &ns, st) : launch_dma<N, 2>(lay, sta, &ns, st);
+    if (rc) return rc;
+    return reduce_tail<N, S>(lay, sa, sta.gphi_part, ns, gpl, grad_phi, grad_alpha, grad_base, st);
   }
   const int64_t nx = sta.T * N * (int64_t)sta.D;
   if (streaming) {

@@ -209,7 +209,7 @@ def test_pre_bwd_parity(T, N, D, dtype, phi_dtype, recipe, clamp, iters):
 @pytest.mark.parametrize("T,N,D,dtype", [
     (1000, 4, 1024, torch.bfloat16),    # LDS-pipelined kernel, grad_x_in accumulated in place
     (4133, 4, 7168, torch.bfloat16),
-    (70, 8, 256, torch.bfloat16),       # streaming kernel + separate add
+    (70, 8, 256, torch.bfloat16),       # LDS-pipelined kernel, two stream groups, grad_x_in in place
     (40, 4, 100, torch.bfloat16),       # D % 8 != 0: generic kernel + separate add
     (33, 4, 64, torch.float32),
 ])
