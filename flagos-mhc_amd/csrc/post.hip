@@ -595,10 +595,12 @@ static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
       return check_launch("post_fwd_dma");
     }
   }
-  const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1, kPostFwdBlockWaves));
-  // one token per CU at a time (D >= 5120 here): 2.6% faster at D = 7168,
-  // 1.6% at D = 5120
-  const size_t lds = one_block_per_cu_lds();
+  const int waves = post_block_waves(D, vec ? Store<S>::VEC : 1, kPostFwdBlockWaves);
+  const dim3 gs((unsigned)T), bs(kWave * waves);
+  // Blocks of 10 or more waves run one token per CU at a time (D = 7168 /
+  // 5120: 2.6% / 1.6% faster); narrower ones (N = 8 takes this kernel at
+  // every D) several to a CU (N = 8, D = 2048: 440 -> 376 us at T = 32768).
+  const size_t lds = waves >= 10 ? one_block_per_cu_lds() : 0;
   if (vec)
     hipLaunchKernelGGL((post_fwd_block_kernel<N, S, true>), gs, bs, lds, st, (const S*)x, h_res,
                        (const S*)h_out, h_post, (S*)y, D);
