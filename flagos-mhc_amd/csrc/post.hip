@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void post_bwd_kernel(
 // wave per token a call with few tokens runs a handful of waves, each
 // streaming its whole token serially (T = 1, N = 4, D = 7168: 11 us forward,
 // 19 us backward, against 3.3 and 6.4 us here).  At large T the block forms
-// also beat the LDS-pipelined kernels below for D >= 5120 (c5 width on one
+// also beat the LDS-pipelined kernels below for D >= 5120 (D = 7168 on one
 // MI355X: backward 2.23 against 2.50 ms, forward 1.48 against 1.60 ms): only
 // a few tokens per CU are in flight, each read as a few long contiguous
 // streams.  Inputs are read once, so loads are non-temporal (measured 3-7%

@@ -41,7 +41,8 @@
 // kernel.  The y pass used to run as stages of this kernel (8 tokens x 4
 // streams x 512 columns each, which needed D >= 3136 so that a y stage's
 // loads followed the stores of its columns); as the block-per-token kernel
-// it is faster (c5: 2.55 -> 2.26 ms for the fused forward on one MI355X).
+// it is faster (N = 4, D = 7168, T = 65536: 2.55 -> 2.26 ms for the fused
+// forward on one MI355X).
 #include "mhc_launch.hpp"
 #include "pre_common.hpp"
 #include "pre_host.hpp"

@@ -179,7 +179,7 @@ def test_post_bf16_rounding_bit_exact():
 
 
 def test_post_identity_gates_full_size():
-    """h_res = I, h_post = 0 => y == x bit for bit (c5 width)."""
+    """h_res = I, h_post = 0 => y == x bit for bit (D = 7168)."""
     T, N, D = 8192, 4, 7168
     x, _, h_out, _, _ = post_inputs(T, N, D, torch.bfloat16)
     eye = torch.eye(N, device=DEV).expand(T, N, N).contiguous()

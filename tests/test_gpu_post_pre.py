@@ -51,7 +51,7 @@ CASES = [
     (1000, 4, 4096, torch.bfloat16),    # fused kernel
     (333, 4, 3136, torch.bfloat16),     # fused, partial last 512-column y chunk, ragged tile
     (200, 4, 3584, torch.bfloat16),     # fused
-    (4133, 4, 7168, torch.bfloat16),    # fused, c5 width, several tiles per block
+    (4133, 4, 7168, torch.bfloat16),    # fused, D = 7168, several tiles per block
     (31, 4, 7168, torch.bfloat16),      # fused, one partial tile
     (65536, 4, 7168, torch.bfloat16),   # fused, config 5 (bench shape)
     (2000, 4, 3072, torch.bfloat16),    # fused

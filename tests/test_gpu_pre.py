@@ -295,7 +295,7 @@ def test_pre_bwd_compensated(T, N, D, dtype, recipe):
 
 
 def test_pre_bwd_compensated_c5_width():
-    """c5 width (K = 28672: 224 column blocks, several token splits): the
+    """D = 7168 (K = 28672: 224 column blocks, several token splits): the
     compensated grad_phi agrees with the default path's to its accuracy, and
     the autograd wrapper forwards the option."""
     T, N, D = 4133, 4, 7168
