@@ -29,8 +29,10 @@ namespace mhc {
 
 constexpr int kPostWavesPerBlock = 4;
 
-template <int N, typename S, bool VECTOR>
-__global__ __launch_bounds__(256) void post_bwd_kernel(
+// MINW: waves per SIMD the register allocation must allow (2 caps the
+// kernel at 256 VGPRs).
+template <int N, typename S, bool VECTOR, int MINW = 1>
+__global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
     const S* __restrict__ gy, const S* __restrict__ x, const float* __restrict__ h_res,
     const S* __restrict__ h_out, const float* __restrict__ h_post, S* __restrict__ gx,
     float* __restrict__ g_hres, S* __restrict__ g_hout, float* __restrict__ g_hpost,
@@ -639,6 +641,16 @@ static int launch_post_bwd(const void* gy, const void* x, const float* h_res, co
                          (const bf16_t*)x, h_res, (const bf16_t*)h_out, h_post, (bf16_t*)gx, g_hres,
                          (bf16_t*)g_hout, g_hpost, T, D);
       return check_launch("post_bwd_dma");
+    }
+  }
+  if constexpr (N == 8) {
+    // 270 VGPRs leave one wave per SIMD; capped at 256 (a 60-byte spill) two
+    // fit, which pays at narrow rows (D = 2048, T = 32768: 729 -> 629 us) but
+    // not wider ones (D = 4096: 706 -> 756 us; D = 7168: equal)
+    if (vec && D <= 2048) {
+      hipLaunchKernelGGL((post_bwd_kernel<N, S, true, 2>), grid, block, 0, st, (const S*)gy, (const S*)x, h_res,
+                         (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, T, D);
+      return check_launch("post_bwd");
     }
   }
   if (vec)
