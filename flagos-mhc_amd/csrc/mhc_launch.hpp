@@ -58,6 +58,18 @@ inline size_t one_block_per_cu_lds() {
 // per 16 tokens) in a 32-bit grid dimension, which must not wrap.
 constexpr int64_t kMaxTokens = 2147483647;
 
+// A dispatch packet holds the grid size in work-items as 32-bit numbers, so a
+// grid of one block per token of B threads fits up to (2^32 - 1) / B tokens
+// (4.2 M with 1024-thread blocks).  Launches of that form check it first and
+// refuse larger calls instead of relying on the runtime.
+inline int check_grid(const dim3& g, const dim3& b, const char* what) {
+  const uint64_t lim = 0xffffffffull;
+  if ((uint64_t)g.x * b.x > lim || (uint64_t)g.y * b.y > lim || (uint64_t)g.z * b.z > lim)
+    return set_error(MHC_ERR_UNSUPPORTED, "%s: %u x %u x %u blocks of %u x %u x %u threads exceed the 2^32 work-items of a dispatch",
+                     what, g.x, g.y, g.z, b.x, b.y, b.z);
+  return MHC_OK;
+}
+
 inline int check_tokens(int64_t T, const char* who) {
   if (T > kMaxTokens)
     return set_error(MHC_ERR_UNSUPPORTED, "%s: T=%lld above the supported %lld tokens", who, (long long)T,

@@ -603,6 +603,7 @@ static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
   // 5120: 2.6% / 1.6% faster); narrower ones (N = 8 takes this kernel at
   // every D) several to a CU (N = 8, D = 2048: 440 -> 376 us at T = 32768).
   const size_t lds = waves >= 10 ? one_block_per_cu_lds() : 0;
+  if (int rc = check_grid(gs, bs, "mhc_post_fwd")) return rc;
   if (vec)
     hipLaunchKernelGGL((post_fwd_block_kernel<N, S, true>), gs, bs, lds, st, (const S*)x, h_res,
                        (const S*)h_out, h_post, (S*)y, D);
@@ -626,6 +627,7 @@ static int launch_post_bwd(const void* gy, const void* x, const float* h_res, co
   }
   if (block_form) {
     const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1, kPostBlockWaves));
+    if (int rc = check_grid(gs, bs, "mhc_post_bwd")) return rc;
     if (vec)
       hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
                          h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D);

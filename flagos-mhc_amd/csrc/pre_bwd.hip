@@ -6,9 +6,9 @@
 // <grad_y, y> + <grad_post_out, post_out> + <grad_comb_frag, comb_frag>.
 //
 // Kernel A (pre_bwd_small_kernel), a block per 16 tokens:
-//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token;
-//   for T < 16384 summed in fixed order from the partials of
-//   pre_bwd_gpre_kernel, a block per (token, 2048 columns))
+//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token
+//   for N = 4 at T >= 16384; otherwise summed in fixed order from the
+//   partials of pre_bwd_gpre_kernel, a block per (token, 2048 columns))
 //   Sinkhorn / softmax / clamp / sigmoid-head VJP, lane per matrix element
 //   -> grad_mixes (T,M) and scale[t] = -inv^2 * <grad_mixes, mixes> / (N*D)
 //   (because <x, grad_mixes @ phi> = <grad_mixes, mixes> / inv), plus a
@@ -93,39 +93,46 @@ __device__ __forceinline__ void kahan_add(float& s, float& c, float v) {
 // 8 columns, wave_sum, then the 4 waves in order).
 constexpr int kGpreCols = kBwdThreads * 8;
 
+// Blocks in x: at most kGpreGridT, each looping over the tokens
+// blockIdx.x, blockIdx.x + gridDim.x, ..., so the launch stays far below the
+// 2^32 work-items of a dispatch at any T.
+constexpr int64_t kGpreGridT = 65536;
+
 template <int N, typename S, bool VEC>
 __global__ __launch_bounds__(kBwdThreads) void pre_bwd_gpre_kernel(const void* xv, const void* gyv, float* part,
-                                                                   int D) {
+                                                                   int64_t T, int D) {
   __shared__ float red[kBwdThreads / kWave][N];
   const S* __restrict__ x = static_cast<const S*>(xv);
   const S* __restrict__ gy = static_cast<const S*>(gyv);
-  const int64_t tok = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int64_t d = (int64_t)blockIdx.y * kGpreCols + tid * 8;
   const bool ok = d < D;
-  float acc[N];
-  float g8[8];
-  load8f<S, VEC>(gy + tok * D, d, D, ok, g8);
+  for (int64_t tok = blockIdx.x; tok < T; tok += gridDim.x) {  // uniform over the block
+    float acc[N];
+    float g8[8];
+    load8f<S, VEC>(gy + tok * D, d, D, ok, g8);
 #pragma unroll
-  for (int n = 0; n < N; ++n) {
-    float x8[8];
-    load8f<S, VEC>(x + (tok * N + n) * D, d, D, ok, x8);
-    acc[n] = 0.f;
+    for (int n = 0; n < N; ++n) {
+      float x8[8];
+      load8f<S, VEC>(x + (tok * N + n) * D, d, D, ok, x8);
+      acc[n] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
-  }
+      for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
+    }
 #pragma unroll
-  for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
-  if (lane == 0) {
+    for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
+    if (lane == 0) {
 #pragma unroll
-    for (int n = 0; n < N; ++n) red[wave][n] = acc[n];
-  }
-  __syncthreads();
-  if (tid < N) {
-    float s = red[0][tid];
+      for (int n = 0; n < N; ++n) red[wave][n] = acc[n];
+    }
+    __syncthreads();
+    if (tid < N) {
+      float s = red[0][tid];
 #pragma unroll
-    for (int w = 1; w < kBwdThreads / kWave; ++w) s += red[w][tid];
-    part[(tok * gridDim.y + blockIdx.y) * N + tid] = s;
+      for (int w = 1; w < kBwdThreads / kWave; ++w) s += red[w][tid];
+      part[(tok * gridDim.y + blockIdx.y) * N + tid] = s;
+    }
+    __syncthreads();  // red is rewritten for the next token
   }
 }
 
@@ -1621,12 +1628,12 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
   }
   int rc;
   if (sa.gpre_part) {
-    const dim3 gG((unsigned)sa.T, (unsigned)lay.gpre_chunks);
+    const dim3 gG((unsigned)(sa.T < kGpreGridT ? sa.T : kGpreGridT), (unsigned)lay.gpre_chunks);
     float* part = const_cast<float*>(sa.gpre_part);
     if (vec)
-      hipLaunchKernelGGL((pre_bwd_gpre_kernel<N, S, true>), gG, bA, 0, st, sa.x, sa.gy, part, sa.D);
+      hipLaunchKernelGGL((pre_bwd_gpre_kernel<N, S, true>), gG, bA, 0, st, sa.x, sa.gy, part, sa.T, sa.D);
     else
-      hipLaunchKernelGGL((pre_bwd_gpre_kernel<N, S, false>), gG, bA, 0, st, sa.x, sa.gy, part, sa.D);
+      hipLaunchKernelGGL((pre_bwd_gpre_kernel<N, S, false>), gG, bA, 0, st, sa.x, sa.gy, part, sa.T, sa.D);
     if ((rc = check_launch("pre_bwd_gpre"))) return rc;
   }
   if (vec)

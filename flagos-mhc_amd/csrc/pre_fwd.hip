@@ -713,6 +713,7 @@ static int launch_pre_fwd_y(const PreFwdArgs& a, hipStream_t st) {
   // 7168: 1.5% / 2% faster); narrower ones faster several to a CU (D = 4096:
   // 267 -> 247 us for the operator at T = 16384; D = 5120: 2%).
   const size_t lds = waves >= 12 ? one_block_per_cu_lds() : 0;
+  if (int rc = check_grid(grid, block, "mhc_pre_fwd")) return rc;
   if (a.x_scaled)
     hipLaunchKernelGGL((pre_fwd_y_kernel<N, true>), grid, block, lds, st, a);
   else

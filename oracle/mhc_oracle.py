@@ -53,6 +53,7 @@ __all__ = [
     "pre_bwd",
     "sinkhorn_fwd",
     "sinkhorn_bwd",
+    "small_stage_bwd",
 ]
 
 
@@ -195,6 +196,48 @@ def pre_fwd(x, phi, alpha, base, norm_eps=1e-6, hc_eps=1e-6,
     }
 
 
+def small_stage_bwd(mixes, grad_pre, grad_post_out, grad_comb_frag, alpha, base, N,
+                    hc_eps=1e-6, clamp_min=0.0, clamp_max=0.0, iter_times=20):
+    """VJP of the per-token heads, clamp, softmax and Sinkhorn of
+    :func:`pre_fwd` with respect to mixes, alpha and base, given
+    grad_pre = d loss / d pre (T,N) (the reference's ``_small_stage_bwd``,
+    ``src/mhc_pre_clamp_sinkhorn_backward.py:1251-1286``, semantics of the
+    autograd path ``:1428-1453``).
+
+    Returns (grad_mixes (T,M), grad_alpha (3,), grad_base (M,)).  The clamp
+    gradient passes where ``clamp_min <= logit <= clamp_max`` (inclusive, as
+    torch.clamp's backward; ``:1434-1435``).
+    """
+    mixes, grad_pre, alpha, base = map(_f64, (mixes, grad_pre, alpha, base))
+    T = mixes.shape[0]
+    gpost = _f64(grad_post_out).reshape(T, N)
+    gcomb = _f64(grad_comb_frag).reshape(T, N, N)
+    z_pre = mixes[:, :N] * alpha[0] + base[:N]
+    z_post = mixes[:, N:2 * N] * alpha[1] + base[N:2 * N]
+    ml = mixes[:, 2 * N:].reshape(T, N, N)
+    logits = ml * alpha[2] + base[2 * N:].reshape(N, N)
+    clamp = _clamp_enabled(clamp_min, clamp_max)
+    lc = np.clip(logits, clamp_min, clamp_max) if clamp else logits
+    _, saved = sinkhorn_fwd(lc, hc_eps, iter_times, keep_states=True)
+    sp = _sigmoid(z_pre)
+    spo = _sigmoid(z_post)
+    dz_pre = grad_pre * sp * (1.0 - sp)
+    dz_post = gpost * 2.0 * spo * (1.0 - spo)
+    dlc = sinkhorn_bwd(gcomb, saved)
+    if clamp:
+        dlc = dlc * ((logits >= clamp_min) & (logits <= clamp_max))
+    grad_mixes = np.concatenate(
+        [dz_pre * alpha[0], dz_post * alpha[1], (dlc * alpha[2]).reshape(T, N * N)], axis=1)
+    grad_alpha = np.array([
+        (dz_pre * mixes[:, :N]).sum(),
+        (dz_post * mixes[:, N:2 * N]).sum(),
+        (dlc * ml).sum(),
+    ])
+    grad_base = np.concatenate(
+        [dz_pre.sum(axis=0), dz_post.sum(axis=0), dlc.sum(axis=0).reshape(N * N)])
+    return grad_mixes, grad_alpha, grad_base
+
+
 def pre_bwd(x, phi, alpha, base, grad_y, grad_post_out, grad_comb_frag,
             norm_eps=1e-6, hc_eps=1e-6, clamp_min=0.0, clamp_max=0.0,
             iter_times=20, return_intermediates=False):
@@ -219,33 +262,13 @@ def pre_bwd(x, phi, alpha, base, grad_y, grad_post_out, grad_comb_frag,
     inv = 1.0 / np.sqrt((xf * xf).mean(axis=-1) + norm_eps)
     x_scaled = xf * inv[:, None]
     mixes = x_scaled @ phi.T
-    z_pre = mixes[:, :N] * alpha[0] + base[:N]
-    z_post = mixes[:, N:2 * N] * alpha[1] + base[N:2 * N]
-    ml = mixes[:, 2 * N:].reshape(T, N, N)
-    logits = ml * alpha[2] + base[2 * N:].reshape(N, N)
-    clamp = _clamp_enabled(clamp_min, clamp_max)
-    lc = np.clip(logits, clamp_min, clamp_max) if clamp else logits
-    _, saved = sinkhorn_fwd(lc, hc_eps, iter_times, keep_states=True)
-    sp = _sigmoid(z_pre)
-    pre = sp + hc_eps
-    spo = _sigmoid(z_post)
+    pre = _sigmoid(mixes[:, :N] * alpha[0] + base[:N]) + hc_eps
 
     # --- small stage -------------------------------------------------------
     grad_pre = np.einsum("td,tnd->tn", gy, x)             # from y = sum_n x[n] pre[n]
-    dz_pre = grad_pre * sp * (1.0 - sp)
-    dz_post = gpost * 2.0 * spo * (1.0 - spo)
-    dlc = sinkhorn_bwd(gcomb, saved)
-    if clamp:
-        dlc = dlc * ((logits >= clamp_min) & (logits <= clamp_max))
-    grad_mixes = np.concatenate(
-        [dz_pre * alpha[0], dz_post * alpha[1], (dlc * alpha[2]).reshape(T, N * N)], axis=1)
-    grad_alpha = np.array([
-        (dz_pre * mixes[:, :N]).sum(),
-        (dz_post * mixes[:, N:2 * N]).sum(),
-        (dlc * ml).sum(),
-    ])
-    grad_base = np.concatenate(
-        [dz_pre.sum(axis=0), dz_post.sum(axis=0), dlc.sum(axis=0).reshape(N * N)])
+    grad_mixes, grad_alpha, grad_base = small_stage_bwd(
+        mixes, grad_pre, gpost, gcomb, alpha, base, N, hc_eps=hc_eps, clamp_min=clamp_min,
+        clamp_max=clamp_max, iter_times=iter_times)
 
     # --- contraction and RMSNorm backward ---------------------------------
     gs = grad_mixes @ phi                                  # d loss / d x_scaled

@@ -100,4 +100,4 @@ def test_gpu_pre_golden(name, c):
         _t(c["grad_comb_frag"], torch.float32), **kw)
     _close(gx, c["grad_x"], 2e-2, 2e-2, "grad_x")
     for got, k in ((gphi, "grad_phi"), (ga, "grad_alpha"), (gb, "grad_base")):
-        _close(got, c[k], 1e-3, 1e-4 * np.abs(c[k]).max(), k)
+        _close(got, c[k], 1e-4, 1e-5 * np.abs(c[k]).max(), k)

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import FlagOS_mhc as m
+from gpu_ref import close_gpu
 from oracle import mhc_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -70,11 +71,45 @@ def fp32_post_fwd(x, h_res, h_out, h_post):
     return y
 
 
+def check_post_fwd_full(y, x, h_res, h_out, h_post, rtol, atol, chunk=4096):
+    """Whole output against the fp32 restatement, a chunk of tokens at a time."""
+    for s in range(0, x.shape[0], chunk):
+        e = slice(s, s + chunk)
+        close_gpu(y[e], fp32_post_fwd(x[e], h_res[e], h_out[e], h_post[e]), rtol, atol,
+                  f"y vs fp32, tokens {s}..")
+
+
+def check_post_bwd_full(grads, gy, x, h_res, h_out, h_post, rtol, atol, chunk=2048):
+    """Whole outputs of the post backward against an fp32 elementwise
+    restatement on the GPU: grad_x and grad_h_out at the activation dtype's
+    tolerance, the D-long dot products grad_h_res / grad_h_post at rtol 1e-4
+    with atol 1e-4 * max|ref| (fp32 sums of up to 8192 products)."""
+    gx, ghr, gho, ghp = grads
+    N = x.shape[1]
+    refs = {"grad_h_res": [], "grad_h_post": []}
+    for s in range(0, x.shape[0], chunk):
+        e = slice(s, s + chunk)
+        gyf, xf, hr = gy[e].float(), x[e].float(), h_res[e].float()
+        gx_ref = sum(hr[:, :, i].unsqueeze(-1) * gyf[:, i : i + 1, :] for i in range(N))
+        close_gpu(gx[e], gx_ref, rtol, atol, f"grad_x vs fp32, tokens {s}..")
+        gho_ref = sum(h_post[e, i].float().unsqueeze(-1) * gyf[:, i, :] for i in range(N))
+        close_gpu(gho[e], gho_ref, rtol, atol, f"grad_h_out vs fp32, tokens {s}..")
+        refs["grad_h_res"].append(torch.stack(
+            [torch.stack([(xf[:, j] * gyf[:, i]).sum(-1) for i in range(N)], -1) for j in range(N)], 1))
+        refs["grad_h_post"].append((h_out[e].float().unsqueeze(1) * gyf).sum(-1))
+        del gyf, xf
+    for got, name in ((ghr, "grad_h_res"), (ghp, "grad_h_post")):
+        ref = torch.cat(refs[name])
+        close_gpu(got, ref, 1e-4, 1e-4 * float(ref.abs().max()), name + " full")
+
+
 CONFIGS = [
     # (T, N, D, dtype, gates) -- BASELINE configs 1, 2, 4 and the reference test case
     (1024, 4, 256, torch.float32, "softmax"),
     (16384, 4, 4096, torch.bfloat16, "softmax"),
     (32768, 8, 2048, torch.bfloat16, "softmax"),
+    (4133, 4, 7168, torch.bfloat16, "softmax"),    # config-5 width, ragged T
+    (65536, 4, 7168, torch.bfloat16, "softmax"),   # config 5 (64-bit offsets past 2^31 bytes)
     (16, 4, 64, torch.bfloat16, "randn"),
     (40, 4, 100, torch.bfloat16, "randn"),     # D % 8 != 0: scalar path
     (33, 2, 264, torch.float16, "randn"),
@@ -94,7 +129,7 @@ def test_post_fwd_parity(T, N, D, dtype, gates):
     idx = _subset(T)
     want = orc.post_fwd(_np(x[idx]), _np(h_res[idx]), _np(h_out[idx]), _np(h_post[idx]))
     assert_close(y[idx], want, rtol, atol, "y vs oracle")
-    assert_close(y, fp32_post_fwd(x, h_res, h_out, h_post), rtol, atol, "y vs fp32")
+    check_post_fwd_full(y, x, h_res, h_out, h_post, rtol, atol)
     # deterministic
     assert torch.equal(m.mhc_post(x, h_res, h_out, h_post), y)
 
@@ -114,11 +149,7 @@ def test_post_bwd_parity(T, N, D, dtype, gates):
     assert_close(gho[idx], w[2], rtol, atol, "grad_h_out")
     for got, want, name in ((ghr[idx], w[1], "grad_h_res"), (ghp[idx], w[3], "grad_h_post")):
         assert_close(got, want, 1e-4, 1e-4 * np.abs(want).max(), name)
-    # full-size fp32 check of the reductions
-    gyf, xf = gy.float(), x.float()
-    ghr_ref = torch.stack([torch.stack([(xf[:, j] * gyf[:, i]).sum(-1) for i in range(N)], -1)
-                           for j in range(N)], 1)
-    assert_close(ghr, ghr_ref, 1e-4, 1e-4 * ghr_ref.abs().max().item(), "grad_h_res full")
+    check_post_bwd_full((gx, ghr, gho, ghp), gy, x, h_res, h_out, h_post, rtol, atol)
     again = m.mhc_post_backward(gy, x, h_res, h_out, h_post)
     for a, b in zip(again, (gx, ghr, gho, ghp)):
         assert torch.equal(a, b)

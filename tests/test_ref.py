@@ -100,3 +100,60 @@ def test_pre_bwd_ref_autograd_vs_oracle_vjp(rng, N, clamp, iters):
     for g, w in zip(got[1:], want[1:]):
         scale = np.abs(w).max()
         _close(g, w, 1e-3, 1e-4 * scale)
+
+
+def clamp_bound_base(N, c, rng):
+    """base for phi = 0: mixes are then exactly 0 and the logits equal
+    base[2N:] bit for bit, so entries can sit exactly on a clamp bound.  Row i
+    of the N x N logits holds +c, -c, a value inside and a value outside the
+    range (the rest random inside)."""
+    M = 2 * N + N * N
+    base = rng.uniform(-0.5, 0.5, M) * c
+    lg = base[2 * N:].reshape(N, N)
+    for i in range(N):
+        lg[i, i % N] = c
+        lg[i, (i + 1) % N] = -c
+        lg[i, (i + 2) % N] = 1.5 * c * (1 if i % 2 else -1)
+    base[2 * N:] = lg.reshape(-1)
+    return base.astype(np.float32)
+
+
+@pytest.mark.parametrize("N", [4, 8])
+def test_clamp_gradient_inclusive_at_bounds(rng, N):
+    """F7: the reference's *_ref passes the clamp gradient where the logit
+    equals a bound (torch.clamp autograd, src/mhc_pre_clamp_sinkhorn_backward.py:
+    1434-1435); its Triton kernel masks them out (strict, :1186-1191).  With
+    phi = 0 the logits are exactly base, some exactly on +-clamp: the oracle's
+    grad_base must match torch autograd through the package's *_ref there, and
+    a strict mask (the Triton semantics, planted here in a copy of the oracle's
+    result) must not."""
+    T, D, c = 8, 32, 0.5
+    M = 2 * N + N * N
+    x = _t(rng.standard_normal((T, N, D)))
+    phi = torch.zeros(M, N * D)
+    alpha = torch.tensor([0.5, 0.5, 1.0])
+    base = torch.from_numpy(clamp_bound_base(N, c, rng))
+    gy = _t(rng.standard_normal((T, D)))
+    gpost = _t(rng.standard_normal((T, N)))
+    gcomb = _t(rng.standard_normal((T, N, N)))
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-c, clamp_max=c, iter_times=20)
+    logits = orc.pre_fwd(x.double(), phi.double(), alpha.double(), base.double(), **kw)["h_res_logits"]
+    lg = base.double().numpy()[2 * N:].reshape(N, N)
+    assert np.array_equal(logits, np.broadcast_to(lg, (T, N, N)))   # logits == base exactly
+    on_bound = np.abs(lg) == c
+    outside = np.abs(lg) > c
+    assert on_bound.sum() == 2 * N and outside.sum() == N
+
+    got = mhc_pre_clamp_sinkhorn_backward_ref(x, phi, alpha, base, gy, gpost, gcomb, **kw)
+    want = orc.pre_bwd(x.double(), phi.double(), alpha.double(), base.double(), gy.double(),
+                       gpost.double(), gcomb.double(), **kw)
+    gb_torch, gb_orc = got[3].double().numpy(), want[3]
+    scale = np.abs(gb_orc).max()
+    np.testing.assert_allclose(gb_torch, gb_orc, rtol=1e-4, atol=1e-5 * scale)
+    gl = gb_orc[2 * N:].reshape(N, N)
+    scale_l = np.abs(gl).max()
+    np.testing.assert_allclose(gb_torch[2 * N:].reshape(N, N), gl, rtol=1e-4, atol=1e-5 * scale_l)
+    assert (gl[on_bound] != 0).all()                         # gradient passes at the bounds
+    assert (gl[outside] == 0).all()                          # and not outside them
+    strict = gl * ~on_bound                                   # Triton's strict mask
+    assert not np.allclose(strict, gb_torch[2 * N:].reshape(N, N), rtol=1e-4, atol=1e-5 * scale_l)
