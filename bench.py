@@ -85,16 +85,20 @@ SINGLE_KERNEL_OPS = {
 }
 
 
-def measured_traffic(op):
-    """HBM bytes per launch of the op's kernel from the committed rocprofv3
-    --pmc summary (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy of known
-    size), or None when no summary for it is committed."""
-    path = os.path.join(ROOT, "profiles", "c5_pmc_traffic.json")
+PMC_SUMMARY = os.path.join("profiles", "c5_pmc_traffic.json")
+
+
+def profile_traffic():
+    """Per-operator HBM bytes per call from the committed rocprofv3 --pmc
+    summary of the headline shape (FETCH_SIZE and WRITE_SIZE of every kernel
+    of the operator, each scaled by what the counter reads for a plain copy of
+    known size).  These are the committed profile's figures, not a
+    measurement of this run; {} when no summary is committed."""
     try:
-        with open(path) as f:
-            return json.load(f)["ops"][op]["traffic_bytes"]
+        with open(os.path.join(ROOT, PMC_SUMMARY)) as f:
+            return json.load(f)["ops"]
     except (OSError, KeyError, ValueError):
-        return None
+        return {}
 
 
 def pmc_probe(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
@@ -185,9 +189,39 @@ def small_t_latency(m, _pre_forward, dev, kw, token_counts=(1, 64, 1024), reps=5
     return res
 
 
-def cpu_baselines(N, D, sample_tokens, ref_tokens):
-    """Oracle chain (numpy float64, one thread) and the package's torch *_ref
-    chain (fp32, all host threads) on bounded token samples of the workload."""
+def ref_chain_cpu(N, D, tokens, reps=3):
+    """The package's torch fp32 *_ref chain (pre fwd, post fwd, post bwd, pre
+    bwd: the reference's own CPU path, src/*.py *_ref) on all host threads:
+    median of `reps` runs after one warm-up.  Returns (seconds, threads)."""
+    import torch
+
+    import FlagOS_mhc as m
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    M = 2 * N + N * N
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-10.0, clamp_max=10.0, iter_times=20)
+    g = torch.Generator().manual_seed(0)
+    xt = torch.randn(tokens, N, D, generator=g).to(torch.bfloat16)
+    phit = (torch.randn(M, N * D, generator=g) / (N * D) ** 0.5).to(torch.bfloat16)
+    at, bt = torch.tensor([0.5, 0.5, 1.0]), torch.randn(M, generator=g) * 0.1
+    nt = (torch.randn(tokens, D, generator=g) * 0.1).to(torch.bfloat16)
+    gt = torch.randn(tokens, N, D, generator=g).to(torch.bfloat16)
+    times = []
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        ro = m.mhc_pre_clamp_sinkhorn_ref(xt, phit, at, bt, **kw)
+        h = ro["y"] + nt
+        m.mhc_post_ref(xt, ro["comb_frag"], h, ro["post_out"])
+        _, ghr, gho, ghp = m.mhc_post_backward_ref(gt, xt, ro["comb_frag"], h, ro["post_out"])
+        m.mhc_pre_clamp_sinkhorn_backward_ref(xt, phit, at, bt, gho, ghp, ghr, **kw)
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times[1:]), threads
+
+
+def oracle_chain_cpu(N, D, tokens):
+    """The float64 numpy oracle chain on one thread (test infrastructure,
+    timed here only as a second CPU figure)."""
     import numpy as np
     import torch
 
@@ -200,14 +234,12 @@ def cpu_baselines(N, D, sample_tokens, ref_tokens):
     def bf(a):
         return torch.tensor(a, dtype=torch.float32).to(torch.bfloat16).double().numpy()
 
-    Ts = sample_tokens
-    x = bf(r.standard_normal((Ts, N, D), dtype=np.float32))
+    x = bf(r.standard_normal((tokens, N, D), dtype=np.float32))
     phi = bf(r.standard_normal((M, N * D), dtype=np.float32) / np.sqrt(N * D))
     alpha = np.array([0.5, 0.5, 1.0])
     base = r.standard_normal(M) * 0.1
-    noise = bf(r.standard_normal((Ts, D), dtype=np.float32) * 0.1)
-    gup = bf(r.standard_normal((Ts, N, D), dtype=np.float32))
-
+    noise = bf(r.standard_normal((tokens, D), dtype=np.float32) * 0.1)
+    gup = bf(r.standard_normal((tokens, N, D), dtype=np.float32))
     try:
         from threadpoolctl import threadpool_limits
         limiter = threadpool_limits(limits=1)
@@ -219,38 +251,136 @@ def cpu_baselines(N, D, sample_tokens, ref_tokens):
     orc.post_fwd(x, out["comb_frag"], h_out, out["post_out"])
     _, g_hres, g_hout, g_hpost = orc.post_bwd(gup, x, out["comb_frag"], h_out, out["post_out"])
     orc.pre_bwd(x, phi, alpha, base, g_hout, g_hpost, g_hres, **kw)
-    oracle_s = time.perf_counter() - t0
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
+    secs = time.perf_counter() - t0
+    if limiter is not None and hasattr(limiter, "unregister"):
+        limiter.unregister()
+    return secs
+
+
+def cpu_baselines(N, D, T, sample_tokens, ref_tokens):
+    """cpu_baseline: the package's torch fp32 *_ref chain on every host
+    thread, median of 3 after one warm-up, on `ref_tokens` tokens of the
+    workload and scaled linearly in T (each token's work is independent; the
+    full-T fp32 autograd reference needs tens of GB).  oracle_cpu_baseline:
+    the float64 oracle chain on one thread over `sample_tokens` tokens."""
+    ref_s, threads = ref_chain_cpu(N, D, ref_tokens)
+    oracle_s = oracle_chain_cpu(N, D, sample_tokens)
+    return (
+        {"value": ref_tokens / ref_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+         "sample": f"FlagOS_mhc *_ref torch fp32 chain (pre fwd, post fwd, post bwd, pre bwd) on "
+                   f"{ref_tokens} of the {T} tokens (N={N}, D={D}), {threads} threads, median of 3 "
+                   f"after 1 warm-up: {ref_s:.2f} s; tokens/s scaled linearly to T={T}"},
+        {"value": sample_tokens / oracle_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+         "sample": f"oracle/mhc_oracle.py float64 chain on {sample_tokens} tokens of the N={N} D={D} "
+                   f"workload, one thread, {oracle_s:.1f} s"},
+    )
+
+
+def config_table(reps=20):
+    """BASELINE configs 1-4, per operator: GPU time (HIP events on the launch
+    stream, median of `reps` calls after one warm-up) against the compulsory
+    bytes, and the package's torch fp32 *_ref on every host thread (median of
+    3 after one warm-up) on the same seeded inputs, full size.  Config 3's
+    pre forward is the public call with need_backward=True, which writes the
+    fp32 x_scaled (4*N*D bytes per token, counted); config 4's pre forward is
+    the autograd path's (no x_scaled)."""
+    import torch
 
     import FlagOS_mhc as m
+    from FlagOS_mhc.mhc_pre_clamp_sinkhorn import _pre_forward
 
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    Tr = ref_tokens
-    xt = torch.randn(Tr, N, D).to(torch.bfloat16)
-    phit = (torch.randn(M, N * D) / (N * D) ** 0.5).to(torch.bfloat16)
-    at, bt = torch.tensor([0.5, 0.5, 1.0]), torch.randn(M) * 0.1
-    nt = (torch.randn(Tr, D) * 0.1).to(torch.bfloat16)
-    gt = torch.randn(Tr, N, D).to(torch.bfloat16)
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        ro = m.mhc_pre_clamp_sinkhorn_ref(xt, phit, at, bt, **kw)
-        h = ro["y"] + nt
-        m.mhc_post_ref(xt, ro["comb_frag"], h, ro["post_out"])
-        _, ghr, gho, ghp = m.mhc_post_backward_ref(gt, xt, ro["comb_frag"], h, ro["post_out"])
-        m.mhc_pre_clamp_sinkhorn_backward_ref(xt, phit, at, bt, gho, ghp, ghr, **kw)
-        times.append(time.perf_counter() - t0)
-    ref_s = min(times)
-    return (
-        {"value": Ts / oracle_s, "unit": "tokens/s", "cores": 1, "kind": "port",
-         "sample": f"oracle/mhc_oracle.py float64 chain (pre fwd, post fwd, post bwd, pre bwd) "
-                   f"on {Ts} tokens of the N={N} D={D} workload, one thread, {oracle_s:.1f} s"},
-        {"value": Tr / ref_s, "unit": "tokens/s", "cores": threads, "kind": "port",
-         "sample": f"FlagOS_mhc *_ref torch fp32 chain on {Tr} tokens, {threads} threads, "
-                   f"best of 2: {ref_s:.2f} s"},
-    )
+    kw = dict(norm_eps=1e-6, hc_eps=1e-6, clamp_min=-10.0, clamp_max=10.0, iter_times=20)
+
+    def gen(seed):
+        return torch.Generator().manual_seed(seed)
+
+    def post_case(T, N, D, dtype, seed):
+        g = gen(seed)
+        x = torch.randn(T, N, D, generator=g).to(dtype)
+        h_out = torch.randn(T, D, generator=g).to(dtype)
+        h_post = torch.rand(T, N, generator=g) * 2
+        h_res = torch.softmax(torch.randn(T, N, N, generator=g), dim=-1)
+        gy = torch.randn(T, N, D, generator=g).to(dtype)
+        return x, h_res, h_out, h_post, gy
+
+    def pre_case(T, N, D, seed):
+        g = gen(seed)
+        M = 2 * N + N * N
+        x = torch.randn(T, N, D, generator=g).to(torch.bfloat16)
+        phi = (torch.randn(M, N * D, generator=g) / (N * D) ** 0.5).to(torch.bfloat16)
+        alpha = torch.tensor([0.5, 0.5, 1.0])
+        base = torch.randn(M, generator=g) * 0.1
+        gy = torch.randn(T, D, generator=g).to(torch.bfloat16)
+        gpost = torch.randn(T, N, generator=g)
+        gcomb = torch.randn(T, N, N, generator=g)
+        return x, phi, alpha, base, gy, gpost, gcomb
+
+    def gpu_ms(fn):
+        fn()
+        return time_events(fn, reps, stream)[0]
+
+    def cpu_ms(fn):
+        ts = []
+        for _ in range(4):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts[1:]) * 1e3
+
+    rows = []
+
+    def add(cfg, op, T, N, D, b, gms, cms, extra_bytes=0):
+        algo = algorithmic_bytes(T, N, D, b)[op] + extra_bytes
+        rows.append({"config": cfg, "op": op, "T": T, "N": N, "D": D, "gpu_ms": round(gms, 4),
+                     "algo_GB": round(algo / 1e9, 4), "GBps": round(algo / gms / 1e6, 1),
+                     "frac_hbm": round(algo / gms / 1e6 / PEAK_HBM_GBS, 4),
+                     "gpu_tokens_per_s": round(T / gms * 1e3, 1),
+                     "cpu_ref_ms": round(cms, 2), "cpu_ref_tokens_per_s": round(T / cms * 1e3, 1)})
+        print(json.dumps(rows[-1]), flush=True)
+
+    # config 1: post forward, fp32, N=4, D=256, T=1024
+    # config 2: post forward + backward, bf16, N=4, D=4096, T=16384
+    for cfg, (T, N, D, dt, b) in (("c1", (1024, 4, 256, torch.float32, 4)),
+                                  ("c2", (16384, 4, 4096, torch.bfloat16, 2))):
+        c = post_case(T, N, D, dt, 0)
+        x, hr, ho, hp, gy = (t.to(dev) for t in c)
+        add(cfg, "post_fwd", T, N, D, b, gpu_ms(lambda: m.mhc_post(x, hr, ho, hp)),
+            cpu_ms(lambda: m.mhc_post_ref(*c[:4])))
+        if cfg == "c2":
+            add(cfg, "post_bwd", T, N, D, b, gpu_ms(lambda: m.mhc_post_backward(gy, x, hr, ho, hp)),
+                cpu_ms(lambda: m.mhc_post_backward_ref(c[4], *c[:4])))
+        del x, hr, ho, hp, gy, c
+    # config 3: pre forward, need_backward=True (x_scaled written), N=4, D=4096, T=16384
+    T, N, D = 16384, 4, 4096
+    c = pre_case(T, N, D, 0)
+    x, phi, alpha, base = (t.to(dev) for t in c[:4])
+    add("c3", "pre_fwd", T, N, D, 2,
+        gpu_ms(lambda: m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **kw)),
+        cpu_ms(lambda: m.mhc_pre_clamp_sinkhorn_ref(*c[:4], **kw)), extra_bytes=T * 4 * N * D)
+    del x, phi, alpha, base, c
+    # config 4: both operators forward + backward, N=8, D=2048, T=32768
+    T, N, D = 32768, 8, 2048
+    pc = post_case(T, N, D, torch.bfloat16, 1)
+    x, hr, ho, hp, gy = (t.to(dev) for t in pc)
+    add("c4", "post_fwd", T, N, D, 2, gpu_ms(lambda: m.mhc_post(x, hr, ho, hp)),
+        cpu_ms(lambda: m.mhc_post_ref(*pc[:4])))
+    add("c4", "post_bwd", T, N, D, 2, gpu_ms(lambda: m.mhc_post_backward(gy, x, hr, ho, hp)),
+        cpu_ms(lambda: m.mhc_post_backward_ref(pc[4], *pc[:4])))
+    del x, hr, ho, hp, gy, pc
+    c = pre_case(T, N, D, 2)
+    x, phi, alpha, base, gy, gpost, gcomb = (t.to(dev) for t in c)
+    fw = lambda: _pre_forward(x, phi, alpha, base, need_backward=True, want_x_scaled=False, **kw)
+    o = fw()
+    add("c4", "pre_fwd", T, N, D, 2, gpu_ms(fw), cpu_ms(lambda: m.mhc_pre_clamp_sinkhorn_ref(*c[:4], **kw)))
+    add("c4", "pre_bwd", T, N, D, 2,
+        gpu_ms(lambda: m.mhc_pre_clamp_sinkhorn_backward(x, phi, alpha, base, o["inv_rms"], None, o["mixes"],
+                                                         None, o["pre"], gy, gpost, gcomb, **kw)),
+        cpu_ms(lambda: m.mhc_pre_clamp_sinkhorn_backward_ref(*c, **kw)))
+    return {"configs": rows, "cpu_threads": threads, "device": torch.cuda.get_device_name(0)}
 
 
 def main():
@@ -261,10 +391,12 @@ def main():
     ap.add_argument("--tokens", type=int, default=65536)
     ap.add_argument("--n", type=int, default=4, choices=(4, 8), help="streams (BASELINE config 4: 8)")
     ap.add_argument("--d", type=int, default=7168, help="model width (BASELINE config 4: 2048)")
-    ap.add_argument("--cpu-sample", type=int, default=3072, help="oracle tokens for cpu_baseline")
-    ap.add_argument("--ref-sample", type=int, default=8192, help="torch *_ref tokens on CPU")
+    ap.add_argument("--cpu-sample", type=int, default=3072, help="oracle tokens for oracle_cpu_baseline")
+    ap.add_argument("--ref-sample", type=int, default=8192, help="torch *_ref tokens for cpu_baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-small-t", action="store_true", help="skip the few-token latency block")
+    ap.add_argument("--configs", action="store_true",
+                    help="per-operator GPU and CPU *_ref table of BASELINE configs 1-4 instead of the chain")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run one step and a 1 GiB copy (for rocprofv3 --pmc), no timing")
     args = ap.parse_args()
@@ -284,6 +416,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.configs:
+        print(json.dumps(config_table()), flush=True)
+        return
     N, D, T = args.n, args.d, args.tokens
     # the headline shape; elsewhere the roofline names no kernel and reports
     # no measured traffic (the committed counter summary covers this shape)
@@ -368,7 +503,9 @@ def main():
     # as a single kernel (pre_bwd is four kernels; its largest is shorter)
     dominant = max(SINGLE_KERNEL_OPS, key=lambda k: op_stats[k]["ms"])
     dom = op_stats[dominant]
-    traffic = measured_traffic(dominant) if headline else None
+    prof = profile_traffic() if headline else {}
+    traffic = prof.get(dominant, {}).get("traffic_bytes")
+    traffic_ratio = {op: round(v["traffic_bytes"] / v["algo_bytes"], 3) for op, v in prof.items()}
     mhc_ms = sum(v["ms"] for v in op_stats.values())
     chain_bytes = sum(algo.values())
 
@@ -394,6 +531,9 @@ def main():
                      "frac": dom["frac_hbm"], "traffic": traffic,
                      "algo_bytes": algo[dominant]},
         "ops": op_stats,
+        "traffic_over_algorithmic": {"source": PMC_SUMMARY + " (committed rocprofv3 --pmc summary of "
+                                               "this shape, not measured in this run)",
+                                     **traffic_ratio} if traffic_ratio else None,
         "mhc_ops_ms": round(mhc_ms, 4),
         "glue": glue,
         "post_pre_fused": post_pre,
@@ -402,9 +542,9 @@ def main():
     if not args.no_small_t:
         result["small_t_latency"] = small_t_latency(m, _pre_forward, dev, kw)
     if not args.no_cpu:
-        cb, rb = cpu_baselines(N, D, args.cpu_sample, args.ref_sample)
+        cb, ob = cpu_baselines(N, D, T, args.cpu_sample, args.ref_sample)
         result["cpu_baseline"] = cb
-        result["ref_cpu_baseline"] = rb
+        result["oracle_cpu_baseline"] = ob
     print(json.dumps(result), flush=True)
 
 
