@@ -32,6 +32,8 @@ _SIGNATURES = {
     "mhc_pre_fwd": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                _i64, _i32, _i32, _vp]),
+    "mhc_pre_fwd_noalloc": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
     "mhc_pre_bwd_acc": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _f32, _f32, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                    _i64, _i32, _i32, _vp]),

@@ -926,3 +926,74 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_fwd: x dtype %d not supported", x_dtype);
 }
+
+// ---- allocation-free variant ------------------------------------------------
+// mhc_pre_fwd_noalloc runs mhc_pre_fwd with its workspace in `scratch`, a
+// static device array of MHC_PRE_FWD_SCRATCH_BYTES: every GPU the library runs
+// on holds its own copy (the code object's zero-initialised data) until the
+// process ends.  In host code the name `scratch` is a host-side stand-in, not
+// a device address; the device address of the current GPU's copy comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+// Nothing in the workspace has to start at zero: every kernel writes the
+// parts it later reads within the same call.  Calls that overlap on one GPU
+// (two streams, two threads) share the array and race.
+namespace mhc {
+
+static __device__ __align__(256) unsigned char scratch[MHC_PRE_FWD_SCRATCH_BYTES];
+
+// Device address of `scratch` on device `dev` (the current device), looked up
+// on the first call for that device and cached.
+static void* pre_fwd_scratch(int dev, int* rc) {
+  static std::atomic<void*> cache[64];
+  if (dev < 0 || dev >= 64) {
+    *rc = set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_fwd_noalloc: device %d above the 64 supported", dev);
+    return nullptr;
+  }
+  void* p = cache[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    *rc = set_error(MHC_ERR_HIP, "mhc_pre_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+    return nullptr;
+  }
+  cache[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+}  // namespace mhc
+
+extern "C" int mhc_pre_fwd_noalloc(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                                   const float* alpha, const float* base, float norm_eps, float hc_eps,
+                                   float clamp_min, float clamp_max, int32_t iter_times, void* y,
+                                   float* post_out, float* comb_frag, float* inv_rms, float* mixes,
+                                   float* h_res_logits, float* pre, float* x_scaled, int64_t T, int32_t N,
+                                   int32_t D, void* stream) {
+  clear_error();
+  if (T < 0 || D <= 0 || N <= 0)
+    return set_error(MHC_ERR_INVALID, "mhc_pre_fwd_noalloc: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
+  const size_t need = mhc_pre_fwd_workspace_size(T, N, D, phi_dtype);
+  if (need > (size_t)MHC_PRE_FWD_SCRATCH_BYTES)
+    return set_error(MHC_ERR_INVALID,
+                     "mhc_pre_fwd_noalloc: T=%lld N=%d D=%d needs %zu bytes of workspace, above the %zu of "
+                     "its static scratch (use mhc_pre_fwd with a workspace)",
+                     (long long)T, N, D, need, (size_t)MHC_PRE_FWD_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (T > 0) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess)
+      return set_error(MHC_ERR_HIP, "mhc_pre_fwd_noalloc: no current device");
+    if (stream) {  // the scratch looked up below belongs to the current device
+      int sdev = -1;
+      if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || sdev != dev)
+        return set_error(MHC_ERR_INVALID, "mhc_pre_fwd_noalloc: stream of device %d, current device %d", sdev,
+                         dev);
+    }
+    int rc = MHC_OK;
+    ws = pre_fwd_scratch(dev, &rc);
+    if (!ws) return rc;
+  }
+  return mhc_pre_fwd(x, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
+                     y, post_out, comb_frag, inv_rms, mixes, h_res_logits, pre, x_scaled, ws,
+                     (size_t)MHC_PRE_FWD_SCRATCH_BYTES, T, N, D, stream);
+}

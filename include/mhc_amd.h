@@ -11,7 +11,8 @@
  * Conventions (all entry points):
  *   - plain device pointers and sizes; the library never allocates or
  *     frees memory: scratch space is passed in by the caller as `workspace`
- *     (size from the matching *_workspace_size call);
+ *     (size from the matching *_workspace_size call), except for
+ *     mhc_pre_fwd_noalloc, whose workspace is a static per-GPU array;
  *   - every tensor is contiguous, row-major, in the (T, N, D) token layout
  *     (T = tokens = B*S, N = streams, D = width); gates and Sinkhorn
  *     quantities are fp32;
@@ -89,6 +90,26 @@ int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dty
                 float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits, float* pre,
                 float* x_scaled, void* workspace, size_t workspace_bytes, int64_t T, int32_t N,
                 int32_t D, void* stream);
+
+/*
+ * mhc_pre_fwd without a workspace argument.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  It calls
+ * no hipMalloc / hipFree or other allocating routine: the workspace is a
+ * static device array of MHC_PRE_FWD_SCRATCH_BYTES per GPU, held until the
+ * process ends.  Calls whose mhc_pre_fwd_workspace_size exceeds it are
+ * refused with MHC_ERR_INVALID (N = 4, bf16 phi: about 1.6 M tokens).  The
+ * current device must be the one `stream` and the tensors belong to.  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams or threads) race.  Arguments and outputs as in mhc_pre_fwd.
+ */
+#define MHC_PRE_FWD_SCRATCH_BYTES (64u << 20)
+int mhc_pre_fwd_noalloc(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                        const float* alpha, const float* base, float norm_eps, float hc_eps,
+                        float clamp_min, float clamp_max, int32_t iter_times, void* y,
+                        float* post_out, float* comb_frag, float* inv_rms, float* mixes,
+                        float* h_res_logits, float* pre, float* x_scaled, int64_t T, int32_t N,
+                        int32_t D, void* stream);
 
 /*
  * mhc_pre_clamp_sinkhorn backward.  Replaces the device work of

@@ -147,3 +147,15 @@ def test_public_api_names():
     ]
     for name in m.__all__:
         assert callable(getattr(m, name))
+
+
+def test_noalloc_pre_fwd_refuses_sizes_above_its_scratch(lib):
+    """mhc_pre_fwd_noalloc checks the workspace it would need against its
+    static scratch before touching the device."""
+    T = 5_000_000
+    assert lib.mhc_pre_fwd_workspace_size(T, 4, 1024, 1) > 64 << 20
+    rc = lib.mhc_pre_fwd_noalloc(None, 1, None, 1, None, None, 1e-6, 1e-6, 0.0, 0.0, 20, None, None,
+                                 None, None, None, None, None, None, T, 4, 1024, None)
+    assert rc == -1 and b"static scratch" in lib.mhc_last_error()
+    assert lib.mhc_pre_fwd_noalloc(None, 1, None, 1, None, None, 1e-6, 1e-6, 0.0, 0.0, 20, None, None,
+                                   None, None, None, None, None, None, -1, 4, 1024, None) == -1
