@@ -616,7 +616,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
     acc_l += a.part[row * M + 2 * N + e];
     acc_h += a.part[row * M + eh];
   }
-  const float inv = 1.0f / sqrtf(ssq / K + a.norm_eps);
+  const float inv = rms_inv(ssq, K, a.norm_eps);
   const float mix_l = acc_l * inv, mix_h = acc_h * inv;
   if (ok) {
     if (a.mixes) {
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
     if (a.logits) a.logits[tok * L + e] = logit;
   }
   if (e < N) {
-    const float p = sigmoidf_(mix_h * a0 + a.base[e]) + a.hc_eps;
+    const float p = pre_gate(mix_h, a0, a.base[e], a.hc_eps);
     if (ok) {
       a.pre_ws[tok * N + e] = p;
       if (a.pre) a.pre[tok * N + e] = p;
@@ -764,6 +764,12 @@ static FwdSplitPlan fwd_split_plan(int64_t T, int N, int D) {
   return p;
 }
 
+}  // namespace mhc
+
+#include "pre_fwd_coop.hpp"
+
+namespace mhc {
+
 // The LDS-pipelined kernel covers the bf16 fast path (N = 4, 8).  Buffer
 // ranges are 32-bit: a tile of x rows (64 * N * D, fp32 x_scaled) must fit.
 static bool fwd_dma_usable(const PreFwdArgs& a, int N, bool bf16x, bool vec) {
@@ -773,6 +779,11 @@ static bool fwd_dma_usable(const PreFwdArgs& a, int N, bool bf16x, bool vec) {
 
 template <int N>
 static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if constexpr (N == 4) {  // x read from HBM once where the single-pass form applies
+    bool used = false;
+    const int rc = launch_pre_fwd_coop(a, workspace, workspace_bytes, st, &used);
+    if (rc || used) return rc;
+  }
   const int64_t ntiles = (a.T + kFwdTile - 1) / kFwdTile;
   const FwdSplitPlan plan = fwd_split_plan(a.T, N, a.D);
   if (plan.nsplit >= 2 && workspace && workspace_bytes >= kPreFwdWsBase + plan.bytes) {
@@ -857,7 +868,8 @@ static int dispatch_pre_fwd(int N, const PreFwdArgs& a, bool vec, hipStream_t st
 
 using namespace mhc;
 
-extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype) {
+// Workspace of the two-pass forms (every path runs with this much).
+static size_t pre_fwd_ws_min(int64_t T, int32_t N, int32_t D, int32_t phi_dtype) {
   if (N <= 0 || D <= 0) return 0;
   const int M = 2 * N + N * N;
   const int64_t K = (int64_t)N * D;
@@ -869,6 +881,14 @@ extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, in
     return kPreFwdWsBase + (split > y ? split : y);
   }
   return align256(phi_planes_bytes(phi_dtype, M, K));
+}
+
+// With room for the single-pass form where it applies (N = 4, bf16 phi).
+extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype) {
+  const size_t base = pre_fwd_ws_min(T, N, D, phi_dtype);
+  if (phi_dtype != MHC_DTYPE_BF16) return base;
+  const size_t coop = coop_ws_bytes(T, N, D);
+  return coop && kPreFwdWsBase + coop > base ? kPreFwdWsBase + coop : base;
 }
 
 extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
@@ -972,7 +992,8 @@ extern "C" int mhc_pre_fwd_noalloc(const void* x, int32_t x_dtype, const void* p
   clear_error();
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_fwd_noalloc: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
-  const size_t need = mhc_pre_fwd_workspace_size(T, N, D, phi_dtype);
+  // the two-pass forms fit in less; the single-pass one runs when it fits too
+  const size_t need = pre_fwd_ws_min(T, N, D, phi_dtype);
   if (need > (size_t)MHC_PRE_FWD_SCRATCH_BYTES)
     return set_error(MHC_ERR_INVALID,
                      "mhc_pre_fwd_noalloc: T=%lld N=%d D=%d needs %zu bytes of workspace, above the %zu of "

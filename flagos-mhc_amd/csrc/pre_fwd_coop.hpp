@@ -1,0 +1,770 @@
+// mhc_pre_clamp_sinkhorn forward in one HBM pass over x: N = 4, bf16 x and
+// phi, D = 256 G with G = 16 or 28 <= G <= 32 (coop_nch; D = 7168: G = 28).
+// Included by pre_fwd.hip.
+//
+// Semantics: mhc_pre_clamp_sinkhorn_ref, src/mhc_pre_clamp_sinkhorn.py:974-1022.
+// The passes it replaces are the reference's RMS / contraction passes over x
+// (:897-916) and its y pass (:956), which read x three times.
+//
+// y needs pre, pre needs the whole N*D row of a token reduced (sum of squares
+// and x . phi^T), and a 16-token tile of x is 917 KB at D = 7168: no CU holds
+// it.  So G CUs of one XCC form a group that shares every tile: member c owns
+// columns [256 c, 256 c + 256) of all four streams (a 32 KB "slice" of a
+// 16-token tile) and keeps it in LDS / registers from its one HBM read until
+// y of those columns is written.  A block (one per CU) has three kinds of
+// waves:
+//   L-waves (one per stream) land the slice in an LDS slot by direct-to-LDS
+//     loads (two tiles ahead), contract it with their phi columns on MFMA
+//     (16 tokens x 32 m x 256 k) and form the sums of squares; the last of
+//     the four adds the four partials in stream order and publishes the
+//     member's record (16 tokens x 25 sums) to the group's exchange ring;
+//   P-waves (four, tiles taken round robin) read, once this CU has published
+//     a tile, the words y needs (four pre mixes and the sum of squares per
+//     token) and this member's share of the heads' mixes from every member's
+//     record, add them in member order, and leave the totals and each
+//     token's pre / inv_rms (rms_inv / pre_gate, as the finalize kernel) in
+//     LDS;
+//   Y-waves copy each landed slice into a ring of three tiles of registers
+//     (freeing the LDS slot) and, two tiles later, write y (and the optional
+//     fp32 x_scaled) of their columns with the P-waves' pre / inv_rms, this
+//     member's share of the heads' totals, and (for the tile's designated
+//     member, tile sequence % G) the y values' totals to the [T][M] / [T]
+//     buffers that pre_fwd_finalize_kernel turns into mixes, inv_rms, the
+//     heads and Sinkhorn afterwards.
+// Loads and stores live in different waves (P-waves only load, Y-waves only
+// store): with both in flight the compiler waits for the memory counter to
+// reach zero wherever one load is needed, which puts a store round trip into
+// every tile.  x is read from HBM once; only the 3.2 KB records per member
+// and tile cross CUs, and they stay in the XCC's L2.
+//
+// Exchange.  A record is 200 16-byte words, each two (value, tag) pairs; the
+// tag is the tile's sequence number in its group plus one, so a reader knows
+// a value has arrived from its tag alone, with no flags, counters or fences
+// (one word is written by one store and read by one load, so it never
+// tears).  The ring (kCoR tiles per group) and the control words are zeroed
+// before every launch.  Records are stored with the default policy (the
+// lines stay in the writer's XCC L2) and read with device-scope (sc1) loads,
+// which skip the reader's CU L1 (it may hold stale copies of the ring) and
+// find them in that L2: every member of a group sits on one XCC.
+// Membership comes from the XCC_ID hardware register at the start of the
+// kernel (a grid-wide registration, so all blocks must be resident:
+// cooperative launch, one block per CU), so it holds whichever CU the
+// dispatcher chose for a block.
+//
+// Progress.  L-waves reuse an LDS slot once the Y-waves copied it; P-waves
+// reuse their LDS slot once the Y-waves read it; records of tile q are
+// overwritten by tile q + kCoR only after every member's P-waves are past
+// tile q (kCoR >= 2 S + 2 kCoLag + 2 tiles, see CoCfg).  Every wait is
+// bounded: after kCoTimeout of s_memrealtime without progress a wave sets the
+// block's abort flag and the status word, and every wave leaves.
+#pragma once
+
+namespace mhc {
+
+constexpr int kCoTT = 16;                          // tokens per tile
+constexpr int kCoLW = 4;                           // L-waves: one per stream (N = 4)
+constexpr int kCoLag = 2;                          // Y-waves: y of tile j - 2 while tile j lands
+constexpr int kCoYW = 4;                           // Y-waves: y writers
+constexpr int kCoPW = 4;                           // P-waves: exchange readers
+constexpr int kCoPSlots = 4;                       // tiles of P-wave sums in LDS
+constexpr int kCoR = 16;                           // exchange ring: tiles per group
+constexpr int kCoVals = 25;                        // sums per token: 24 mixes + sum(x^2)
+constexpr int kCoRecWords = kCoTT * kCoVals / 2;   // 16-byte words of a record (200)
+constexpr int kCoYWords = kCoTT * 5 / 2;           // words y needs: 4 pre mixes + sum(x^2) (40)
+constexpr int kCoMaxGroups = 16;
+constexpr int kCoMinG = 16;                        // fewest members per group
+constexpr int kCoMaxHW = (160 + kCoMinG - 1) / kCoMinG;  // head words a member totals, at most (10)
+constexpr int kCoMaxG = 32;
+constexpr int kCoCtlWords = 64;
+constexpr uint64_t kCoTimeout = 25000000ull;       // 0.25 s of s_memrealtime (100 MHz)
+// control words: [0..15] blocks registered per XCC, then
+constexpr int kCtlArrived = 16, kCtlStatus = 17;
+// status (first failure wins): 1 registration, 2 no group formed, then the
+// wait that timed out: 3 L slot copied, 4 L partial buffer, 5 Y tile landed,
+// 6 P exchange poll, 7 Y sums, 8 P own publish, 9 P sums slot
+constexpr uint32_t kStReg = 1, kStNoGroup = 2, kStLCopied = 3, kStLPread = 4, kStYLanded = 5, kStPPoll = 6,
+                   kStYSums = 7, kStPPub = 8, kStPSlot = 9;
+
+// Value order inside a record: v * 16 + token, v = 0..3 the pre mixes
+// (m = 0..3), v = 4 the sum of squares, v = 5..24 the mixes m = 4..23, so
+// the 80 values y needs are the first 40 words.
+__host__ __device__ constexpr int co_vidx(int m) { return m < 4 ? m : m + 1; }
+
+template <int NCH>  // 16-byte chunks per stream row of a slice: 16 (128 columns) or 32 (256)
+struct CoCfg {
+  static_assert(NCH == 16 || NCH == 32, "slice of 128 or 256 columns");
+  static constexpr int CS = NCH * 8;                // slice columns
+  static constexpr int H = NCH / 16;                // 256-byte half rows per stream row
+  static constexpr int STREAM = kCoTT * NCH * 16;   // bytes of one stream of a slot
+  static constexpr int SLOT = 4 * STREAM;           // bytes of a slot (one tile slice)
+  static constexpr int S = 131072 / SLOT;           // LDS slots: 4 or 8 (128 KB)
+  static constexpr int A = S - 2;                   // tiles of loads issued ahead (the Y-waves may lag one more)
+  static constexpr int DMA = STREAM / 1024;         // direct-to-LDS loads per stream and tile
+  static constexpr int STEPS = NCH / 4;             // 32-column MFMA steps per stream
+  static constexpr int RB = NCH / 4;                // 1 KB row blocks per stream slot (4 tokens x 256 bytes)
+  static constexpr int YW = kCoYW;                  // Y-waves
+  static constexpr int YB = RB / YW;                // row blocks per Y-wave
+  static_assert(YB * YW == RB, "row blocks split evenly over the Y-waves");
+  static constexpr int THREADS = (kCoLW + YW + kCoPW) * kWave;
+  static_assert(kCoR >= 2 * S + 2 * kCoLag + 2, "exchange ring shorter than the lag it must cover");
+};
+
+struct CoopArgs {
+  PreFwdArgs a;     // inputs and outputs; part / part_ssq receive the designated sums
+  uint32_t* ctl;    // kCoCtlWords control words, zeroed before the launch
+  u32x4* rec;       // [maxg][kCoR][G][kCoRecWords], zeroed before the launch
+  int G;            // members per group (D / CS)
+  int maxg;         // groups the ring has room for
+};
+
+// ---- LDS accesses of the L-waves (direct-to-LDS loads in flight: inline
+// asm, see lds_dma.hpp) and LDS counters --------------------------------------
+__device__ __forceinline__ uint32_t co_lds_ld(uint32_t a) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+__device__ __forceinline__ void co_lds_add(uint32_t a, uint32_t v) {
+  asm volatile("ds_add_u32 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(a), "v"(v) : "memory");
+}
+__device__ __forceinline__ uint32_t co_lds_add_rtn(uint32_t a, uint32_t v) {
+  uint32_t old;
+  asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(old) : "v"(a), "v"(v) : "memory");
+  return old;
+}
+// Counter updates from lane 0 only: a ds_add issued by the whole wave would
+// add once per active lane.  The returned old value is broadcast.
+__device__ __forceinline__ void co_lds_inc(uint32_t a) {
+  if (__lane_id() == 0) co_lds_add(a, 1u);
+}
+__device__ __forceinline__ uint32_t co_lds_inc_rtn(uint32_t a) {
+  uint32_t old = 0u;
+  if (__lane_id() == 0) old = co_lds_add_rtn(a, 1u);
+  return __builtin_amdgcn_readfirstlane(old);
+}
+__device__ __forceinline__ void co_lds_st(uint32_t a, float v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+__device__ __forceinline__ void co_lds_st4(uint32_t a, floatx4 v) {  // a 16-byte aligned
+  asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+// the value pairs at a (8-byte aligned) of the four L-waves' partials (WB
+// bytes apart): v[w] = wave w's pair
+template <int WB>
+__device__ __forceinline__ void co_lds_rd_part(float2 (&v)[4], uint32_t a) {
+  static_assert(3 * WB < 65536, "ds_read offset field");
+  asm volatile(
+      "ds_read_b64 %0, %4\n\t"
+      "ds_read_b64 %1, %4 offset:%5\n\t"
+      "ds_read_b64 %2, %4 offset:%6\n\t"
+      "ds_read_b64 %3, %4 offset:%7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(a), "i"(WB), "i"(2 * WB), "i"(3 * WB)
+      : "memory");
+}
+// four 16-byte reads at independent addresses
+__device__ __forceinline__ void co_lds_rd4(u32x4 (&v)[4], uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
+
+__device__ __forceinline__ uint64_t co_now() { return __builtin_amdgcn_s_memrealtime(); }
+
+// Wait until the LDS counter at `a` reaches `target` (or the block aborts /
+// kCoTimeout passes: then false, with the abort flag and status set).
+__device__ __forceinline__ void co_fail(uint32_t* status, uint32_t code) {
+  uint32_t expected = 0u;
+  __hip_atomic_compare_exchange_strong(status, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool co_wait_ge(uint32_t a, uint32_t target, uint32_t abort_a, uint32_t* status,
+                                           uint32_t code) {
+  if (co_lds_ld(a) >= target) return true;
+  const uint64_t deadline = co_now() + kCoTimeout;
+  for (;;) {
+    if (co_lds_ld(a) >= target) return true;
+    if (co_lds_ld(abort_a)) return false;
+    if (co_now() > deadline) {
+      co_lds_inc(abort_a);
+      co_fail(status, code);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// vmcnt(n * PER) for a run-time n in [0, MAXN]
+template <int PER, int MAXN>
+__device__ __forceinline__ void co_wait_tiles(int n) {
+  if constexpr (MAXN >= 0) {
+    if (n >= MAXN) {
+      wait_vmcnt<PER * MAXN>();
+      return;
+    }
+    co_wait_tiles<PER, MAXN - 1>(n);
+  }
+}
+
+// Poll `nm` <= PVN members' words at byte offset `off0` of the group's ring
+// (member stride kCoRecWords words) until
+// every tag equals `tag`; returns the two
+// values summed in member order (reloading into the caller's registers `v`).
+// The loads are device scope (sc1): they bypass this CU's L1, which may hold
+// stale copies of the ring, and read the XCD's L2, where the writers' stores
+// land.  Lanes with !active take part in the wave's retry vote only.
+constexpr int kCoPolicySc1 = 16;
+template <int PVN>
+__device__ __forceinline__ bool co_poll_sum(u32x4 (&v)[PVN], const __amdgpu_buffer_rsrc_t& ring, uint32_t off0, int nm,
+                                            bool active, uint32_t tag, float& s0, float& s1, uint32_t abort_a,
+                                            uint32_t* status) {
+  const uint64_t deadline = co_now() + kCoTimeout;
+  for (;;) {
+    const uint32_t vo = active ? off0 : kBufferOob;
+#pragma unroll
+    for (int i = 0; i < PVN; ++i)
+      if (i < nm) v[i] = __builtin_amdgcn_raw_buffer_load_b128(ring, vo + (uint32_t)(i * kCoRecWords * 16), 0, kCoPolicySc1);
+    bool ok = true;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PVN; ++i)
+      if (i < nm) {
+        ok = ok && ((v[i][1] == tag && v[i][3] == tag) || !active);
+        a0 += __uint_as_float(v[i][0]);
+        a1 += __uint_as_float(v[i][2]);
+      }
+    if (!__any(!ok)) {
+      s0 = a0;
+      s1 = a1;
+      return true;
+    }
+    if (co_lds_ld(abort_a)) return false;
+    if (co_now() > deadline) {
+      co_lds_inc(abort_a);
+      co_fail(status, kStPPoll);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+template <int NCH, bool XS>
+__global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopArgs ca) {
+  using C = CoCfg<NCH>;
+  constexpr int S = C::S, A = C::A, H = C::H, DMA = C::DMA, STEPS = C::STEPS, CS = C::CS, YW = C::YW, YB = C::YB;
+  constexpr int M = 24;
+  __shared__ __align__(1024) u32x4 slots[S * C::SLOT / 16];
+  __shared__ __align__(16) float pbuf[2][kCoLW][kCoTT * kCoVals];   // L-wave partials of a tile (two tiles)
+  __shared__ float tot[kCoPSlots][2 * (kCoYWords + kCoMaxHW)];  // per tile: totals of the polled words (word w -> [2 w], [2 w + 1])
+  __shared__ float pinv[kCoPSlots][kCoTT][5];  // per tile and token: pre (4) and inv_rms
+  // counters: landed[S] at 0, copied[S] at 8, pcnt[2] at 16, pread[2] at 18,
+  // abort at 21, pub (tiles published) at 22, pready[kCoPSlots] at 24,
+  // then ydone[kCoPSlots] and pfinal[kCoPSlots]
+  __shared__ uint32_t cnt[24 + 3 * kCoPSlots];
+  __shared__ int info[4];
+
+  const PreFwdArgs& a = ca.a;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t T = a.T;
+  const int D = a.D, K = 4 * D, G = ca.G;
+  const uint64_t deadline0 = co_now();
+  uint32_t* status = ca.ctl + kCtlStatus;
+
+  // ---- group formation: the blocks of one XCC, in registration order ------
+  if (tid < 24 + 3 * kCoPSlots) cnt[tid] = 0u;
+  if (tid == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 15u;
+    const uint32_t rank = __hip_atomic_fetch_add(ca.ctl + xcc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(ca.ctl + kCtlArrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool ok = true;
+    while (__hip_atomic_load(ca.ctl + kCtlArrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gridDim.x) {
+      if (co_now() > deadline0 + kCoTimeout) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    // an XCC with c registered blocks forms c / G groups: its block of rank r
+    // is member r % G of its group r / G (if r / G < c / G)
+    int group = -1, ngroups = 0;
+    if (ok) {
+      for (uint32_t x = 0; x < 16; ++x) {
+        const uint32_t c = __hip_atomic_load(ca.ctl + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int ng = (int)(c / (uint32_t)G) < ca.maxg - ngroups ? (int)(c / (uint32_t)G) : ca.maxg - ngroups;
+        if (x == xcc && (int)(rank / (uint32_t)G) < ng) group = ngroups + (int)(rank / (uint32_t)G);
+        ngroups += ng;
+      }
+      if (ngroups == 0) co_fail(status, kStNoGroup);
+    } else {
+      co_fail(status, kStReg);
+    }
+    info[0] = group;
+    info[1] = ngroups;
+    info[2] = (int)(rank % (uint32_t)G);
+  }
+  __syncthreads();
+  const int group = info[0], ngroups = info[1], member = info[2];
+  if (group < 0) return;  // uniform over the block: not a member of a group
+  const int64_t ntiles = (T + kCoTT - 1) / kCoTT;
+  const int64_t nq = (ntiles - group + ngroups - 1) / ngroups;  // tiles of this group
+  if (nq <= 0) return;
+  const int slice0 = member * CS;
+  u32x4* recw = ca.rec + (size_t)group * kCoR * G * kCoRecWords;  // this group's ring
+  const auto ring = rows_rsrc(recw, (int64_t)kCoR * G * kCoRecWords * 16);
+  const uint32_t sbase = lds_addr(slots);
+  const uint32_t c_landed = lds_addr(cnt), c_copied = c_landed + 32, c_pcnt = c_landed + 64,
+                 c_pread = c_landed + 72, c_abort = c_landed + 84, c_pub = c_landed + 88, c_pready = c_landed + 96,
+                 c_ydone = c_pready + 4 * kCoPSlots, c_pfinal = c_ydone + 4 * kCoPSlots;
+  const bf16_t* __restrict__ x = static_cast<const bf16_t*>(a.x);
+
+  if (wave < kCoLW) {
+    // ======================= L-wave: stream w ===============================
+    const int w = wave, r = lane & 15, q = lane >> 4;
+    // phi operands of this stream's slice: step s, m tile mt -> row 16 mt + r,
+    // columns w D + slice0 + 32 s + 8 q .. + 8 (zero rows for m >= 24)
+    u32x4 B[STEPS][2];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int m = 16 * mt + r;
+        B[s][mt] = m < M ? ld16(a.phi + (int64_t)m * K + (int64_t)w * D + slice0 + 32 * s + 8 * q) : zero4();
+      }
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+
+    // direct-to-LDS loads of tile sequence qi, stream w: instruction i moves
+    // tokens 4 (i / H) + rho (rho = lane / 16), 256 bytes each; lane rho*16 +
+    // kp lands chunk 16 (i % H) + (kp ^ token) of its row (XOR swizzle: the
+    // MFMA reads of 16 tokens x one chunk hit 16 different bank groups)
+    auto issue = [&](int64_t qi) {
+      const int64_t t0 = (group + qi * ngroups) * kCoTT;
+      const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
+      const auto rs = rows_rsrc(x + (t0 * 4 + w) * D + slice0, ((int64_t)(nv - 1) * K + CS) * 2);
+      const uint32_t slot = sbase + (uint32_t)((qi % S) * C::SLOT + w * C::STREAM);
+      const int rho = lane >> 4, kp = lane & 15;
+#pragma unroll
+      for (int i = 0; i < DMA; ++i) {
+        const int tok = 4 * (i / H) + rho;
+        const int c = 16 * (i % H) + (kp ^ tok);
+        const uint32_t off = tok < nv ? (uint32_t)(((int64_t)tok * K + 8 * c) * 2) : kBufferOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(uintptr_t)(slot + i * 1024), 16, off, 0, 0,
+                                                 2 /* nt */);
+      }
+    };
+    // LDS address of lane (r, q)'s A operand of step s in a stream slot
+    uint32_t aoff[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int c = 4 * s + q;
+      aoff[s] = (uint32_t)((H * (r / 4) + c / 16) * 1024 + (16 * (r % 4) + ((c % 16) ^ r)) * 16);
+    }
+
+    bool alive = true;
+    for (int64_t j = 0; j < (nq < A ? nq : A); ++j) issue(j);
+    for (int64_t j = 0; j < nq && alive; ++j) {
+      if (j + A < nq) {
+        alive = co_wait_ge(c_copied + 4 * (uint32_t)((j + A) % S), (uint32_t)(YW * ((j + A) / S)), c_abort, status,
+                           kStLCopied);
+        if (!alive) break;
+        issue(j + A);
+      }
+      const int64_t after = nq - 1 - j < A ? nq - 1 - j : A;
+      co_wait_tiles<DMA, A>((int)after);
+      co_lds_inc(c_landed + 4 * (uint32_t)(j % S));
+
+      // contraction of this stream's 16 x CS slice: fresh MFMA chain
+      const uint32_t sl = sbase + (uint32_t)((j % S) * C::SLOT + w * C::STREAM);
+      floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+      float ssq = 0.f;
+#pragma unroll
+      for (int sg = 0; sg < STEPS; sg += 4) {  // four steps' operands at a time (register budget)
+        u32x4 Ar[4];
+        co_lds_rd4(Ar, sl + aoff[sg], sl + aoff[sg + 1], sl + aoff[sg + 2], sl + aoff[sg + 3]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float lo = __uint_as_float(Ar[s][u] << 16), hi = __uint_as_float(Ar[s][u] & 0xffff0000u);
+            ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
+          }
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) acc[mt] = mfma16x16x32(as_bf16x8(Ar[s]), as_bf16x8(B[sg + s][mt]), acc[mt]);
+        }
+      }
+      ssq += __shfl_xor(ssq, 16, kWave);
+      ssq += __shfl_xor(ssq, 32, kWave);
+
+      // partial -> pbuf[j % 2][w]; the buffer's previous tile must be published
+      const int pb = (int)(j & 1);
+      alive = co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j / 2), c_abort, status, kStLPread);
+      if (!alive) break;
+      const uint32_t pw = lds_addr(&pbuf[pb][w][0]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int m = 16 * mt + r;  // lane (r, q) holds tokens 4q..4q+3 of mix m
+        if (m < M) co_lds_st4(pw + (uint32_t)((co_vidx(m) * kCoTT + 4 * q) * 4), acc[mt]);
+      }
+      if (q == 0) co_lds_st(pw + (uint32_t)((4 * kCoTT + r) * 4), ssq);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const uint32_t old = co_lds_inc_rtn(c_pcnt + 4 * (uint32_t)pb);
+      if (old == 4u * (uint32_t)(j / 2) + 3u) {
+        // last of the four: add the partials in stream order and publish
+        const uint32_t tag = (uint32_t)(j + 1);
+        // ring layout [tile][member][word]: a record is one contiguous run
+        const uint32_t dst = (uint32_t)(((j % kCoR) * G + member) * kCoRecWords * 16);  // byte offset in the ring
+        const uint32_t p0 = lds_addr(&pbuf[pb][0][0]);
+        constexpr int WB = kCoTT * kCoVals * 4;  // bytes between the waves' partials
+#pragma unroll
+        for (int it = 0; it < (kCoRecWords + kWave - 1) / kWave; ++it) {
+          const int wd = lane + kWave * it;
+          if (wd < kCoRecWords) {
+            float2 pv[4];
+            co_lds_rd_part<WB>(pv, p0 + (uint32_t)(8 * wd));
+            u32x4 word;
+            word[0] = __float_as_uint(((pv[0].x + pv[1].x) + pv[2].x) + pv[3].x);
+            word[1] = tag;
+            word[2] = __float_as_uint(((pv[0].y + pv[1].y) + pv[2].y) + pv[3].y);
+            word[3] = tag;
+            // default policy: the line stays in this XCD's L2, where the
+            // readers' device-scope loads find it
+            __builtin_amdgcn_raw_buffer_store_b128(word, ring, dst + (uint32_t)(wd * 16), 0, 0);
+          }
+        }
+        co_lds_inc(c_pread + 4 * (uint32_t)pb);
+        co_lds_inc(c_pub);
+      }
+    }
+    wait_vmcnt<0>();  // no direct-to-LDS load may outlive the block
+    return;
+  }
+
+  // The exchange reads and the y stores live in different waves: a wave with
+  // both loads and stores in flight gets s_waitcnt vmcnt(0) from the
+  // compiler wherever it needs one load (the counter may then decrement out
+  // of order), which would put a full store round trip into every tile.
+  // P-waves only load (the group's records) and hand sums to the Y-waves
+  // through LDS; Y-waves only store (y, x_scaled, part).
+  const int hw0 = kCoYWords + (kCoRecWords - kCoYWords) * member / G;
+  const int nhw = kCoYWords + (kCoRecWords - kCoYWords) * (member + 1) / G - hw0;  // <= kCoMaxHW
+  // uniform parameters moved to scalar registers up front: a vector register
+  // still waiting on its load would make a loop wait on vmcnt(0) (every load
+  // or store in flight) at its first use in each iteration
+  auto uniform = [](float f) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f))); };
+  const float Kf = (float)K;
+
+  if (wave >= kCoLW + YW) {
+    // ======================= P-wave pw ======================================
+    // P-wave pw takes the tiles u = pw (mod kCoPW) (so kCoPW tiles' polls are
+    // in flight at once, and each P-wave owns psum slot pw): once this CU has
+    // published tile u it reads, from every member, the 40 words y needs
+    // (lanes 0..39) and this member's share [hw0, hw0 + nhw) of the 160 words
+    // of the heads' values (lanes 40 ..), adds them in member order, and
+    // leaves the totals and each token's pre / inv_rms (rms_inv, pre_gate, as
+    // the finalize kernel) in LDS for the Y-waves.  Its loads are issued and
+    // consumed in the same iteration.
+    const int pw = wave - kCoLW - YW;
+    static_assert(kCoPSlots == kCoPW, "a psum slot per P-wave");
+    const float a0 = uniform(a.alpha[0]);
+    float base_n[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) base_n[n] = uniform(a.base[n]);
+    const bool pact = lane < kCoYWords + nhw;
+    const uint32_t poff = (uint32_t)((lane < kCoYWords ? lane : (pact ? hw0 + lane - kCoYWords : 0)) * 16);
+    auto rec_off = [&](int64_t t) { return (uint32_t)((t % kCoR) * G * kCoRecWords * 16) + poff; };
+    const int sl = pw;
+    for (int64_t u = pw; u < nq; u += kCoPW) {
+      if (!co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub)) break;
+      // two rounds of up to 16 members (register budget), added in member order
+      const uint32_t tag = (uint32_t)(u + 1);
+      float s0 = 0.f, s1 = 0.f;
+      bool alive = true;
+#pragma unroll
+      for (int h = 0; h < 2 && alive; ++h) {
+        const int mb = 16 * h, nmh = G - mb < 16 ? G - mb : 16;
+        const uint32_t vo = pact ? rec_off(u) + (uint32_t)(mb * kCoRecWords * 16) : kBufferOob;
+        u32x4 PV[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          PV[i] = __builtin_amdgcn_raw_buffer_load_b128(ring, i < nmh ? vo : kBufferOob, i * kCoRecWords * 16, kCoPolicySc1);
+        float h0 = 0.f, h1 = 0.f;
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          ok = ok && ((PV[i][1] == tag && PV[i][3] == tag) || !(pact && i < nmh));
+          h0 += __uint_as_float(PV[i][0]);
+          h1 += __uint_as_float(PV[i][2]);
+        }
+        if (__any(!ok) && !co_poll_sum<16>(PV, ring, vo, nmh, pact, tag, h0, h1, c_abort, status)) alive = false;
+        s0 = h == 0 ? h0 : s0 + h0;
+        s1 = h == 0 ? h1 : s1 + h1;
+      }
+      if (!alive) break;
+      // the slot's previous tile must be read by every Y-wave
+      if (!co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot)) break;
+      if (pact) {
+        tot[sl][2 * lane] = s0;
+        tot[sl][2 * lane + 1] = s1;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane < kCoTT) {
+        const float iv = rms_inv(tot[sl][4 * kCoTT + lane], Kf, a.norm_eps);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) pinv[sl][lane][n] = pre_gate(tot[sl][n * kCoTT + lane] * iv, a0, base_n[n], a.hc_eps);
+        pinv[sl][lane][4] = iv;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      co_lds_inc(c_pfinal + 4 * (uint32_t)sl);  // after the LDS writes (a wave's LDS operations stay in order)
+    }
+    return;
+  }
+
+  // ========================= Y-wave v =======================================
+  // Y-wave v holds row blocks v + YW b (b < YB) of every stream slot: row
+  // block rb is tokens 4 (rb / H) + rho (rho = lane / 16), 256-byte half row
+  // rb % H; lane rho*16 + kp holds the 16-byte chunk 16 (rb % H) + (kp ^
+  // token) of its token (where the direct-to-LDS load put it, so copies are
+  // conflict-free 1 KB reads)
+  const int v = wave - kCoLW;
+  const int rho = lane >> 4, kp = lane & 15;
+  int tok[YB], chunk[YB];  // token within a tile and 16-byte chunk of the slice, per row block
+#pragma unroll
+  for (int b = 0; b < YB; ++b) {
+    const int rb = v + YW * b;
+    tok[b] = 4 * (rb / H) + rho;
+    chunk[b] = 16 * (rb % H) + (kp ^ tok[b]);
+  }
+  float p[YB][4], inv[YB];  // pre and inv_rms of this lane's tokens
+
+  // tile j into Xc
+  auto copy = [&](int64_t j, u32x4 (&Xc)[YB][4]) -> bool {
+    if (!co_wait_ge(c_landed + 4 * (uint32_t)(j % S), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status, kStYLanded))
+      return false;
+#pragma unroll
+    for (int b = 0; b < YB; ++b) {
+      const uint32_t o = sbase + (uint32_t)((j % S) * C::SLOT + (v + YW * b) * 1024 + lane * 16);
+      co_lds_rd4(Xc[b], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
+    }
+    co_lds_inc(c_copied + 4 * (uint32_t)(j % S));
+    return true;
+  };
+
+  // y (and x_scaled) of tile u from Xt with this lane's p / inv: buffer
+  // stores against the tile's rows (scalar base, 32-bit offsets; rows past T
+  // fall outside the range and are dropped)
+  auto write_y = [&](int64_t u, const u32x4 (&Xt)[YB][4]) {
+    const int64_t t0 = (group + u * ngroups) * kCoTT;
+    const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
+    const auto ys = rows_rsrc(static_cast<bf16_t*>(a.y) + t0 * D, (int64_t)nv * D * 2);
+#pragma unroll
+    for (int b = 0; b < YB; ++b) {
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = 0.f;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          o[2 * w] = fmaf(p[b][n], __uint_as_float(Xt[b][n][w] << 16), o[2 * w]);
+          o[2 * w + 1] = fmaf(p[b][n], __uint_as_float(Xt[b][n][w] & 0xffff0000u), o[2 * w + 1]);
+        }
+      u32x4 ov;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
+      const uint32_t col = (uint32_t)(slice0 + 8 * chunk[b]);
+      __builtin_amdgcn_raw_buffer_store_b128(ov, ys, ((uint32_t)tok[b] * D + col) * 2, 0, 2 /* nt */);
+      if constexpr (XS) {
+        const auto xr = rows_rsrc(a.x_scaled + t0 * 4 * D, (int64_t)nv * 4 * D * 4);
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            u32x4 xs;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              const uint32_t xw = Xt[b][n][2 * h + w];
+              xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv[b]);
+              xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv[b]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(xs, xr, (((uint32_t)tok[b] * 4 + n) * D + col + 4 * h) * 4, 0, 2);
+          }
+      }
+    }
+  };
+
+  // Step j: copy tile j into X[j % 3], then take tile t = j - 2 from
+  // X[t % 3]: pre / inv_rms and the part totals from the P-waves, y, the
+  // heads' share and (designated member) the y values' totals to part.  The
+  // loop body is three steps, so the ring never moves between registers.
+  static_assert(kCoLag == 2, "three register buffers: tiles j - 2 .. j");
+  auto step = [&](int64_t j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) -> bool {
+    const int64_t t = j - kCoLag;
+    if (j < nq && !copy(j, Xc)) return false;
+    if (t >= 0 && t < nq) {
+      const int sl = (int)(t % kCoPSlots);
+      if (!co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums))
+        return false;
+#pragma unroll
+      for (int b = 0; b < YB; ++b) {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) p[b][n] = pinv[sl][tok[b]][n];
+        inv[b] = pinv[sl][tok[b]][4];
+      }
+      const int pv = (v - 1) * kWave + lane;
+      const bool des = (int)(t % G) == member && v >= 1 && pv < 5 * kCoTT;
+      const bool hs = v == 0 && lane < 2 * nhw;
+      const float sh = hs ? tot[sl][2 * kCoYWords + lane] : 0.f;
+      const float dv = des ? tot[sl][pv] : 0.f;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      co_lds_inc(c_ydone + 4 * (uint32_t)sl);  // slot read
+      write_y(t, Xt);
+      const int64_t t0 = (group + t * ngroups) * kCoTT;
+      const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
+      const auto ps = rows_rsrc(a.part + t0 * M, (int64_t)nv * M * 4);
+      if (hs) {  // this member's share of the heads' values
+        const int hv = 2 * hw0 + lane;  // value index in the record (>= 80)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sh), ps, (uint32_t)((hv % kCoTT) * M + hv / kCoTT - 1) * 4,
+                                              0, 0);
+      }
+      if (des) {  // the designated member: the y values' totals to part / part_ssq
+        const int vt = pv / kCoTT, tk = pv % kCoTT;
+        if (vt == 4) {
+          const auto ss = rows_rsrc(a.part_ssq + t0, (int64_t)nv * 4);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dv), ss, (uint32_t)tk * 4, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dv), ps, (uint32_t)(tk * M + vt) * 4, 0, 0);
+        }
+      }
+    }
+    return true;
+  };
+  u32x4 XA[YB][4], XB[YB][4], XC[YB][4];
+  for (int64_t j = 0; j < nq + kCoLag; j += 3) {
+    if (!step(j, XA, XB)) break;
+    if (!step(j + 1, XB, XC)) break;
+    if (!step(j + 2, XC, XA)) break;
+  }
+}
+
+// zero `n` 16-byte words (the control words and the exchange ring before a launch)
+__global__ __launch_bounds__(256) void co_zero_kernel(u32x4* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = zero4();
+}
+
+// Slice geometry for D: 256-column slices, G = D / 256 members per group.
+// Used where it measured faster than the two-pass forms on MI355X (32-CU
+// XCCs): G = 16 (two groups per XCC, D = 4096) and 28 <= G <= 32 (one group
+// per XCC, D = 7168 .. 8192).  With G = 12, 14, 20 or 24 too many CUs idle
+// or the slices are too short, and the two-pass forms win; 0 selects them.
+inline int coop_nch(int D, int* G) {
+  if (D % 256) return 0;
+  const int g = D / 256;
+  if (g == 16 || (g >= 28 && g <= kCoMaxG)) {
+    *G = g;
+    return 32;
+  }
+  return 0;
+}
+
+// Groups the exchange ring is sized for: one per G CUs, at most kCoMaxGroups.
+inline int coop_max_groups(int G) {
+  const int g = (int)(device_cu_count() / G);
+  return g < kCoMaxGroups ? g : kCoMaxGroups;
+}
+
+constexpr int64_t kCoopMinT = 8192;  // below this the split-K forms have lower latency
+
+// Workspace of the single-pass form after kPreFwdWsBase: control words, the
+// exchange ring, then part [T][M] and part_ssq [T] (the finalize kernel's
+// input) and its pre / inv_rms outputs.  0 if the form does not apply.
+inline size_t coop_ws_bytes(int64_t T, int N, int D) {
+  int G = 0;
+  if (N != 4 || T < kCoopMinT || !coop_nch(D, &G)) return 0;
+  return align256((size_t)kCoCtlWords * 4) + align256((size_t)coop_max_groups(G) * kCoR * G * kCoRecWords * 16) +
+         align256((size_t)T * 24 * 4) + align256((size_t)T * 4) + fwd_y_ws_bytes(T, 4);
+}
+
+// Per-device: can the single-pass kernel run co-resident on every CU?
+inline bool coop_supported(const void* kernel, int threads, int nch) {
+  static std::atomic<int> cache[64][2];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  std::atomic<int>& slot = cache[dev][nch == 32];
+  int v = slot.load(std::memory_order_relaxed);
+  if (v) return v > 0;
+  int coop = 0, nb = 0;
+  bool ok = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess && coop &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1;
+  hipGetLastError();
+  slot.store(ok ? 1 : -1, std::memory_order_relaxed);
+  return ok;
+}
+
+// Runs the single-pass form when it applies (N = 4 bf16 fast path, D with a
+// slice geometry, T >= kCoopMinT, enough workspace, not under stream capture,
+// cooperative launch available); *used says whether it ran.
+template <bool XS>
+static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace_bytes, hipStream_t st,
+                                  bool* used) {
+  *used = false;
+  int G = 0;
+  const int nch = coop_nch(a.D, &G);
+  const size_t need = coop_ws_bytes(a.T, 4, a.D);
+  if (!nch || !need || !workspace || workspace_bytes < kPreFwdWsBase + need) return MHC_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    hipGetLastError();
+    return MHC_OK;
+  }
+  const void* kfn = (const void*)pre_fwd_coop_kernel<32, XS>;
+  const int threads = CoCfg<32>::THREADS;
+  if (!coop_supported(kfn, threads, nch)) return MHC_OK;
+  char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
+  CoopArgs ca;
+  ca.ctl = reinterpret_cast<uint32_t*>(w);
+  w += align256((size_t)kCoCtlWords * 4);
+  ca.rec = reinterpret_cast<u32x4*>(w);
+  ca.maxg = coop_max_groups(G);
+  const size_t rec_bytes = align256((size_t)ca.maxg * kCoR * G * kCoRecWords * 16);
+  w += rec_bytes;
+  a.part = reinterpret_cast<float*>(w);
+  w += align256((size_t)a.T * 24 * 4);
+  a.part_ssq = reinterpret_cast<float*>(w);
+  w += align256((size_t)a.T * 4);
+  a.pre_ws = reinterpret_cast<float*>(w);
+  a.inv_ws = reinterpret_cast<float*>(w + align256((size_t)a.T * 4 * 4));
+  ca.a = a;
+  ca.G = G;
+  // zero the control words and the ring (contiguous)
+  const int64_t words = (int64_t)((align256((size_t)kCoCtlWords * 4) + rec_bytes) / 16);
+  hipLaunchKernelGGL(co_zero_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(ca.ctl), words);
+  int rc = check_launch("pre_fwd_coop_zero");
+  if (rc) return rc;
+  void* args[] = {&ca};
+  const hipError_t e = hipLaunchCooperativeKernel(kfn, dim3((unsigned)device_cu_count()), dim3(threads), args, 0, st);
+  if (e != hipSuccess) {  // not co-resident after all: the caller runs the two-pass forms
+    hipGetLastError();
+    return MHC_OK;
+  }
+  *used = true;
+  hipLaunchKernelGGL((pre_fwd_finalize_kernel<4>), dim3((unsigned)((a.T + 15) / 16)), dim3(kFwdThreads), 0, st, a, 1);
+  return check_launch("pre_fwd_finalize");
+}
+
+static int launch_pre_fwd_coop(const PreFwdArgs& a, void* workspace, size_t workspace_bytes, hipStream_t st,
+                               bool* used) {
+  return a.x_scaled ? launch_pre_fwd_coop_x<true>(a, workspace, workspace_bytes, st, used)
+                    : launch_pre_fwd_coop_x<false>(a, workspace, workspace_bytes, st, used);
+}
+
+}  // namespace mhc

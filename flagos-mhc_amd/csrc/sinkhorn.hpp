@@ -121,6 +121,15 @@ __device__ float sinkhorn_vjp_scratch(float lc, float g, float eps, int iters, f
 
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
 
+// inv_rms of a token from its sum of squares over k = N*D values, and the
+// pre gate sigma(mix * alpha0 + base) + hc_eps, written once so every kernel
+// that forms them (the finalize kernel and the single-pass forward, which
+// uses pre for y before the finalize kernel writes it out) rounds alike.
+__device__ __forceinline__ float rms_inv(float ssq, float k, float eps) { return 1.0f / sqrtf(ssq / k + eps); }
+__device__ __forceinline__ float pre_gate(float mix, float a0, float base, float hc_eps) {
+  return sigmoidf_(fmaf(mix, a0, base)) + hc_eps;
+}
+
 __device__ __forceinline__ float clamp_logit(float l, int apply, float lo, float hi) {
   // torch.clamp(l, lo, hi) == min(max(l, lo), hi)
   return apply ? fminf(fmaxf(l, lo), hi) : l;

@@ -81,7 +81,10 @@ int mhc_post_bwd(const void* grad_y, const void* x, const float* h_res, const vo
  * Optional outputs (may be NULL): inv_rms (T,), mixes (T,M), h_res_logits
  * (T,N,N) pre-clamp, pre (T,N), x_scaled (T,N*D) -- all fp32.
  * N in {4, 8}.  Any D >= 1; D % 8 == 0 with 16-byte aligned rows takes the
- * vectorised path.
+ * vectorised path.  mhc_pre_fwd_workspace_size includes, for N = 4 with bf16
+ * x and phi, D = 4096 or 7168 .. 8192 and T >= 8192, the exchange ring of the
+ * single-pass form (x read from HBM once, ~13 MB + 120 bytes per token); a
+ * smaller workspace that still holds the two-pass forms' runs those.
  */
 size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype);
 int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
@@ -97,8 +100,11 @@ int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dty
  * capture, tight serving loops, harnesses that forbid hipMalloc).  It calls
  * no hipMalloc / hipFree or other allocating routine: the workspace is a
  * static device array of MHC_PRE_FWD_SCRATCH_BYTES per GPU, held until the
- * process ends.  Calls whose mhc_pre_fwd_workspace_size exceeds it are
- * refused with MHC_ERR_INVALID (N = 4, bf16 phi: about 1.6 M tokens).  The
+ * process ends.  Calls whose two-pass workspace exceeds it are refused with
+ * MHC_ERR_INVALID (N = 4, bf16 phi: above about 3.3 M tokens); where the
+ * single-pass form's larger workspace fits too (N = 4, bf16, D = 4096 or
+ * 7168 .. 8192, T from 8192 to about 450 K tokens) that form runs, as in
+ * mhc_pre_fwd with a full workspace.  The
  * current device must be the one `stream` and the tensors belong to.  Every
  * call on a GPU shares that GPU's array: calls that overlap on one GPU (other
  * streams or threads) race.  Arguments and outputs as in mhc_pre_fwd.

@@ -56,7 +56,10 @@ def test_version_and_error_string(lib):
 
 def test_workspace_sizes(lib):
     # bf16 phi is used in place: the workspace holds pre (T,N) and inv_rms (T,) for the y kernel
-    assert lib.mhc_pre_fwd_workspace_size(65536, 4, 7168, 1) == 256 + 65536 * 4 * 4 + 65536 * 4
+    assert lib.mhc_pre_fwd_workspace_size(65536, 4, 5120, 1) == 256 + 65536 * 4 * 4 + 65536 * 4
+    # D = 7168: also room for the single-pass form (control words, exchange
+    # ring, the [T][24] and [T] sums for the finalize kernel, then pre / inv_rms)
+    assert lib.mhc_pre_fwd_workspace_size(65536, 4, 7168, 1) > 256 + 65536 * (16 + 4 + 25 * 4)
     fp32 = lib.mhc_pre_fwd_workspace_size(65536, 4, 7168, 0)
     assert fp32 >= 2 * 24 * 28672 * 2
     ws20 = lib.mhc_pre_bwd_workspace_size(65536, 4, 7168, 1, 20)
