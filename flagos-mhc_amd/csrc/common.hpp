@@ -163,11 +163,38 @@ constexpr int kDppXor1 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int kDppRor4 = 0x124;
 constexpr int kDppRor8 = 0x128;
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane l <- 7 - l within each 8 lanes
+
+// v + (v of lane xor 16) and v + (v of lane xor 32) with the gfx950 lane
+// swaps (one VALU instruction, no LDS round trip).  permlane16_swap(a, b)
+// exchanges the odd 16-lane rows of a with the even rows of b, permlane32
+// the upper half of a with the lower half of b; with a = b = v the two
+// results hold, lane for lane, v and its partner's v (in some order), so
+// their sum is the pair sum.
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 // Sum over lanes whose indices differ only in the bits of `mask`
 // (mask is a compile-time set of xor offsets, e.g. 0b0011 -> offsets 1 and 2).
-// Offsets 1, 2, 8 and the pair {4, 8} run on DPP; 4 alone and 16, 32 use
-// cross-lane shuffles.
+// Offsets 1, 2, 8 and the pair {4, 8} run on DPP, 4 after 1 and 2 as a
+// half-row mirror (every lane of a quad then holds the quad's sum), 16 and
+// 32 on the lane swaps; only 4 alone is a cross-lane shuffle.  Each step
+// adds a lane's value to its partner's, so the bits equal those of the
+// __shfl_xor form.
 template <int MASK>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (MASK & 1) v += dpp_mov<kDppXor1>(v);
@@ -177,11 +204,13 @@ __device__ __forceinline__ float group_sum(float v) {
     v += dpp_mov<kDppRor8>(v);  // {l, l-4, l-8, l-12}: the 4 lanes of l's class mod 4
   } else if constexpr (MASK & 8) {
     v += dpp_mov<kDppRor8>(v);
+  } else if constexpr ((MASK & 7) == 7) {
+    v += dpp_mov<kDppHalfMirror>(v);  // the other quad of the 8 lanes
   } else if constexpr (MASK & 4) {
     v += __shfl_xor(v, 4, kWave);
   }
-  if constexpr (MASK & 16) v += __shfl_xor(v, 16, kWave);
-  if constexpr (MASK & 32) v += __shfl_xor(v, 32, kWave);
+  if constexpr (MASK & 16) v = add_xor16(v);
+  if constexpr (MASK & 32) v = add_xor32(v);
   return v;
 }
 template <int MASK>
@@ -193,11 +222,13 @@ __device__ __forceinline__ float group_max(float v) {
     v = fmaxf(v, dpp_mov<kDppRor8>(v));
   } else if constexpr (MASK & 8) {
     v = fmaxf(v, dpp_mov<kDppRor8>(v));
+  } else if constexpr ((MASK & 7) == 7) {
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
   } else if constexpr (MASK & 4) {
     v = fmaxf(v, __shfl_xor(v, 4, kWave));
   }
-  if constexpr (MASK & 16) v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  if constexpr (MASK & 32) v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  if constexpr (MASK & 16) v = max_xor16(v);
+  if constexpr (MASK & 32) v = max_xor32(v);
   return v;
 }
 
