@@ -60,6 +60,9 @@ struct PreFwdArgs {
   float* part_ssq;
   float* pre_ws;
   float* inv_ws;
+  // single-pass form: its status word (nonzero when a bounded wait timed
+  // out); the finalize kernel then writes NaN to every output of the call
+  const uint32_t* co_status;
 };
 
 template <int N, typename S, bool VEC, int P>
@@ -616,8 +619,19 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
     acc_l += a.part[row * M + 2 * N + e];
     acc_h += a.part[row * M + eh];
   }
-  const float inv = rms_inv(ssq, K, a.norm_eps);
+  // a failed single-pass run makes every output of the call NaN (y and
+  // x_scaled rows included) rather than leave wrong values behind
+  const bool failed = a.co_status && *a.co_status != 0u;
+  const float inv = failed ? __builtin_nanf("") : rms_inv(ssq, K, a.norm_eps);
   const float mix_l = acc_l * inv, mix_h = acc_h * inv;
+  if (failed) {
+    const int64_t t0 = (int64_t)blockIdx.x * TPP;
+    const int64_t nt = T - t0 < TPP ? T - t0 : TPP;
+    uint16_t* y = static_cast<uint16_t*>(a.y);  // the single-pass form's y is bf16
+    for (int64_t i = tid; i < nt * a.D; i += kFwdThreads) y[t0 * a.D + i] = 0x7FC0u;  // bf16 NaN
+    if (a.x_scaled)
+      for (int64_t i = tid; i < nt * N * a.D; i += kFwdThreads) a.x_scaled[t0 * N * a.D + i] = __builtin_nanf("");
+  }
   if (ok) {
     if (a.mixes) {
       a.mixes[tok * M + 2 * N + e] = mix_l;
@@ -631,7 +645,8 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
   const float a0 = a.alpha[0], a1 = a.alpha[1], a2 = a.alpha[2];
   const float logit = mix_l * a2 + a.base[2 * N + e];
   const float lc = clamp_logit(logit, a.apply_clamp, a.cmin, a.cmax);
-  const float c = sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
+  // (the clamp would turn a NaN logit into a bound: NaN is set directly)
+  const float c = failed ? __builtin_nanf("") : sinkhorn_fwd<N>(lc, a.hc_eps, a.iters);
   if (ok) {
     a.comb[tok * L + e] = c;
     if (a.logits) a.logits[tok * L + e] = logit;

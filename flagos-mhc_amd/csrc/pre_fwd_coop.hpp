@@ -56,7 +56,8 @@
 // overwritten by tile q + kCoR only after every member's P-waves are past
 // tile q (kCoR >= 2 S + 2 kCoLag + 2 tiles, see CoCfg).  Every wait is
 // bounded: after kCoTimeout of s_memrealtime without progress a wave sets the
-// block's abort flag and the status word, and every wave leaves.
+// block's abort flag and the status word, and every wave leaves; the finalize
+// kernel then writes NaN to every output of the call.
 #pragma once
 
 namespace mhc {
@@ -115,6 +116,7 @@ struct CoopArgs {
   u32x4* rec;       // [maxg][kCoR][G][kCoRecWords], zeroed before the launch
   int G;            // members per group (D / CS)
   int maxg;         // groups the ring has room for
+  uint64_t timeout; // s_memrealtime ticks a wait may last without progress
 };
 
 // ---- LDS accesses of the L-waves (direct-to-LDS loads in flight: inline
@@ -179,16 +181,17 @@ __device__ __forceinline__ void co_lds_rd4(u32x4 (&v)[4], uint32_t a0, uint32_t 
 __device__ __forceinline__ uint64_t co_now() { return __builtin_amdgcn_s_memrealtime(); }
 
 // Wait until the LDS counter at `a` reaches `target` (or the block aborts /
-// kCoTimeout passes: then false, with the abort flag and status set).
+// `timeout` ticks pass without it: then false, with the abort flag and
+// status set).
 __device__ __forceinline__ void co_fail(uint32_t* status, uint32_t code) {
   uint32_t expected = 0u;
   __hip_atomic_compare_exchange_strong(status, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ bool co_wait_ge(uint32_t a, uint32_t target, uint32_t abort_a, uint32_t* status,
-                                           uint32_t code) {
+                                           uint32_t code, uint64_t timeout) {
   if (co_lds_ld(a) >= target) return true;
-  const uint64_t deadline = co_now() + kCoTimeout;
+  const uint64_t deadline = co_now() + timeout;
   for (;;) {
     if (co_lds_ld(a) >= target) return true;
     if (co_lds_ld(abort_a)) return false;
@@ -224,8 +227,8 @@ constexpr int kCoPolicySc1 = 16;
 template <int PVN>
 __device__ __forceinline__ bool co_poll_sum(u32x4 (&v)[PVN], const __amdgpu_buffer_rsrc_t& ring, uint32_t off0, int nm,
                                             bool active, uint32_t tag, float& s0, float& s1, uint32_t abort_a,
-                                            uint32_t* status) {
-  const uint64_t deadline = co_now() + kCoTimeout;
+                                            uint32_t* status, uint64_t timeout) {
+  const uint64_t deadline = co_now() + timeout;
   for (;;) {
     const uint32_t vo = active ? off0 : kBufferOob;
 #pragma unroll
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t T = a.T;
   const int D = a.D, K = 4 * D, G = ca.G;
-  const uint64_t deadline0 = co_now();
+  const uint64_t deadline0 = co_now(), to = ca.timeout;
   uint32_t* status = ca.ctl + kCtlStatus;
 
   // ---- group formation: the blocks of one XCC, in registration order ------
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     __hip_atomic_fetch_add(ca.ctl + kCtlArrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     bool ok = true;
     while (__hip_atomic_load(ca.ctl + kCtlArrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gridDim.x) {
-      if (co_now() > deadline0 + kCoTimeout) {
+      if (co_now() > deadline0 + ca.timeout) {
         ok = false;
         break;
       }
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     for (int64_t j = 0; j < nq && alive; ++j) {
       if (j + A < nq) {
         alive = co_wait_ge(c_copied + 4 * (uint32_t)((j + A) % S), (uint32_t)(YW * ((j + A) / S)), c_abort, status,
-                           kStLCopied);
+                           kStLCopied, to);
         if (!alive) break;
         issue(j + A);
       }
@@ -407,7 +410,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
 
       // partial -> pbuf[j % 2][w]; the buffer's previous tile must be published
       const int pb = (int)(j & 1);
-      alive = co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j / 2), c_abort, status, kStLPread);
+      alive = co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j / 2), c_abort, status, kStLPread, to);
       if (!alive) break;
       const uint32_t pw = lds_addr(&pbuf[pb][w][0]);
 #pragma unroll
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     auto rec_off = [&](int64_t t) { return (uint32_t)((t % kCoR) * G * kCoRecWords * 16) + poff; };
     const int sl = pw;
     for (int64_t u = pw; u < nq; u += kCoPW) {
-      if (!co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub)) break;
+      if (!co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to)) break;
       // two rounds of up to 16 members (register budget), added in member order
       const uint32_t tag = (uint32_t)(u + 1);
       float s0 = 0.f, s1 = 0.f;
@@ -505,13 +508,13 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
           h0 += __uint_as_float(PV[i][0]);
           h1 += __uint_as_float(PV[i][2]);
         }
-        if (__any(!ok) && !co_poll_sum<16>(PV, ring, vo, nmh, pact, tag, h0, h1, c_abort, status)) alive = false;
+        if (__any(!ok) && !co_poll_sum<16>(PV, ring, vo, nmh, pact, tag, h0, h1, c_abort, status, to)) alive = false;
         s0 = h == 0 ? h0 : s0 + h0;
         s1 = h == 0 ? h1 : s1 + h1;
       }
       if (!alive) break;
       // the slot's previous tile must be read by every Y-wave
-      if (!co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot)) break;
+      if (!co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot, to)) break;
       if (pact) {
         tot[sl][2 * lane] = s0;
         tot[sl][2 * lane + 1] = s1;
@@ -548,7 +551,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
 
   // tile j into Xc
   auto copy = [&](int64_t j, u32x4 (&Xc)[YB][4]) -> bool {
-    if (!co_wait_ge(c_landed + 4 * (uint32_t)(j % S), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status, kStYLanded))
+    if (!co_wait_ge(c_landed + 4 * (uint32_t)(j % S), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status, kStYLanded, to))
       return false;
 #pragma unroll
     for (int b = 0; b < YB; ++b) {
@@ -612,7 +615,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     if (j < nq && !copy(j, Xc)) return false;
     if (t >= 0 && t < nq) {
       const int sl = (int)(t % kCoPSlots);
-      if (!co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums))
+      if (!co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums, to))
         return false;
 #pragma unroll
       for (int b = 0; b < YB; ++b) {
@@ -735,6 +738,12 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   w += align256((size_t)kCoCtlWords * 4);
   ca.rec = reinterpret_cast<u32x4*>(w);
   ca.maxg = coop_max_groups(G);
+  // MHC_PRE_FWD_COOP_TIMEOUT (s_memrealtime ticks, 100 MHz) shortens the
+  // bounded waits: the tests set it to 0 to force the failure path (every
+  // wait that is not already satisfied gives up at once, the status word is
+  // set and the outputs become NaN)
+  ca.timeout = kCoTimeout;
+  if (const char* env = getenv("MHC_PRE_FWD_COOP_TIMEOUT")) ca.timeout = strtoull(env, nullptr, 10);
   const size_t rec_bytes = align256((size_t)ca.maxg * kCoR * G * kCoRecWords * 16);
   w += rec_bytes;
   a.part = reinterpret_cast<float*>(w);
@@ -757,6 +766,7 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
     return MHC_OK;
   }
   *used = true;
+  a.co_status = ca.ctl + kCtlStatus;  // a timed-out wait turns every output of the call into NaN
   hipLaunchKernelGGL((pre_fwd_finalize_kernel<4>), dim3((unsigned)((a.T + 15) / 16)), dim3(kFwdThreads), 0, st, a, 1);
   return check_launch("pre_fwd_finalize");
 }

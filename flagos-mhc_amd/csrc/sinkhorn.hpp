@@ -58,12 +58,11 @@ __device__ float sinkhorn_fwd(float lc, float eps, int iters) {
   return c;
 }
 
-// VJP through  out = u / (sum(u) + eps)  along the lanes of MASK, given out
-// and the incoming gradient g.
+// VJP through  out = u / s  with s = sum(u) + eps along the lanes of MASK,
+// given out, s and the incoming gradient g.
 template <int MASK>
-__device__ __forceinline__ float norm_vjp(float g, float u, float out, float eps) {
-  const float inv = 1.0f / (group_sum<MASK>(u) + eps);
-  return inv * (g - group_sum<MASK>(g * out));
+__device__ __forceinline__ float norm_vjp(float g, float out, float s) {
+  return (1.0f / s) * (g - group_sum<MASK>(g * out));
 }
 
 // Backward of one step C_k = colnorm(rownorm(C_{k-1})): given C_{k-1} and
@@ -71,10 +70,12 @@ __device__ __forceinline__ float norm_vjp(float g, float u, float out, float eps
 template <int N>
 __device__ __forceinline__ float sink_step_vjp(float cprev, float g, float eps) {
   constexpr int ROW = SinkLanes<N>::ROW, COL = SinkLanes<N>::COL;
-  const float r = cprev / (group_sum<ROW>(cprev) + eps);
-  const float c = r / (group_sum<COL>(r) + eps);
-  const float gr = norm_vjp<COL>(g, r, c, eps);
-  return norm_vjp<ROW>(gr, cprev, r, eps);
+  // each group sum once: the recomputed forward's denominators serve the VJP
+  const float sr = group_sum<ROW>(cprev) + eps;
+  const float r = cprev / sr;
+  const float sc = group_sum<COL>(r) + eps;
+  const float c = r / sc;
+  return norm_vjp<ROW>(norm_vjp<COL>(g, c, sc), r, sr);
 }
 
 // Backward of softmax + eps + first column normalisation: given the softmax
@@ -83,8 +84,8 @@ template <int N>
 __device__ __forceinline__ float sink_first_vjp(float s, float g, float eps) {
   constexpr int ROW = SinkLanes<N>::ROW, COL = SinkLanes<N>::COL;
   const float m0 = s + eps;
-  const float c0 = m0 / (group_sum<COL>(m0) + eps);
-  const float gm = norm_vjp<COL>(g, m0, c0, eps);
+  const float s0 = group_sum<COL>(m0) + eps;
+  const float gm = norm_vjp<COL>(g, m0 / s0, s0);
   return s * (gm - group_sum<ROW>(gm * s));
 }
 

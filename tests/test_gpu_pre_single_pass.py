@@ -134,3 +134,25 @@ def test_two_pass_workspace_is_not_the_single_pass():
     tp, _ = _run("two-pass", x, phi, alpha, base, False)
     assert not torch.equal(sp["mixes"], tp["mixes"])
     assert torch.allclose(sp["mixes"], tp["mixes"], rtol=1e-4, atol=2e-4)
+
+
+def test_single_pass_failure_is_loud(monkeypatch):
+    """With the waits' limit forced to zero ticks from the host (the
+    MHC_PRE_FWD_COOP_TIMEOUT hook), the single-pass kernel gives up at its
+    first unsatisfied wait and every kernel still exits; the status word is
+    set and every output of the call is NaN, never silently wrong.  The next
+    call with the normal limit is correct again."""
+    T, N, D = 8192, 4, 7168
+    x, phi, alpha, base = _inputs(T, N, D, seed=9)
+    good, ctl = _run("full", x, phi, alpha, base, True)
+    assert ctl[STATUS] == 0
+    monkeypatch.setenv("MHC_PRE_FWD_COOP_TIMEOUT", "0")
+    bad, ctl_bad = _run("full", x, phi, alpha, base, True)
+    assert ctl_bad[STATUS] != 0
+    for k, v in bad.items():
+        assert bool(torch.isnan(v.float()).all()), k
+    monkeypatch.delenv("MHC_PRE_FWD_COOP_TIMEOUT")
+    again, ctl2 = _run("full", x, phi, alpha, base, True)
+    assert ctl2[STATUS] == 0
+    for k in good:
+        assert torch.equal(good[k], again[k]), k
