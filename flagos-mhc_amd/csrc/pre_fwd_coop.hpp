@@ -178,6 +178,29 @@ __device__ __forceinline__ void co_lds_rd4(u32x4 (&v)[4], uint32_t a0, uint32_t 
       : "memory");
 }
 
+// Two 8-byte reads per stream, four streams STRIDE bytes apart: stream n's
+// reads at a0 + n STRIDE and a1 + n STRIDE land in v[n][0..1] and v[n][2..3].
+template <int STRIDE>
+__device__ __forceinline__ void co_lds_rd4x2(u32x4 (&v)[4], uint32_t a0, uint32_t a1) {
+  static_assert(3 * STRIDE < 65536, "ds_read offset field");
+  u32x2 h[8];
+  asm volatile(
+      "ds_read_b64 %0, %8\n\t"
+      "ds_read_b64 %1, %9\n\t"
+      "ds_read_b64 %2, %8 offset:%10\n\t"
+      "ds_read_b64 %3, %9 offset:%10\n\t"
+      "ds_read_b64 %4, %8 offset:%11\n\t"
+      "ds_read_b64 %5, %9 offset:%11\n\t"
+      "ds_read_b64 %6, %8 offset:%12\n\t"
+      "ds_read_b64 %7, %9 offset:%12\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]), "=&v"(h[4]), "=&v"(h[5]), "=&v"(h[6]), "=&v"(h[7])
+      : "v"(a0), "v"(a1), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE)
+      : "memory");
+#pragma unroll
+  for (int n = 0; n < 4; ++n) v[n] = u32x4{h[2 * n][0], h[2 * n][1], h[2 * n + 1][0], h[2 * n + 1][1]};
+}
+
 __device__ __forceinline__ uint64_t co_now() { return __builtin_amdgcn_s_memrealtime(); }
 
 // Wait until the LDS counter at `a` reaches `target` (or the block aborts /
@@ -548,6 +571,17 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     chunk[b] = 16 * (rb % H) + (kp ^ tok[b]);
   }
   float p[YB][4], inv[YB];  // pre and inv_rms of this lane's tokens
+  // With x_scaled the ring and the stores' data fill the register budget:
+  // the per-lane addresses are then recomputed from an opaque copy of the
+  // lane index at each use instead of being held across the loop (the
+  // compiler would spill them, and a scratch reload in this store-only wave
+  // waits for every store in flight).
+  auto lane_at_use = [&]() -> int {
+    int l = lane;
+    if constexpr (XS) asm volatile("" : "+v"(l));
+    return l;
+  };
+  auto tok_of = [&](int l, int b) -> int { return 4 * ((v + YW * b) / H) + (l >> 4); };
 
   // tile j into Xc
   auto copy = [&](int64_t j, u32x4 (&Xc)[YB][4]) -> bool {
@@ -555,8 +589,17 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       return false;
 #pragma unroll
     for (int b = 0; b < YB; ++b) {
-      const uint32_t o = sbase + (uint32_t)((j % S) * C::SLOT + (v + YW * b) * 1024 + lane * 16);
-      co_lds_rd4(Xc[b], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
+      if constexpr (XS) {
+        // columns 4 kp .. 4 kp + 3 and 64 + 4 kp .. of the half row: chunk
+        // kp / 2 and 8 + kp / 2, half kp % 2, each at the lane position
+        // chunk ^ token where the direct-to-LDS load put it
+        const int l = lane_at_use(), k2 = (l & 15) >> 1, tk = tok_of(l, b);
+        const uint32_t o = sbase + (uint32_t)((j % S) * C::SLOT + (v + YW * b) * 1024 + (l >> 4) * 256 + 8 * (l & 1));
+        co_lds_rd4x2<C::STREAM>(Xc[b], o + (uint32_t)((k2 ^ tk) * 16), o + (uint32_t)(((8 + k2) ^ tk) * 16));
+      } else {
+        const uint32_t o = sbase + (uint32_t)((j % S) * C::SLOT + (v + YW * b) * 1024 + lane * 16);
+        co_lds_rd4(Xc[b], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
+      }
     }
     co_lds_inc(c_copied + 4 * (uint32_t)(j % S));
     return true;
@@ -584,9 +627,18 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       u32x4 ov;
 #pragma unroll
       for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
-      const uint32_t col = (uint32_t)(slice0 + 8 * chunk[b]);
-      __builtin_amdgcn_raw_buffer_store_b128(ov, ys, ((uint32_t)tok[b] * D + col) * 2, 0, 2 /* nt */);
-      if constexpr (XS) {
+      if constexpr (!XS) {
+        const uint32_t col = (uint32_t)(slice0 + 8 * chunk[b]);
+        __builtin_amdgcn_raw_buffer_store_b128(ov, ys, ((uint32_t)tok[b] * D + col) * 2, 0, 2 /* nt */);
+      } else {
+        // columns col0 .. col0 + 3 (registers 0, 1) and col0 + 64 .. (2, 3):
+        // every store instruction writes contiguous runs (16-byte pieces at
+        // a 32-byte stride, as a lane's 8 columns would give, write at a
+        // third of the rate)
+        const int l = lane_at_use();
+        const uint32_t tk = (uint32_t)tok_of(l, b), col0 = (uint32_t)(slice0 + 128 * ((v + YW * b) % H) + 4 * (l & 15));
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{ov[0], ov[1]}, ys, (tk * D + col0) * 2, 0, 2);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{ov[2], ov[3]}, ys, (tk * D + col0) * 2 + 128u, 0, 2);
         const auto xr = rows_rsrc(a.x_scaled + t0 * 4 * D, (int64_t)nv * 4 * D * 4);
 #pragma unroll
         for (int n = 0; n < 4; ++n)
@@ -599,7 +651,12 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
               xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv[b]);
               xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv[b]);
             }
-            __builtin_amdgcn_raw_buffer_store_b128(xs, xr, (((uint32_t)tok[b] * 4 + n) * D + col + 4 * h) * 4, 0, 2);
+            // The stream offset goes into the lane offset, soffset stays the
+            // constant 0: with a register soffset the compiler does not
+            // separate a 16-byte store from the next write of its data
+            // registers, and on gfx950 that lost the data of the last four
+            // lanes of each sixteen now and then.
+            __builtin_amdgcn_raw_buffer_store_b128(xs, xr, ((tk * 4 + n) * D + col0) * 4 + 256u * h, 0, 2);
           }
       }
     }
@@ -640,7 +697,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
                                               0, 0);
       }
       if (des) {  // the designated member: the y values' totals to part / part_ssq
-        const int vt = pv / kCoTT, tk = pv % kCoTT;
+        const int pl = (v - 1) * kWave + lane_at_use(), vt = pl / kCoTT, tk = pl % kCoTT;
         if (vt == 4) {
           const auto ss = rows_rsrc(a.part_ssq + t0, (int64_t)nv * 4);
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dv), ss, (uint32_t)tk * 4, 0, 0);
