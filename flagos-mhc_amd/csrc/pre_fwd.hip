@@ -681,7 +681,53 @@ __global__ __launch_bounds__(kWave * kFwdYWaves) void pre_fwd_y_kernel(PreFwdArg
   float p[N];
 #pragma unroll
   for (int n = 0; n < N; ++n) p[n] = a.pre_ws[t * N + n];
-  const float inv = XS ? a.inv_ws[t] : 0.f;
+  if constexpr (XS) {
+    // lane l takes columns 4 l .. 4 l + 3 and 256 + 4 l .. of each chunk, so
+    // every store instruction writes one contiguous run (fp32 16-byte pieces
+    // at a 32-byte lane stride, as 8 columns a lane would give, write at
+    // about a third of the contiguous rate).  D % 8 == 0: a 4-column piece
+    // is in range when its first column is.
+    const float inv = a.inv_ws[t];
+    for (int c0 = wave * 512; c0 < D; c0 += W * 512) {
+      const int col = c0 + 4 * lane;
+      const bool hi = col + 256 < D;  // the lane's second piece is in range
+      const bf16_t* x = static_cast<const bf16_t*>(a.x) + t * N * D + col;
+      u32x2 X[2][N];  // all loads before any store (one in-order counter covers both)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+          X[h][n] = (h == 0 ? col < D : hi)
+                        ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + (int64_t)n * D + 256 * h))
+                        : u32x2{0u, 0u};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (!(h == 0 ? col < D : hi)) break;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int n = 0; n < N; ++n)
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            o[2 * w] = fmaf(p[n], __uint_as_float(X[h][n][w] << 16), o[2 * w]);
+            o[2 * w + 1] = fmaf(p[n], __uint_as_float(X[h][n][w] & 0xffff0000u), o[2 * w + 1]);
+          }
+        const u32x2 ov = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        __builtin_nontemporal_store(ov,
+                                    reinterpret_cast<u32x2*>(static_cast<bf16_t*>(a.y) + t * D + col + 256 * h));
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+          u32x4 xs;
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            xs[2 * w] = __float_as_uint(__uint_as_float(X[h][n][w] << 16) * inv);
+            xs[2 * w + 1] = __float_as_uint(__uint_as_float(X[h][n][w] & 0xffff0000u) * inv);
+          }
+          st16nt(a.x_scaled + (t * N + n) * (int64_t)D + col + 256 * h, xs);
+        }
+      }
+    }
+    return;
+  }
   for (int col = wave * 512 + 8 * lane; col < D; col += W * 512) {
     const bf16_t* x = static_cast<const bf16_t*>(a.x) + t * N * D + col;
     u32x4 X[N];
@@ -701,21 +747,6 @@ __global__ __launch_bounds__(kWave * kFwdYWaves) void pre_fwd_y_kernel(PreFwdArg
 #pragma unroll
     for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
     st16nt(static_cast<bf16_t*>(a.y) + t * D + col, ov);
-    if constexpr (XS) {
-#pragma unroll
-      for (int n = 0; n < N; ++n)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          u32x4 xs;
-#pragma unroll
-          for (int w = 0; w < 2; ++w) {
-            const uint32_t xw = X[n][2 * h + w];
-            xs[2 * w] = __float_as_uint(__uint_as_float(xw << 16) * inv);
-            xs[2 * w + 1] = __float_as_uint(__uint_as_float(xw & 0xffff0000u) * inv);
-          }
-          st16nt(a.x_scaled + (t * N + n) * (int64_t)D + col + 4 * h, xs);
-        }
-    }
   }
 }
 

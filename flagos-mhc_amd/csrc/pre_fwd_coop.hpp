@@ -765,7 +765,7 @@ inline bool coop_supported(const void* kernel, int threads, int nch) {
   int coop = 0, nb = 0;
   bool ok = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess && coop &&
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1;
-  hipGetLastError();
+  (void)hipGetLastError();
   slot.store(ok ? 1 : -1, std::memory_order_relaxed);
   return ok;
 }
@@ -783,7 +783,7 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   if (!nch || !need || !workspace || workspace_bytes < kPreFwdWsBase + need) return MHC_OK;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-    hipGetLastError();
+    (void)hipGetLastError();
     return MHC_OK;
   }
   const void* kfn = (const void*)pre_fwd_coop_kernel<32, XS>;
@@ -819,7 +819,7 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   void* args[] = {&ca};
   const hipError_t e = hipLaunchCooperativeKernel(kfn, dim3((unsigned)device_cu_count()), dim3(threads), args, 0, st);
   if (e != hipSuccess) {  // not co-resident after all: the caller runs the two-pass forms
-    hipGetLastError();
+    (void)hipGetLastError();
     return MHC_OK;
   }
   *used = true;
