@@ -411,8 +411,11 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
 
       // contraction of this stream's 16 x CS slice: fresh MFMA chain
       const uint32_t sl = sbase + (uint32_t)((j % S) * C::SLOT + w * C::STREAM);
+      // sum(x^2) on the matrix cores too: the A operand is also the B operand
+      // of x x^T (the register layouts coincide), whose diagonal holds each
+      // token's sum of squares
       floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-      float ssq = 0.f;
+      floatx4 gram = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int sg = 0; sg < STEPS; sg += 4) {  // four steps' operands at a time (register budget)
         u32x4 Ar[4];
@@ -420,16 +423,13 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float lo = __uint_as_float(Ar[s][u] << 16), hi = __uint_as_float(Ar[s][u] & 0xffff0000u);
-            ssq = fmaf(lo, lo, fmaf(hi, hi, ssq));
-          }
-#pragma unroll
           for (int mt = 0; mt < 2; ++mt) acc[mt] = mfma16x16x32(as_bf16x8(Ar[s]), as_bf16x8(B[sg + s][mt]), acc[mt]);
+          gram = mfma16x16x32(as_bf16x8(Ar[s]), as_bf16x8(Ar[s]), gram);
         }
       }
-      ssq += __shfl_xor(ssq, 16, kWave);
-      ssq += __shfl_xor(ssq, 32, kWave);
+      // token r's sum of squares: row r of column r, element r % 4 of lane (r, r / 4)
+      const int e4 = r & 3;
+      const float ssq = e4 == 0 ? gram[0] : e4 == 1 ? gram[1] : e4 == 2 ? gram[2] : gram[3];
 
       // partial -> pbuf[j % 2][w]; the buffer's previous tile must be published
       const int pb = (int)(j & 1);
@@ -441,7 +441,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         const int m = 16 * mt + r;  // lane (r, q) holds tokens 4q..4q+3 of mix m
         if (m < M) co_lds_st4(pw + (uint32_t)((co_vidx(m) * kCoTT + 4 * q) * 4), acc[mt]);
       }
-      if (q == 0) co_lds_st(pw + (uint32_t)((4 * kCoTT + r) * 4), ssq);
+      if (q == (r >> 2)) co_lds_st(pw + (uint32_t)((4 * kCoTT + r) * 4), ssq);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const uint32_t old = co_lds_inc_rtn(c_pcnt + 4 * (uint32_t)pb);
       if (old == 4u * (uint32_t)(j / 2) + 3u) {
