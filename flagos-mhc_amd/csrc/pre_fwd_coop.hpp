@@ -126,8 +126,11 @@ __device__ __forceinline__ uint32_t co_lds_ld(uint32_t a) {
   asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
   return v;
 }
+// No wait: a wave's LDS operations are performed in issue order, so a count
+// raised after LDS writes is seen only after them, and nothing this wave
+// does next depends on the add having landed.
 __device__ __forceinline__ void co_lds_add(uint32_t a, uint32_t v) {
-  asm volatile("ds_add_u32 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(a), "v"(v) : "memory");
+  asm volatile("ds_add_u32 %0, %1" ::"v"(a), "v"(v) : "memory");
 }
 __device__ __forceinline__ uint32_t co_lds_add_rtn(uint32_t a, uint32_t v) {
   uint32_t old;
@@ -150,19 +153,51 @@ __device__ __forceinline__ void co_lds_st(uint32_t a, float v) {
 __device__ __forceinline__ void co_lds_st4(uint32_t a, floatx4 v) {  // a 16-byte aligned
   asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
 }
-// the value pairs at a (8-byte aligned) of the four L-waves' partials (WB
-// bytes apart): v[w] = wave w's pair
-template <int WB>
-__device__ __forceinline__ void co_lds_rd_part(float2 (&v)[4], uint32_t a) {
-  static_assert(3 * WB < 65536, "ds_read offset field");
+// The 200 value pairs of a record from the four L-waves' partials (1600
+// bytes apart) in one batch: v[it][w] = wave w's pair of word 64 it + lane;
+// words 0..191 from a = base + 8 lane, words 192.. from a3 (lanes past the
+// record read word 199 again).
+__device__ __forceinline__ void co_lds_rd_rec(float2 (&v)[4][4], uint32_t a, uint32_t a3) {
+  static_assert(kCoTT * kCoVals * 4 == 1600 && kCoRecWords == 200, "offsets below");
   asm volatile(
-      "ds_read_b64 %0, %4\n\t"
-      "ds_read_b64 %1, %4 offset:%5\n\t"
-      "ds_read_b64 %2, %4 offset:%6\n\t"
-      "ds_read_b64 %3, %4 offset:%7\n\t"
+      "ds_read_b64 %0, %16\n\t"
+      "ds_read_b64 %1, %16 offset:1600\n\t"
+      "ds_read_b64 %2, %16 offset:3200\n\t"
+      "ds_read_b64 %3, %16 offset:4800\n\t"
+      "ds_read_b64 %4, %16 offset:512\n\t"
+      "ds_read_b64 %5, %16 offset:2112\n\t"
+      "ds_read_b64 %6, %16 offset:3712\n\t"
+      "ds_read_b64 %7, %16 offset:5312\n\t"
+      "ds_read_b64 %8, %16 offset:1024\n\t"
+      "ds_read_b64 %9, %16 offset:2624\n\t"
+      "ds_read_b64 %10, %16 offset:4224\n\t"
+      "ds_read_b64 %11, %16 offset:5824\n\t"
+      "ds_read_b64 %12, %17\n\t"
+      "ds_read_b64 %13, %17 offset:1600\n\t"
+      "ds_read_b64 %14, %17 offset:3200\n\t"
+      "ds_read_b64 %15, %17 offset:4800\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
-      : "v"(a), "i"(WB), "i"(2 * WB), "i"(3 * WB)
+      : "=&v"(v[0][0]), "=&v"(v[0][1]), "=&v"(v[0][2]), "=&v"(v[0][3]), "=&v"(v[1][0]), "=&v"(v[1][1]),
+        "=&v"(v[1][2]), "=&v"(v[1][3]), "=&v"(v[2][0]), "=&v"(v[2][1]), "=&v"(v[2][2]), "=&v"(v[2][3]),
+        "=&v"(v[3][0]), "=&v"(v[3][1]), "=&v"(v[3][2]), "=&v"(v[3][3])
+      : "v"(a), "v"(a3)
+      : "memory");
+}
+// eight 16-byte reads at base + o[i]
+__device__ __forceinline__ void co_lds_rd8(u32x4 (&v)[8], uint32_t base, const uint32_t (&o)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\t"
+      "ds_read_b128 %5, %13\n\t"
+      "ds_read_b128 %6, %14\n\t"
+      "ds_read_b128 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+      : "v"(base + o[0]), "v"(base + o[1]), "v"(base + o[2]), "v"(base + o[3]), "v"(base + o[4]), "v"(base + o[5]),
+        "v"(base + o[6]), "v"(base + o[7])
       : "memory");
 }
 // four 16-byte reads at independent addresses
@@ -416,14 +451,14 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       // token's sum of squares
       floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
       floatx4 gram = {0.f, 0.f, 0.f, 0.f};
+      static_assert(STEPS == 8, "the slice's operands in one batch of eight reads");
+      {
+        u32x4 Ar[8];
+        co_lds_rd8(Ar, sl, aoff);
 #pragma unroll
-      for (int sg = 0; sg < STEPS; sg += 4) {  // four steps' operands at a time (register budget)
-        u32x4 Ar[4];
-        co_lds_rd4(Ar, sl + aoff[sg], sl + aoff[sg + 1], sl + aoff[sg + 2], sl + aoff[sg + 3]);
+        for (int s = 0; s < STEPS; ++s) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) acc[mt] = mfma16x16x32(as_bf16x8(Ar[s]), as_bf16x8(B[sg + s][mt]), acc[mt]);
+          for (int mt = 0; mt < 2; ++mt) acc[mt] = mfma16x16x32(as_bf16x8(Ar[s]), as_bf16x8(B[s][mt]), acc[mt]);
           gram = mfma16x16x32(as_bf16x8(Ar[s]), as_bf16x8(Ar[s]), gram);
         }
       }
@@ -442,7 +477,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         if (m < M) co_lds_st4(pw + (uint32_t)((co_vidx(m) * kCoTT + 4 * q) * 4), acc[mt]);
       }
       if (q == (r >> 2)) co_lds_st(pw + (uint32_t)((4 * kCoTT + r) * 4), ssq);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // no wait: the count below is raised after these writes (issue order)
       const uint32_t old = co_lds_inc_rtn(c_pcnt + 4 * (uint32_t)pb);
       if (old == 4u * (uint32_t)(j / 2) + 3u) {
         // last of the four: add the partials in stream order and publish
@@ -450,13 +485,14 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         // ring layout [tile][member][word]: a record is one contiguous run
         const uint32_t dst = (uint32_t)(((j % kCoR) * G + member) * kCoRecWords * 16);  // byte offset in the ring
         const uint32_t p0 = lds_addr(&pbuf[pb][0][0]);
-        constexpr int WB = kCoTT * kCoVals * 4;  // bytes between the waves' partials
+        float2 pr[4][4];
+        co_lds_rd_rec(pr, p0 + (uint32_t)(8 * lane),
+                      p0 + (uint32_t)(8 * (3 * kWave + (lane < kCoRecWords - 3 * kWave ? lane : kCoRecWords - 1 - 3 * kWave))));
 #pragma unroll
-        for (int it = 0; it < (kCoRecWords + kWave - 1) / kWave; ++it) {
+        for (int it = 0; it < 4; ++it) {
           const int wd = lane + kWave * it;
           if (wd < kCoRecWords) {
-            float2 pv[4];
-            co_lds_rd_part<WB>(pv, p0 + (uint32_t)(8 * wd));
+            const float2(&pv)[4] = pr[it];
             u32x4 word;
             word[0] = __float_as_uint(((pv[0].x + pv[1].x) + pv[2].x) + pv[3].x);
             word[1] = tag;
