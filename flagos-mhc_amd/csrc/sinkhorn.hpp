@@ -13,7 +13,12 @@
 // (src/mhc_pre_clamp_sinkhorn_backward.py:1440-1453); here the normalisation
 // VJP  du = inv * (g - sum(g * out))  is applied along columns / rows in
 // reverse order, using the column-normalised states C_k kept in registers
-// (iters <= kSinkRegIters) or in caller scratch (longer runs).
+// (iters <= kSinkRegIters) or in caller scratch (longer runs).  The backward
+// divides by multiplying with v_rcp_f32 (1 ulp) instead of the correctly
+// rounded division sequence (about ten instructions each, half of the VJP's
+// instructions): its states and gradient differ from the exact ones by a few
+// ulp, far inside the gradient tolerance, while the forward output keeps the
+// correctly rounded divisions.
 #pragma once
 
 #include "common.hpp"
@@ -58,11 +63,32 @@ __device__ float sinkhorn_fwd(float lc, float eps, int iters) {
   return c;
 }
 
+// 1 / s by v_rcp_f32 (s >= eps > 0 here: no denormal or zero inputs)
+__device__ __forceinline__ float rcp1(float s) { return __builtin_amdgcn_rcpf(s); }
+
+// the backward's recomputation of the forward states (reciprocal multiplies)
+template <int N>
+__device__ __forceinline__ float sink_step_r(float c, float eps) {
+  const float r = c * rcp1(group_sum<SinkLanes<N>::ROW>(c) + eps);
+  return r * rcp1(group_sum<SinkLanes<N>::COL>(r) + eps);
+}
+template <int N>
+__device__ __forceinline__ float sink_softmax_r(float lc) {
+  const float mx = group_max<SinkLanes<N>::ROW>(lc);
+  const float e = expf(lc - mx);
+  return e * rcp1(group_sum<SinkLanes<N>::ROW>(e));
+}
+template <int N>
+__device__ __forceinline__ float sink_first_r(float s, float eps) {
+  const float m0 = s + eps;
+  return m0 * rcp1(group_sum<SinkLanes<N>::COL>(m0) + eps);
+}
+
 // VJP through  out = u / s  with s = sum(u) + eps along the lanes of MASK,
 // given out, s and the incoming gradient g.
 template <int MASK>
 __device__ __forceinline__ float norm_vjp(float g, float out, float s) {
-  return (1.0f / s) * (g - group_sum<MASK>(g * out));
+  return rcp1(s) * (g - group_sum<MASK>(g * out));
 }
 
 // Backward of one step C_k = colnorm(rownorm(C_{k-1})): given C_{k-1} and
@@ -72,9 +98,9 @@ __device__ __forceinline__ float sink_step_vjp(float cprev, float g, float eps) 
   constexpr int ROW = SinkLanes<N>::ROW, COL = SinkLanes<N>::COL;
   // each group sum once: the recomputed forward's denominators serve the VJP
   const float sr = group_sum<ROW>(cprev) + eps;
-  const float r = cprev / sr;
+  const float r = cprev * rcp1(sr);
   const float sc = group_sum<COL>(r) + eps;
-  const float c = r / sc;
+  const float c = r * rcp1(sc);
   return norm_vjp<ROW>(norm_vjp<COL>(g, c, sc), r, sr);
 }
 
@@ -85,7 +111,7 @@ __device__ __forceinline__ float sink_first_vjp(float s, float g, float eps) {
   constexpr int ROW = SinkLanes<N>::ROW, COL = SinkLanes<N>::COL;
   const float m0 = s + eps;
   const float s0 = group_sum<COL>(m0) + eps;
-  const float gm = norm_vjp<COL>(g, m0 / s0, s0);
+  const float gm = norm_vjp<COL>(g, m0 * rcp1(s0), s0);
   return s * (gm - group_sum<ROW>(gm * s));
 }
 
@@ -94,11 +120,11 @@ __device__ __forceinline__ float sink_first_vjp(float s, float g, float eps) {
 template <int N>
 __device__ float sinkhorn_vjp_regs(float lc, float g, float eps, int iters) {
   float st[kSinkRegIters];
-  const float s = sink_softmax<N>(lc);
-  st[0] = sink_first<N>(s, eps);
+  const float s = sink_softmax_r<N>(lc);
+  st[0] = sink_first_r<N>(s, eps);
 #pragma unroll
   for (int k = 1; k < kSinkRegIters; ++k)
-    if (k < iters - 1) st[k] = sink_step<N>(st[k - 1], eps);
+    if (k < iters - 1) st[k] = sink_step_r<N>(st[k - 1], eps);
 #pragma unroll
   for (int k = kSinkRegIters - 1; k >= 1; --k)
     if (k < iters) g = sink_step_vjp<N>(st[k - 1], g, eps);
@@ -110,11 +136,11 @@ __device__ float sinkhorn_vjp_regs(float lc, float g, float eps, int iters) {
 template <int N>
 __device__ float sinkhorn_vjp_scratch(float lc, float g, float eps, int iters, float* buf,
                                       int64_t stride) {
-  const float s = sink_softmax<N>(lc);
-  float c = sink_first<N>(s, eps);
+  const float s = sink_softmax_r<N>(lc);
+  float c = sink_first_r<N>(s, eps);
   for (int k = 0; k < iters - 1; ++k) {
     buf[k * stride] = c;
-    c = sink_step<N>(c, eps);
+    c = sink_step_r<N>(c, eps);
   }
   for (int k = iters - 1; k >= 1; --k) g = sink_step_vjp<N>(buf[(k - 1) * stride], g, eps);
   return sink_first_vjp<N>(s, g, eps);
