@@ -57,7 +57,57 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
   const int64_t xrow = t * (int64_t)N * D;
   const int64_t hrow = t * (int64_t)D;
 
-  if constexpr (VECTOR) {
+  if constexpr (VECTOR && N == 8 && std::is_same<S, bf16_t>::value) {
+    // N = 8: the N*N + N dot products take v_dot2_f32_bf16 on the packed
+    // rows (two bf16 products and an fp32 add per instruction, no unpacking
+    // of x and h_out); only grad_y is unpacked, for grad_x and grad_h_out
+    constexpr int V = 8;
+    auto dot2 = [](uint32_t a, uint32_t b, float c) {
+      return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                             false);
+    };
+    for (int d = lane * V; d < D; d += kWave * V) {
+      u32x4 graw[N], xraw[N];
+#pragma unroll
+      for (int i = 0; i < N; ++i) graw[i] = ld16nt(gy + xrow + (int64_t)i * D + d);
+#pragma unroll
+      for (int j = 0; j < N; ++j) xraw[j] = ld16nt(x + xrow + (int64_t)j * D + d);
+      const u32x4 hraw = ld16nt(h_out + hrow + d);
+      float gv[N][V];
+#pragma unroll
+      for (int i = 0; i < N; ++i) Store<S>::unpack(graw[i], gv[i]);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float o[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          float a = 0.f;
+#pragma unroll
+          for (int i = 0; i < N; ++i) a = fmaf(hr[j * N + i], gv[i][e], a);
+          o[e] = a;
+        }
+        st16nt(gx + xrow + (int64_t)j * D + d, Store<S>::pack(o));
+      }
+      float oh[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) a = fmaf(hp[i], gv[i][e], a);
+        oh[e] = a;
+      }
+      st16nt(g_hout + hrow + d, Store<S>::pack(oh));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+#pragma unroll
+          for (int i = 0; i < N; ++i) acc_r[j * N + i] = dot2(xraw[j][w], graw[i][w], acc_r[j * N + i]);
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc_p[i] = dot2(hraw[w], graw[i][w], acc_p[i]);
+      }
+    }
+  } else if constexpr (VECTOR) {
     constexpr int V = Store<S>::VEC;
     for (int d = lane * V; d < D; d += kWave * V) {
       float gv[N][V], xv[N][V], hv[V];
