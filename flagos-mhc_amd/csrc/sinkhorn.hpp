@@ -13,12 +13,11 @@
 // (src/mhc_pre_clamp_sinkhorn_backward.py:1440-1453); here the normalisation
 // VJP  du = inv * (g - sum(g * out))  is applied along columns / rows in
 // reverse order, using the column-normalised states C_k kept in registers
-// (iters <= kSinkRegIters) or in caller scratch (longer runs).  The backward
-// divides by multiplying with v_rcp_f32 (1 ulp) instead of the correctly
-// rounded division sequence (about ten instructions each, half of the VJP's
-// instructions): its states and gradient differ from the exact ones by a few
-// ulp, far inside the gradient tolerance, while the forward output keeps the
-// correctly rounded divisions.
+// (iters <= kSinkRegIters) or in caller scratch (longer runs).  Both
+// directions divide by multiplying with v_rcp_f32 (1 ulp) instead of the
+// correctly rounded division sequence (about ten instructions each, half of
+// the VJP's instructions): states, output and gradient differ from exactly
+// rounded ones by a few ulp, far inside the tolerances.
 #pragma once
 
 #include "common.hpp"
@@ -34,39 +33,11 @@ template <int N> struct SinkLanes {
   static_assert((N & (N - 1)) == 0 && L <= kWave, "N must be a power of two, N*N <= 64");
 };
 
-// One (row, column) normalisation pair: C_{k-1} -> C_k.
-template <int N>
-__device__ __forceinline__ float sink_step(float c, float eps) {
-  const float r = c / (group_sum<SinkLanes<N>::ROW>(c) + eps);
-  return r / (group_sum<SinkLanes<N>::COL>(r) + eps);
-}
-
-// softmax output (without eps) of this lane's row.
-template <int N>
-__device__ __forceinline__ float sink_softmax(float lc) {
-  const float mx = group_max<SinkLanes<N>::ROW>(lc);
-  const float e = expf(lc - mx);
-  return e / group_sum<SinkLanes<N>::ROW>(e);
-}
-
-template <int N>
-__device__ __forceinline__ float sink_first(float s, float eps) {
-  const float m0 = s + eps;
-  return m0 / (group_sum<SinkLanes<N>::COL>(m0) + eps);
-}
-
-// Forward only; returns this lane's comb_frag element.
-template <int N>
-__device__ float sinkhorn_fwd(float lc, float eps, int iters) {
-  float c = sink_first<N>(sink_softmax<N>(lc), eps);
-  for (int k = 1; k < iters; ++k) c = sink_step<N>(c, eps);
-  return c;
-}
-
 // 1 / s by v_rcp_f32 (s >= eps > 0 here: no denormal or zero inputs)
 __device__ __forceinline__ float rcp1(float s) { return __builtin_amdgcn_rcpf(s); }
 
-// the backward's recomputation of the forward states (reciprocal multiplies)
+// One (row, column) normalisation pair C_{k-1} -> C_k, the softmax output
+// (without eps) of this lane's row, and the first column normalisation.
 template <int N>
 __device__ __forceinline__ float sink_step_r(float c, float eps) {
   const float r = c * rcp1(group_sum<SinkLanes<N>::ROW>(c) + eps);
@@ -82,6 +53,14 @@ template <int N>
 __device__ __forceinline__ float sink_first_r(float s, float eps) {
   const float m0 = s + eps;
   return m0 * rcp1(group_sum<SinkLanes<N>::COL>(m0) + eps);
+}
+
+// Forward only; returns this lane's comb_frag element.
+template <int N>
+__device__ float sinkhorn_fwd(float lc, float eps, int iters) {
+  float c = sink_first_r<N>(sink_softmax_r<N>(lc), eps);
+  for (int k = 1; k < iters; ++k) c = sink_step_r<N>(c, eps);
+  return c;
 }
 
 // VJP through  out = u / s  with s = sum(u) + eps along the lanes of MASK,
