@@ -486,27 +486,43 @@ def main():
     # A stack of mHC layers runs mhc_post of layer l and mhc_pre_clamp_sinkhorn
     # of layer l+1 back to back, and its backward adds the pre backward's
     # grad_x to the residual-stream gradient of the same tensor.  The fused
-    # forward replaces post_fwd + pre_fwd; the accumulating pre backward
-    # replaces pre_bwd + that add.  Reported beside the defined metric.
+    # forward replaces post_fwd + pre_fwd; the add is folded into the post
+    # backward (mhc_post_backward_sum reads both parts) or, where the post
+    # kernel has no summed form, into the pre backward (accumulating form).
+    # Reported beside the defined metric.
     from FlagOS_mhc.mhc_pre_clamp_sinkhorn_backward import _pre_backward
     fused = lambda: m.mhc_post_pre_clamp_sinkhorn(x, o["comb_frag"], h_out, o["post_out"], phi, alpha,
                                                   base, need_backward=True, **kw)
     acc = lambda: _pre_backward(x, phi, alpha, base, o["inv_rms"], o["mixes"], o["pre"], pb[2], pb[3],
                                 pb[1], kw["norm_eps"], kw["hc_eps"], kw["clamp_min"], kw["clamp_max"],
                                 kw["iter_times"], grad_x_in=pb[0])
+    from FlagOS_mhc.mhc_post_backward import post_backward_sum_fused
+    post_sum = lambda: m.mhc_post_backward_sum(gup, pb[0], x, o["comb_frag"], h_out, o["post_out"])
     fused()
     acc()
+    post_sum()
     f_med, f_mean = time_events(fused, reps, stream)
     a_mean = time_events(acc, reps, stream)[1]
+    s_mean = time_events(post_sum, reps, stream)[1]
+    # the layer's backward as the fused autograd function runs it at this
+    # shape: pre backward + post backward of the two-part gradient, or the
+    # accumulating pre backward + post backward
+    sum_path = post_backward_sum_fused(T, N, D, x.dtype)
+    bwd_sum = op_stats["pre_bwd"]["ms"] + s_mean
+    bwd_acc = a_mean + op_stats["post_bwd"]["ms"]
     f_algo = T * (2 * N * D * 2 + 2 * D * 2 + 4 * (N * N + N) + 4 * (4 * N + 3 * N * N + 1)) \
         + (2 * N + N * N) * N * D * 2
-    layer_fused = f_mean + op_stats["post_bwd"]["ms"] + a_mean
+    layer_fused = f_mean + (bwd_sum if sum_path else bwd_acc)
     layer_unfused = sum(v["ms"] for v in op_stats.values()) + glue["grad_x_accumulate_ms"]
     post_pre = {"fwd_ms": round(f_mean, 4), "fwd_ms_median": round(f_med, 4),
                 "fwd_unfused_ms": round(op_stats["post_fwd"]["ms"] + op_stats["pre_fwd"]["ms"], 4),
                 "fwd_algo_GB": round(f_algo / 1e9, 4),
                 "fwd_GBps": round(f_algo / (f_mean * 1e-3) / 1e9, 1),
                 "pre_bwd_acc_ms": round(a_mean, 4),
+                "post_bwd_sum_ms": round(s_mean, 4),
+                "layer_bwd": "pre_bwd + post_bwd_sum" if sum_path else "pre_bwd_acc + post_bwd",
+                "layer_bwd_ms": {"pre_bwd + post_bwd_sum": round(bwd_sum, 4),
+                                 "pre_bwd_acc + post_bwd": round(bwd_acc, 4)},
                 "pre_bwd_plus_add_ms": round(op_stats["pre_bwd"]["ms"] + glue["grad_x_accumulate_ms"], 4),
                 "layer_ms": round(layer_fused, 4), "layer_unfused_ms": round(layer_unfused, 4),
                 "layer_tokens_per_s": round(T / (layer_fused * 1e-3), 1),

@@ -13,14 +13,16 @@ functions are the pure-PyTorch references of the same semantics.
     mhc_post_fn, mhc_pre_clamp_sinkhorn_fn   (autograd wrappers)
 
 Beyond the reference: ``mhc_post_pre_clamp_sinkhorn`` (and its autograd
-form) fuses mhc_post of one layer with mhc_pre_clamp_sinkhorn of the next.
+form) fuses mhc_post of one layer with mhc_pre_clamp_sinkhorn of the next;
+``mhc_post_backward_sum`` is mhc_post_backward for a gradient given as two
+summands (the fused layer's backward).
 
 Importing the package also registers the operators as torch.ops.flagos_mhc.*
 (``FlagOS_mhc.library``) for torch.compile and HIP-graph capture.
 """
 
 from .mhc_post import mhc_post, mhc_post_ref
-from .mhc_post_backward import mhc_post_backward, mhc_post_backward_ref
+from .mhc_post_backward import mhc_post_backward, mhc_post_backward_ref, mhc_post_backward_sum
 from .mhc_pre_clamp_sinkhorn import (
     mhc_pre_clamp_sinkhorn,
     mhc_pre_clamp_sinkhorn_ref,
@@ -57,4 +59,6 @@ __all__ = [
     "mhc_post_pre_clamp_sinkhorn",
     "MhcPostPreClampSinkhornFn",
     "mhc_post_pre_clamp_sinkhorn_fn",
+    # beyond the reference: mhc_post_backward for a gradient given as two summands
+    "mhc_post_backward_sum",
 ]

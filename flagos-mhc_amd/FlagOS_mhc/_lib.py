@@ -28,6 +28,9 @@ _SIGNATURES = {
     "mhc_post_fwd": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp]),
     "mhc_post_bwd": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _i64, _i32, _i32, _i32, _vp]),
+    "mhc_post_bwd_sum": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                    _i64, _i32, _i32, _i32, _vp]),
+    "mhc_post_bwd_sum_fused": (_c.c_int, [_i64, _i32, _i32, _i32]),
     "mhc_pre_fwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "mhc_pre_fwd": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,

@@ -6,7 +6,7 @@ from __future__ import annotations
 import torch
 
 from .mhc_post import mhc_post
-from .mhc_post_backward import mhc_post_backward
+from .mhc_post_backward import mhc_post_backward, mhc_post_backward_sum, post_backward_sum_fused
 from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from .mhc_pre_clamp_sinkhorn import _pre_forward
 from .mhc_pre_clamp_sinkhorn_backward import _pre_backward, mhc_pre_clamp_sinkhorn_backward
@@ -86,9 +86,12 @@ def mhc_pre_clamp_sinkhorn_fn(
 
 class MhcPostPreClampSinkhornFn(torch.autograd.Function):
     """mhc_post (layer l) + mhc_pre_clamp_sinkhorn (layer l+1) with one fused
-    forward.  The backward runs the pre backward on x_next with the gradient
-    that reaches x_next directly accumulated into its grad_x in the same
-    kernel (``mhc_pre_bwd_acc``), then the post backward."""
+    forward.  The backward runs the pre backward on x_next, then the post
+    backward for x_next's whole gradient: the post kernel reads the pre
+    backward's grad_x beside the gradient that reaches x_next directly
+    (``mhc_post_bwd_sum``).  Where the post kernel for the shape has no
+    summed form (N = 4 bf16, D < 5120), the pre backward adds that gradient
+    into its grad_x instead (``mhc_pre_bwd_acc``)."""
 
     @staticmethod
     def forward(ctx, x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
@@ -113,11 +116,17 @@ class MhcPostPreClampSinkhornFn(torch.autograd.Function):
         if grad_comb_frag is None:
             N = pre.shape[-1]
             grad_comb_frag = torch.zeros((pre.shape[0], N, N), dtype=torch.float32, device=pre.device)
+        N, D = x.shape[-2], x.shape[-1]
+        use_sum = grad_x_next is not None and post_backward_sum_fused(x.numel() // (N * D), N, D, x.dtype)
         g, gphi, galpha, gbase = _pre_backward(
             x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
             grad_post_out.contiguous(), grad_comb_frag.contiguous(), norm_eps, hc_eps, clamp_min,
-            clamp_max, iter_times, grad_x_in=grad_x_next, compensated=ctx.compensated)
-        gx, ghres, ghout, ghpost = mhc_post_backward(g, x, h_res, h_out, h_post)
+            clamp_max, iter_times, grad_x_in=None if use_sum else grad_x_next,
+            compensated=ctx.compensated)
+        if use_sum:
+            gx, ghres, ghout, ghpost = mhc_post_backward_sum(grad_x_next, g, x, h_res, h_out, h_post)
+        else:
+            gx, ghres, ghout, ghpost = mhc_post_backward(g, x, h_res, h_out, h_post)
         return gx, ghres, ghout, ghpost, gphi, galpha, gbase, None, None, None, None, None, None
 
 

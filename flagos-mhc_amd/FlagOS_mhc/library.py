@@ -7,6 +7,8 @@ HIP-graph capture records their kernels on the current stream):
     torch.ops.flagos_mhc.mhc_post(x, h_res, h_out, h_post) -> y
     torch.ops.flagos_mhc.mhc_post_backward(grad_y, x, h_res, h_out, h_post)
         -> (grad_x, grad_h_res, grad_h_out, grad_h_post)
+    torch.ops.flagos_mhc.mhc_post_backward_sum(grad_y, grad_y2, x, h_res, h_out,
+        h_post) -> the same for the gradient grad_y + grad_y2
     torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, norm_eps,
         hc_eps, clamp_min, clamp_max, iter_times)
         -> (y, post_out, comb_frag, inv_rms, mixes, pre)
@@ -41,7 +43,7 @@ import torch
 from torch import Tensor
 
 from .mhc_post import mhc_post
-from .mhc_post_backward import mhc_post_backward
+from .mhc_post_backward import mhc_post_backward, mhc_post_backward_sum, post_backward_sum_fused
 from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
 from .mhc_pre_clamp_sinkhorn import _pre_forward
 from .mhc_pre_clamp_sinkhorn_backward import _pre_backward, mhc_pre_clamp_sinkhorn_backward
@@ -72,6 +74,17 @@ def _post_bwd_fake(grad_y, x, h_res, h_out, h_post):
     out_shape = tuple(grad_y.shape[:-2]) + (grad_y.shape[-1],)
     return (grad_y.new_empty(grad_y.shape, dtype=x.dtype), h_res.new_empty(h_res.shape),
             h_out.new_empty(out_shape), h_post.new_empty(h_post.shape))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::mhc_post_backward_sum", mutates_args=())
+def _post_bwd_sum(grad_y: Tensor, grad_y2: Tensor, x: Tensor, h_res: Tensor, h_out: Tensor,
+                  h_post: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    return tuple(mhc_post_backward_sum(grad_y, grad_y2, x, h_res, h_out, h_post))
+
+
+@_post_bwd_sum.register_fake
+def _post_bwd_sum_fake(grad_y, grad_y2, x, h_res, h_out, h_post):
+    return _post_bwd_fake(grad_y, x, h_res, h_out, h_post)
 
 
 def _post_setup(ctx, inputs, output):
@@ -208,10 +221,21 @@ def _post_pre_setup(ctx, inputs, output):
 def _post_pre_grad(ctx, grad_x_next, grad_y, grad_post_out, grad_comb_frag, _g_inv, _g_mixes,
                    _g_pre):
     x, h_res, h_out, h_post, phi, alpha, base, x_next, inv_rms, mixes, pre = ctx.saved_tensors
-    g, gphi, galpha, gbase = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward_acc(
-        x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
-        grad_post_out.contiguous(), grad_comb_frag.contiguous(), grad_x_next.contiguous(), *ctx.args)
-    gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward(g, x, h_res, h_out, h_post)
+    # as MhcPostPreClampSinkhornFn.backward: the post kernel reads both parts
+    # of x_next's gradient where it has a summed form, else the pre backward
+    # adds them
+    N, D = x.shape[-2], x.shape[-1]
+    if post_backward_sum_fused(x.numel() // (N * D), N, D, x.dtype):
+        g, gphi, galpha, gbase = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward(
+            x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
+            grad_post_out.contiguous(), grad_comb_frag.contiguous(), *ctx.args)
+        gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward_sum(
+            grad_x_next.contiguous(), g, x, h_res, h_out, h_post)
+    else:
+        g, gphi, galpha, gbase = torch.ops.flagos_mhc.mhc_pre_clamp_sinkhorn_backward_acc(
+            x_next, phi, alpha, base, inv_rms, mixes, pre, grad_y.contiguous(),
+            grad_post_out.contiguous(), grad_comb_frag.contiguous(), grad_x_next.contiguous(), *ctx.args)
+        gx, ghres, ghout, ghpost = torch.ops.flagos_mhc.mhc_post_backward(g, x, h_res, h_out, h_post)
     return (gx, ghres, ghout, ghpost, gphi.to(phi.dtype), galpha.reshape(alpha.shape).to(alpha.dtype),
             gbase.reshape(base.shape).to(base.dtype), None, None, None, None, None, None)
 

@@ -40,14 +40,36 @@ def _flatten(grad_y, x, h_res, h_out, h_post):
 
 def mhc_post_backward(grad_y, x, h_res, h_out, h_post):
     """Backward of mhc_post on the HIP device (no CPU fallback)."""
-    _lib.require_device("mhc_post_backward", grad_y, x, h_res, h_out, h_post)
+    return _post_backward("mhc_post_backward", grad_y, None, x, h_res, h_out, h_post)
+
+
+def mhc_post_backward_sum(grad_y, grad_y2, x, h_res, h_out, h_post):
+    """mhc_post_backward for the incoming gradient grad_y + grad_y2 (same
+    shape and dtype, added in fp32 inside the kernel as they are read).  Not
+    part of the reference's API: the fused post + pre layer's backward uses it
+    so that the pre backward's grad_x and the gradient reaching x_next
+    directly are never summed into a tensor of their own."""
+    if grad_y2.shape != grad_y.shape:
+        raise ValueError(f"mhc_post_backward_sum: grad_y2 shape {tuple(grad_y2.shape)} "
+                         f"!= grad_y shape {tuple(grad_y.shape)}")
+    return _post_backward("mhc_post_backward_sum", grad_y, grad_y2, x, h_res, h_out, h_post)
+
+
+def post_backward_sum_fused(T: int, N: int, D: int, dtype: torch.dtype) -> bool:
+    """True when mhc_post_backward_sum runs the kernel form mhc_post_backward
+    would for this shape (one more read, no slower form)."""
+    return bool(_lib.load().mhc_post_bwd_sum_fused(T, N, D, _lib.dtype_code("mhc_post_backward_sum", dtype)))
+
+
+def _post_backward(what, grad_y, grad_y2, x, h_res, h_out, h_post):
+    _lib.require_device(what, grad_y, x, h_res, h_out, h_post, grad_y2)
     gy, xf, hres, hout, hpost, shape4, shape_out = _flatten(grad_y, x, h_res, h_out, h_post)
     T, N, D = gy.shape
     if N not in SUPPORTED_N:
-        raise NotImplementedError(
-            f"mhc_post_backward: N={N} not supported (supported: {SUPPORTED_N})")
-    code = _lib.dtype_code("mhc_post_backward", xf.dtype)
+        raise NotImplementedError(f"{what}: N={N} not supported (supported: {SUPPORTED_N})")
+    code = _lib.dtype_code(what, xf.dtype)
     gy = gy.to(xf.dtype).contiguous()
+    gy2 = None if grad_y2 is None else grad_y2.reshape(T, N, D).to(xf.dtype).contiguous()
     hout_k = hout.to(xf.dtype).contiguous()
     hres_k = hres.to(torch.float32).contiguous()
     hpost_k = hpost.to(torch.float32).contiguous()
@@ -59,11 +81,14 @@ def mhc_post_backward(grad_y, x, h_res, h_out, h_post):
     if T > 0:
         lib = _lib.load()
         with torch.cuda.device(xf.device):
-            rc = lib.mhc_post_bwd(gy.data_ptr(), xf.data_ptr(), hres_k.data_ptr(),
-                                  hout_k.data_ptr(), hpost_k.data_ptr(), grad_x.data_ptr(),
-                                  grad_hres.data_ptr(), grad_hout.data_ptr(),
-                                  grad_hpost.data_ptr(), T, N, D, code, _lib.stream_of(xf))
-        _lib.check(rc, "mhc_post_backward")
+            tail = (hres_k.data_ptr(), hout_k.data_ptr(), hpost_k.data_ptr(), grad_x.data_ptr(),
+                    grad_hres.data_ptr(), grad_hout.data_ptr(), grad_hpost.data_ptr(), T, N, D, code,
+                    _lib.stream_of(xf))
+            if gy2 is None:
+                rc = lib.mhc_post_bwd(gy.data_ptr(), xf.data_ptr(), *tail)
+            else:
+                rc = lib.mhc_post_bwd_sum(gy.data_ptr(), gy2.data_ptr(), xf.data_ptr(), *tail)
+        _lib.check(rc, what)
     return (
         grad_x.reshape(shape4),
         grad_hres.to(h_res.dtype).reshape(h_res.shape),

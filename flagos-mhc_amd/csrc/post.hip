@@ -31,12 +31,14 @@ constexpr int kPostWavesPerBlock = 4;
 
 // MINW: waves per SIMD the register allocation must allow (2 caps the
 // kernel at 256 VGPRs).
-template <int N, typename S, bool VECTOR, int MINW = 1>
+// SUM: the incoming gradient is gy + gy2 (two tensors of gy's layout, added
+// in fp32 as they are read).
+template <int N, typename S, bool VECTOR, int MINW = 1, bool SUM = false>
 __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
     const S* __restrict__ gy, const S* __restrict__ x, const float* __restrict__ h_res,
     const S* __restrict__ h_out, const float* __restrict__ h_post, S* __restrict__ gx,
     float* __restrict__ g_hres, S* __restrict__ g_hout, float* __restrict__ g_hpost,
-    int64_t T, int D) {
+    int64_t T, int D, const S* __restrict__ gy2) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t = (int64_t)blockIdx.x * kPostWavesPerBlock + wave;
@@ -57,7 +59,7 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
   const int64_t xrow = t * (int64_t)N * D;
   const int64_t hrow = t * (int64_t)D;
 
-  if constexpr (VECTOR && N == 8 && std::is_same<S, bf16_t>::value) {
+  if constexpr (VECTOR && N == 8 && std::is_same<S, bf16_t>::value && !SUM) {
     // N = 8: the N*N + N dot products take v_dot2_f32_bf16 on the packed
     // rows (two bf16 products and an fp32 add per instruction, no unpacking
     // of x and h_out); only grad_y is unpacked, for grad_x and grad_h_out
@@ -113,6 +115,15 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
       float gv[N][V], xv[N][V], hv[V];
 #pragma unroll
       for (int i = 0; i < N; ++i) Store<S>::unpack(ld16nt(gy + xrow + (int64_t)i * D + d), gv[i]);
+      if constexpr (SUM) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          float g2[V];
+          Store<S>::unpack(ld16nt(gy2 + xrow + (int64_t)i * D + d), g2);
+#pragma unroll
+          for (int e = 0; e < V; ++e) gv[i][e] += g2[e];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < N; ++j) Store<S>::unpack(ld16nt(x + xrow + (int64_t)j * D + d), xv[j]);
       Store<S>::unpack(ld16nt(h_out + hrow + d), hv);
@@ -151,7 +162,10 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
     for (int d = lane; d < D; d += kWave) {
       float gv[N], xv[N];
 #pragma unroll
-      for (int i = 0; i < N; ++i) gv[i] = load_elem(gy, xrow + (int64_t)i * D + d);
+      for (int i = 0; i < N; ++i) {
+        gv[i] = load_elem(gy, xrow + (int64_t)i * D + d);
+        if constexpr (SUM) gv[i] += load_elem(gy2, xrow + (int64_t)i * D + d);
+      }
 #pragma unroll
       for (int j = 0; j < N; ++j) xv[j] = load_elem(x, xrow + (int64_t)j * D + d);
       const float hv = load_elem(h_out, hrow + d);
@@ -250,11 +264,12 @@ __global__ __launch_bounds__(kWave * kPostFwdBlockWaves) void post_fwd_block_ker
   }
 }
 
-template <int N, typename S, bool VECTOR>
+template <int N, typename S, bool VECTOR, bool SUM = false>  // SUM as in post_bwd_kernel
 __global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel(
     const S* __restrict__ gy, const S* __restrict__ x, const float* __restrict__ h_res,
     const S* __restrict__ h_out, const float* __restrict__ h_post, S* __restrict__ gx,
-    float* __restrict__ g_hres, S* __restrict__ g_hout, float* __restrict__ g_hpost, int D) {
+    float* __restrict__ g_hres, S* __restrict__ g_hout, float* __restrict__ g_hpost, int D,
+    const S* __restrict__ gy2) {
   constexpr int V = VECTOR ? Store<S>::VEC : 1, CW = kWave * V, R = N * N + N;
   __shared__ float red[kPostBlockWaves][R];
   const int lane = threadIdx.x & (kWave - 1);
@@ -277,12 +292,24 @@ __global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel
     if constexpr (VECTOR) {
 #pragma unroll
       for (int i = 0; i < N; ++i) Store<S>::unpack(ld16nt(gy + xrow + (int64_t)i * D + d), gv[i]);
+      if constexpr (SUM) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+          float g2[V];
+          Store<S>::unpack(ld16nt(gy2 + xrow + (int64_t)i * D + d), g2);
+#pragma unroll
+          for (int e = 0; e < V; ++e) gv[i][e] += g2[e];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < N; ++j) Store<S>::unpack(ld16nt(x + xrow + (int64_t)j * D + d), xv[j]);
       Store<S>::unpack(ld16nt(h_out + hrow + d), hv);
     } else {
 #pragma unroll
-      for (int i = 0; i < N; ++i) gv[i][0] = load_elem(gy, xrow + (int64_t)i * D + d);
+      for (int i = 0; i < N; ++i) {
+        gv[i][0] = load_elem(gy, xrow + (int64_t)i * D + d);
+        if constexpr (SUM) gv[i][0] += load_elem(gy2, xrow + (int64_t)i * D + d);
+      }
 #pragma unroll
       for (int j = 0; j < N; ++j) xv[j][0] = load_elem(x, xrow + (int64_t)j * D + d);
       hv[0] = load_elem(h_out, hrow + d);
@@ -663,31 +690,50 @@ static int launch_post_fwd(const void* x, const float* h_res, const void* h_out,
   return check_launch("post_fwd_block");
 }
 
+// True when the LDS-pipelined kernel (which has no summed-gradient form)
+// is the backward's kernel for this shape.
 template <int N, typename S>
-static int launch_post_bwd(const void* gy, const void* x, const float* h_res, const void* h_out,
+static bool post_bwd_uses_dma(int64_t T, int D, bool vec) {
+  return N == 4 && std::is_same<S, bf16_t>::value && vec && T >= kPostStreamMinT && D < kPostBlockMinD;
+}
+
+// gy2 == nullptr: the gradient is gy; otherwise gy + gy2 (the block and
+// wave-per-token kernels; the LDS-pipelined kernel's shapes take the block
+// kernel then).
+template <int N, typename S>
+static int launch_post_bwd(const void* gy, const void* gy2, const void* x, const float* h_res, const void* h_out,
                            const float* h_post, void* gx, float* g_hres, void* g_hout,
                            float* g_hpost, int64_t T, int D, hipStream_t st) {
   const dim3 grid((unsigned)((T + kPostWavesPerBlock - 1) / kPostWavesPerBlock));
   const dim3 block(kWave * kPostWavesPerBlock);
   const bool vec = (D % Store<S>::VEC == 0) && aligned16(gy) && aligned16(x) &&
-                   aligned16(h_out) && aligned16(gx) && aligned16(g_hout);
-  bool block_form = T < kPostStreamMinT || N <= 4;
-  if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
-    if (vec && T >= kPostStreamMinT && D < kPostBlockMinD) block_form = false;  // LDS-pipelined kernel
-  }
+                   aligned16(h_out) && aligned16(gx) && aligned16(g_hout) && (!gy2 || aligned16(gy2));
+  const bool sum = gy2 != nullptr;
+  const bool dma = post_bwd_uses_dma<N, S>(T, D, vec);
+  const bool block_form = T < kPostStreamMinT || (N <= 4 && !dma) || (sum && dma);
+  const S* g2 = static_cast<const S*>(gy2);
   if (block_form) {
     const dim3 gs((unsigned)T), bs(kWave * post_block_waves(D, vec ? Store<S>::VEC : 1, kPostBlockWaves));
     if (int rc = check_grid(gs, bs, "mhc_post_bwd")) return rc;
-    if (vec)
-      hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
-                         h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D);
-    else
-      hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)gy, (const S*)x,
-                         h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D);
+    if (sum) {
+      if (vec)
+        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                           h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
+      else
+        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                           h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                           h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
+      else
+        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                           h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
+    }
     return check_launch("post_bwd_block");
   }
   if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
-    if (vec) {
+    if (dma) {
       const int64_t g = post_dma_grid(post_bwd_dma_kernel<N>, T);
       hipLaunchKernelGGL((post_bwd_dma_kernel<N>), dim3((unsigned)g), block, 0, st, (const bf16_t*)gy,
                          (const bf16_t*)x, h_res, (const bf16_t*)h_out, h_post, (bf16_t*)gx, g_hres,
@@ -695,24 +741,35 @@ static int launch_post_bwd(const void* gy, const void* x, const float* h_res, co
       return check_launch("post_bwd_dma");
     }
   }
+  if (sum) {
+    if (vec)
+      hipLaunchKernelGGL((post_bwd_kernel<N, S, true, 1, true>), grid, block, 0, st, (const S*)gy,
+                         (const S*)x, h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout,
+                         g_hpost, T, D, g2);
+    else
+      hipLaunchKernelGGL((post_bwd_kernel<N, S, false, 1, true>), grid, block, 0, st, (const S*)gy,
+                         (const S*)x, h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout,
+                         g_hpost, T, D, g2);
+    return check_launch("post_bwd");
+  }
   if constexpr (N == 8) {
     // 270 VGPRs leave one wave per SIMD; capped at 256 (a 60-byte spill) two
     // fit, which pays at narrow rows (D = 2048, T = 32768: 729 -> 629 us) but
     // not wider ones (D = 4096: 706 -> 756 us; D = 7168: equal)
     if (vec && D <= 2048) {
       hipLaunchKernelGGL((post_bwd_kernel<N, S, true, 2>), grid, block, 0, st, (const S*)gy, (const S*)x, h_res,
-                         (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, T, D);
+                         (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, T, D, g2);
       return check_launch("post_bwd");
     }
   }
   if (vec)
     hipLaunchKernelGGL((post_bwd_kernel<N, S, true>), grid, block, 0, st, (const S*)gy,
                        (const S*)x, h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout,
-                       g_hpost, T, D);
+                       g_hpost, T, D, g2);
   else
     hipLaunchKernelGGL((post_bwd_kernel<N, S, false>), grid, block, 0, st, (const S*)gy,
                        (const S*)x, h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout,
-                       g_hpost, T, D);
+                       g_hpost, T, D, g2);
   return check_launch("post_bwd");
 }
 
@@ -730,15 +787,15 @@ static int dispatch_post_fwd_n(const void* x, const float* h_res, const void* h_
 }
 
 template <typename S>
-static int dispatch_post_bwd_n(const void* gy, const void* x, const float* h_res,
+static int dispatch_post_bwd_n(const void* gy, const void* gy2, const void* x, const float* h_res,
                                const void* h_out, const float* h_post, void* gx, float* g_hres,
                                void* g_hout, float* g_hpost, int64_t T, int N, int D,
                                hipStream_t st) {
   switch (N) {
-    case 2: return launch_post_bwd<2, S>(gy, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
-    case 4: return launch_post_bwd<4, S>(gy, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
-    case 6: return launch_post_bwd<6, S>(gy, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
-    case 8: return launch_post_bwd<8, S>(gy, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
+    case 2: return launch_post_bwd<2, S>(gy, gy2, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
+    case 4: return launch_post_bwd<4, S>(gy, gy2, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
+    case 6: return launch_post_bwd<6, S>(gy, gy2, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
+    case 8: return launch_post_bwd<8, S>(gy, gy2, x, h_res, h_out, h_post, gx, g_hres, g_hout, g_hpost, T, D, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_post_bwd: N=%d not supported (2, 4, 6, 8)", N);
 }
@@ -764,21 +821,47 @@ extern "C" int mhc_post_fwd(const void* x, const float* h_res, const void* h_out
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_post_fwd: dtype %d not supported", dtype);
 }
 
+static int post_bwd_entry(const char* what, const void* grad_y, const void* grad_y2, const void* x,
+                          const float* h_res, const void* h_out, const float* h_post, void* grad_x,
+                          float* grad_h_res, void* grad_h_out, float* grad_h_post, int64_t T, int32_t N,
+                          int32_t D, int32_t dtype, void* stream) {
+  clear_error();
+  if (T < 0 || D <= 0) return set_error(MHC_ERR_INVALID, "%s: bad shape T=%lld D=%d", what, (long long)T, D);
+  if (int rc = check_tokens(T, what)) return rc;
+  if (T == 0) return MHC_OK;
+  if (!grad_y || !x || !h_res || !h_out || !h_post || !grad_x || !grad_h_res || !grad_h_out || !grad_h_post)
+    return set_error(MHC_ERR_INVALID, "%s: null pointer", what);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case MHC_DTYPE_BF16: return dispatch_post_bwd_n<bf16_t>(grad_y, grad_y2, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out, grad_h_post, T, N, D, st);
+    case MHC_DTYPE_F16: return dispatch_post_bwd_n<f16_t>(grad_y, grad_y2, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out, grad_h_post, T, N, D, st);
+    case MHC_DTYPE_F32: return dispatch_post_bwd_n<float>(grad_y, grad_y2, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out, grad_h_post, T, N, D, st);
+  }
+  return set_error(MHC_ERR_UNSUPPORTED, "%s: dtype %d not supported", what, dtype);
+}
+
 extern "C" int mhc_post_bwd(const void* grad_y, const void* x, const float* h_res,
                             const void* h_out, const float* h_post, void* grad_x,
                             float* grad_h_res, void* grad_h_out, float* grad_h_post, int64_t T,
                             int32_t N, int32_t D, int32_t dtype, void* stream) {
-  clear_error();
-  if (T < 0 || D <= 0) return set_error(MHC_ERR_INVALID, "mhc_post_bwd: bad shape T=%lld D=%d", (long long)T, D);
-  if (int rc = check_tokens(T, "mhc_post_bwd")) return rc;
-  if (T == 0) return MHC_OK;
-  if (!grad_y || !x || !h_res || !h_out || !h_post || !grad_x || !grad_h_res || !grad_h_out || !grad_h_post)
-    return set_error(MHC_ERR_INVALID, "mhc_post_bwd: null pointer");
-  hipStream_t st = (hipStream_t)stream;
-  switch (dtype) {
-    case MHC_DTYPE_BF16: return dispatch_post_bwd_n<bf16_t>(grad_y, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out, grad_h_post, T, N, D, st);
-    case MHC_DTYPE_F16: return dispatch_post_bwd_n<f16_t>(grad_y, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out, grad_h_post, T, N, D, st);
-    case MHC_DTYPE_F32: return dispatch_post_bwd_n<float>(grad_y, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out, grad_h_post, T, N, D, st);
+  return post_bwd_entry("mhc_post_bwd", grad_y, nullptr, x, h_res, h_out, h_post, grad_x, grad_h_res, grad_h_out,
+                        grad_h_post, T, N, D, dtype, stream);
+}
+
+extern "C" int mhc_post_bwd_sum(const void* grad_y, const void* grad_y2, const void* x, const float* h_res,
+                                const void* h_out, const float* h_post, void* grad_x, float* grad_h_res,
+                                void* grad_h_out, float* grad_h_post, int64_t T, int32_t N, int32_t D,
+                                int32_t dtype, void* stream) {
+  if (!grad_y2) {
+    clear_error();
+    return set_error(MHC_ERR_INVALID, "mhc_post_bwd_sum: null pointer");
   }
-  return set_error(MHC_ERR_UNSUPPORTED, "mhc_post_bwd: dtype %d not supported", dtype);
+  return post_bwd_entry("mhc_post_bwd_sum", grad_y, grad_y2, x, h_res, h_out, h_post, grad_x, grad_h_res,
+                        grad_h_out, grad_h_post, T, N, D, dtype, stream);
+}
+
+extern "C" int mhc_post_bwd_sum_fused(int64_t T, int32_t N, int32_t D, int32_t dtype) {
+  // aligned rows assumed (the caller's tensors come from the allocator)
+  if (N == 4 && dtype == MHC_DTYPE_BF16) return post_bwd_uses_dma<4, bf16_t>(T, D, D % 8 == 0) ? 0 : 1;
+  return 1;
 }

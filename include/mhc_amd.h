@@ -70,6 +70,27 @@ int mhc_post_bwd(const void* grad_y, const void* x, const float* h_res, const vo
                  void* stream);
 
 /*
+ * mhc_post backward for the incoming gradient grad_y + grad_y2 (both (T,N,D)
+ * `dtype`, added in fp32 as they are read; other arguments as mhc_post_bwd).
+ * No counterpart in the reference: it serves the backward of a fused
+ * post(l) + pre(l+1) layer, where x_next's gradient has two parts (the one
+ * that reaches x_next directly and the pre backward's grad_x) and the post
+ * backward of layer l reads both instead of a kernel writing their sum.
+ */
+int mhc_post_bwd_sum(const void* grad_y, const void* grad_y2, const void* x, const float* h_res,
+                     const void* h_out, const float* h_post, void* grad_x, float* grad_h_res,
+                     void* grad_h_out, float* grad_h_post, int64_t T, int32_t N, int32_t D,
+                     int32_t dtype, void* stream);
+
+/*
+ * 1 when mhc_post_bwd_sum runs the kernel form mhc_post_bwd runs for this
+ * shape (16-byte aligned rows), plus one read; 0 when that form has no
+ * summed variant (N = 4 bf16, T >= 1024, D < 5120) and mhc_post_bwd_sum takes
+ * a slower one.  No counterpart in the reference.
+ */
+int mhc_post_bwd_sum_fused(int64_t T, int32_t N, int32_t D, int32_t dtype);
+
+/*
  * mhc_pre_clamp_sinkhorn forward.  Replaces the device work of
  * mhc_pre_clamp_sinkhorn (src/mhc_pre_clamp_sinkhorn.py:857-971; semantics of
  * mhc_pre_clamp_sinkhorn_ref, :974-1022): RMSNorm over N*D, the N*D -> M

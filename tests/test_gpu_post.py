@@ -155,6 +155,42 @@ def test_post_bwd_parity(T, N, D, dtype, gates):
         assert torch.equal(a, b)
 
 
+SUM_CASES = [
+    # (T, N, D, dtype, the summed form is the kernel mhc_post_backward runs)
+    (1100, 4, 7168, torch.bfloat16, True),    # block-per-token kernel (config 5 width)
+    (1100, 4, 4096, torch.bfloat16, False),   # LDS-pipelined shape: the block kernel stands in
+    (1100, 8, 2048, torch.bfloat16, True),    # wave-per-token kernel (config 4 width)
+    (100, 4, 512, torch.bfloat16, True),      # few tokens: block kernel
+    (1030, 4, 264, torch.float32, True),      # fp32 rows
+    (70, 8, 100, torch.bfloat16, True),       # D % 8 != 0: element-wise loads
+]
+
+
+@pytest.mark.parametrize("T,N,D,dtype,fused", SUM_CASES)
+def test_post_bwd_sum_parity(T, N, D, dtype, fused):
+    """mhc_post_backward_sum(gy, gy2, ...) against the fp64 oracle for the
+    exact gradient gy + gy2 (the kernel adds the two in fp32 as it reads
+    them), on a token subset; bitwise repeatable; and its kernel-form query."""
+    print(f"[post_bwd_sum] T={T} N={N} D={D} {dtype}", flush=True)
+    from FlagOS_mhc.mhc_post_backward import post_backward_sum_fused
+    assert post_backward_sum_fused(T, N, D, dtype) == fused
+    x, h_res, h_out, h_post, gy = post_inputs(T, N, D, dtype, seed=11)
+    gy2 = torch.randn(T, N, D, device=DEV, generator=_gen(12)).to(dtype)
+    out = m.mhc_post_backward_sum(gy, gy2, x, h_res, h_out, h_post)
+    torch.cuda.synchronize()
+    rtol, atol = tol_for(dtype)
+    idx = _subset(T)
+    w = orc.post_bwd(_np(gy[idx]) + _np(gy2[idx]), _np(x[idx]), _np(h_res[idx]), _np(h_out[idx]),
+                     _np(h_post[idx]))
+    assert_close(out[0][idx], w[0], rtol, atol, "grad_x")
+    assert_close(out[2][idx], w[2], rtol, atol, "grad_h_out")
+    for got, want, name in ((out[1][idx], w[1], "grad_h_res"), (out[3][idx], w[3], "grad_h_post")):
+        assert_close(got, want, 1e-4, 1e-4 * np.abs(want).max(), name)
+    again = m.mhc_post_backward_sum(gy, gy2, x, h_res, h_out, h_post)
+    for a, b in zip(again, out):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("N,D,dtype", [
     (4, 4096, torch.bfloat16),   # 1100 tokens: LDS-pipelined kernels (D < 5120)
     (4, 2048, torch.bfloat16),

@@ -109,11 +109,13 @@ def test_post_pre_bsnd_and_no_backward_outputs():
     assert torch.equal(out["y"].reshape(B * S, D), out_flat["y"])
 
 
-@pytest.mark.parametrize("D", [3584, 1024])
-def test_post_pre_autograd(D):
+@pytest.mark.parametrize("T,D", [(96, 3584), (96, 1024), (1100, 1024), (1100, 5120)])
+def test_post_pre_autograd(T, D):
     """x -> fused(post, pre) -> loss on x_next, y, post_out and comb_frag,
-    against the unfused autograd chain mhc_post_fn then mhc_pre_clamp_sinkhorn_fn."""
-    T, N = 96, 4
+    against the unfused autograd chain mhc_post_fn then mhc_pre_clamp_sinkhorn_fn.
+    (1100, 1024) takes the accumulating pre backward (the post kernel for
+    that shape has no summed form); the others the summed post backward."""
+    N = 4
     print(f"[post_pre autograd] T={T} N={N} D={D}", flush=True)
     x, h_res, h_out, h_post, phi, alpha, base = _inputs(T, N, D, torch.bfloat16, seed=7)
     g = _gen(8)
@@ -136,11 +138,12 @@ def test_post_pre_autograd(D):
     y, p, c = m.mhc_pre_clamp_sinkhorn_fn(xn, b[4], b[5], b[6], **KW)
     loss(xn, y, p, c).backward()
     torch.cuda.synchronize()
-    # The fused backward rounds x_next's total gradient once (grad_x_next +
-    # dL/dx accumulated in fp32 inside the pre backward), the unfused chain
-    # twice (dL/dx to bf16, then autograd's bf16 add); h_res / h_post
-    # gradients are D-long sums over that gradient, so they get an absolute
-    # tolerance of 1% of their largest entry.
+    # The fused backward rounds x_next's total gradient at most once (the
+    # summed post backward adds grad_x_next and the bf16 dL/dx in fp32; the
+    # accumulating pre backward adds them in fp32 and rounds the sum), the
+    # unfused chain twice (dL/dx to bf16, then autograd's bf16 add); h_res /
+    # h_post gradients are D-long sums over that gradient, so they get an
+    # absolute tolerance of 1% of their largest entry.
     for ta, tb, name in zip(a, b, ("x", "h_res", "h_out", "h_post", "phi", "alpha", "base")):
         w = _np(tb.grad)
         atol = (1e-2 if name in ("h_res", "h_post") else 2e-3) * np.abs(w).max()
