@@ -144,6 +144,24 @@ __device__ __forceinline__ void st16nt(void* p, const u32x4& v) {
 }
 
 // ---------------------------------------------------------------------------
+// XCD-contiguous work order.  Workgroups are dispatched round robin over the
+// eight XCDs (workgroup b runs on XCD b % 8); xcd_contig maps b to an item so
+// that each XCD walks one contiguous eighth of the nb items in order (XCD x
+// gets items [x * q + min(x, r), ..) with q = nb / 8, r = nb % 8; a bijection
+// on [0, nb)).  Token-streaming kernels read each XCD's rows as long runs
+// this way instead of interleaving all eight XCDs over every stretch of
+// memory (on the MI355X: post forward at c5 1446 -> 1360 us, the N = 8 wave-
+// per-token post backward at config 4 670-730 -> 602-617 us; the post
+// backward's block kernel, the pre forward's y pass and the pre backward's
+// kernel A measured equal or slower and keep the plain order).
+// ---------------------------------------------------------------------------
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_contig(int64_t b, int64_t nb) {
+  const int64_t q = nb / kXcds, r = nb % kXcds, x = b % kXcds;
+  return x * q + (x < r ? x : r) + b / kXcds;
+}
+
+// ---------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
     int64_t T, int D, const S* __restrict__ gy2) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t t = (int64_t)blockIdx.x * kPostWavesPerBlock + wave;
+  const int64_t t = xcd_contig(blockIdx.x, gridDim.x) * kPostWavesPerBlock + wave;
   if (t >= T) return;
 
   float hr[N * N], hp[N];
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kWave * kPostFwdBlockWaves) void post_fwd_block_ker
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x / kWave;
-  const int64_t t = blockIdx.x;
+  const int64_t t = xcd_contig(blockIdx.x, gridDim.x);
   float hr[N * N], hp[N];
 #pragma unroll
   for (int i = 0; i < N * N; ++i) hr[i] = h_res[t * (N * N) + i];
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x / kWave;
-  const int64_t t = blockIdx.x;
+  const int64_t t = blockIdx.x;  // (XCD-contiguous order measured 2.5% slower here at c5)
   float hr[N * N], hp[N];
 #pragma unroll
   for (int i = 0; i < N * N; ++i) hr[i] = h_res[t * (N * N) + i];
