@@ -150,10 +150,12 @@ __device__ __forceinline__ void st16nt(void* p, const u32x4& v) {
 // gets items [x * q + min(x, r), ..) with q = nb / 8, r = nb % 8; a bijection
 // on [0, nb)).  Token-streaming kernels read each XCD's rows as long runs
 // this way instead of interleaving all eight XCDs over every stretch of
-// memory (on the MI355X: post forward at c5 1446 -> 1360 us, the N = 8 wave-
-// per-token post backward at config 4 670-730 -> 602-617 us; the post
-// backward's block kernel, the pre forward's y pass and the pre backward's
-// kernel A measured equal or slower and keep the plain order).
+// memory.  Which kernels gain is measured, not predictable: on the MI355X
+// the N = 4 post forward (c5 1446 -> 1360 us) and the N = 8 wave-per-token
+// post backward (config 4 670-730 -> 602-617 us) do; the N = 8 post forward,
+// the post backward's block kernel, the persistent LDS-pipelined post
+// kernels, the pre forward's y pass and the pre backward's kernel A measured
+// equal or slower and keep the plain order.
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;
 __device__ __forceinline__ int64_t xcd_contig(int64_t b, int64_t nb) {

@@ -228,7 +228,9 @@ __global__ __launch_bounds__(kWave * kPostFwdBlockWaves) void post_fwd_block_ker
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x / kWave;
-  const int64_t t = xcd_contig(blockIdx.x, gridDim.x);
+  // XCD-contiguous order at N = 4 (c5: 1447 -> 1360 us); N = 8 rows (D =
+  // 2048, config 4) measured faster in the plain order (380 against 397 us)
+  const int64_t t = N == 4 ? xcd_contig(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
   float hr[N * N], hp[N];
 #pragma unroll
   for (int i = 0; i < N * N; ++i) hr[i] = h_res[t * (N * N) + i];
