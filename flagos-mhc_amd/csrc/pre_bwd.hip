@@ -815,6 +815,14 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
 // per column block (blockIdx.x = cb * NG + group), which keeps the phi^T
 // operands (VC x MK x P registers) and grad_phi accumulators (MT x VC) of a
 // wave within one wave per SIMD.
+// With H = 2 (N = 8, one phi plane, no grad_x_in) a stream has two waves,
+// one per 64-column half of the block's columns: lane (r, q) of half h
+// computes the 4 columns 64h + 4r.. of its tokens (8-byte LDS reads of the
+// 16-byte units, which the loads still fill 8 columns a lane), so the
+// accumulators and phi^T operands halve (80 + 48 registers) and two waves
+// share each SIMD: one wave's LDS, MFMA and barrier waits overlap the
+// other's work.  Each wave issues 2 of its stream's 4 x loads and 2 of the
+// shared units, 4 loads a tile like every wave of the H = 1 form.
 template <int N> struct DmaCfg {
   using PD = PreDims<N>;
   static constexpr int G = 4, NG = N / G;
@@ -856,21 +864,139 @@ struct PreBwdDmaArgs {
   int64_t ntiles;
 };
 
-template <int N, int P, int S, bool ACC>
-__global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
+// A tile's ring reads, all issued before one wait: with one wave per SIMD the
+// LDS latency is then paid once a tile instead of once per group of four
+// reads (the groups used to wait in turn).
+//   xr[e]    = unit X + 4w + e      (xa: the lane's address of unit X + 4w)
+//   gr[e]    = unit GY + e          (la: the lane's address of unit 0)
+//   ag[i][e] = unit GA + 4i + e
+//   cf[e]    = 16 bytes at cfa + 64e
+// The unit offsets are literals: GY = 16, GA = 20 and G = 4 for N = 4 and 8.
+template <int RQ>
+__device__ __forceinline__ void dma_tile_reads(u32x4 (&xr)[4], u32x4 (&gr)[4], u32x4 (&ag)[RQ][4],
+                                               u32x4 (&cf)[4], uint32_t xa, uint32_t la, uint32_t cfa) {
+  static_assert(DmaCfg<4>::X == 0 && DmaCfg<4>::GY == 16 && DmaCfg<4>::GA == 20 && DmaCfg<4>::G == 4 &&
+                    DmaCfg<8>::X == 0 && DmaCfg<8>::GY == 16 && DmaCfg<8>::GA == 20 && DmaCfg<8>::G == 4,
+                "unit offsets written into the reads below");
+  static_assert(RQ == 1 || RQ == 3, "read groups of N = 4 / N = 8");
+  if constexpr (RQ == 1) {
+    asm volatile(
+        "ds_read_b128 %0, %16\n\t"
+        "ds_read_b128 %1, %16 offset:1024\n\t"
+        "ds_read_b128 %2, %16 offset:2048\n\t"
+        "ds_read_b128 %3, %16 offset:3072\n\t"
+        "ds_read_b128 %4, %17 offset:16384\n\t"
+        "ds_read_b128 %5, %17 offset:17408\n\t"
+        "ds_read_b128 %6, %17 offset:18432\n\t"
+        "ds_read_b128 %7, %17 offset:19456\n\t"
+        "ds_read_b128 %8, %17 offset:20480\n\t"
+        "ds_read_b128 %9, %17 offset:21504\n\t"
+        "ds_read_b128 %10, %17 offset:22528\n\t"
+        "ds_read_b128 %11, %17 offset:23552\n\t"
+        "ds_read_b128 %12, %18\n\t"
+        "ds_read_b128 %13, %18 offset:64\n\t"
+        "ds_read_b128 %14, %18 offset:128\n\t"
+        "ds_read_b128 %15, %18 offset:192\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xr[0]), "=&v"(xr[1]), "=&v"(xr[2]), "=&v"(xr[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
+          "=&v"(gr[3]), "=&v"(ag[0][0]), "=&v"(ag[0][1]), "=&v"(ag[0][2]), "=&v"(ag[0][3]), "=&v"(cf[0]),
+          "=&v"(cf[1]), "=&v"(cf[2]), "=&v"(cf[3])
+        : "v"(xa), "v"(la), "v"(cfa)
+        : "memory");
+  } else {
+    asm volatile(
+        "ds_read_b128 %0, %24\n\t"
+        "ds_read_b128 %1, %24 offset:1024\n\t"
+        "ds_read_b128 %2, %24 offset:2048\n\t"
+        "ds_read_b128 %3, %24 offset:3072\n\t"
+        "ds_read_b128 %4, %25 offset:16384\n\t"
+        "ds_read_b128 %5, %25 offset:17408\n\t"
+        "ds_read_b128 %6, %25 offset:18432\n\t"
+        "ds_read_b128 %7, %25 offset:19456\n\t"
+        "ds_read_b128 %8, %25 offset:20480\n\t"
+        "ds_read_b128 %9, %25 offset:21504\n\t"
+        "ds_read_b128 %10, %25 offset:22528\n\t"
+        "ds_read_b128 %11, %25 offset:23552\n\t"
+        "ds_read_b128 %12, %25 offset:24576\n\t"
+        "ds_read_b128 %13, %25 offset:25600\n\t"
+        "ds_read_b128 %14, %25 offset:26624\n\t"
+        "ds_read_b128 %15, %25 offset:27648\n\t"
+        "ds_read_b128 %16, %25 offset:28672\n\t"
+        "ds_read_b128 %17, %25 offset:29696\n\t"
+        "ds_read_b128 %18, %25 offset:30720\n\t"
+        "ds_read_b128 %19, %25 offset:31744\n\t"
+        "ds_read_b128 %20, %26\n\t"
+        "ds_read_b128 %21, %26 offset:64\n\t"
+        "ds_read_b128 %22, %26 offset:128\n\t"
+        "ds_read_b128 %23, %26 offset:192\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xr[0]), "=&v"(xr[1]), "=&v"(xr[2]), "=&v"(xr[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
+          "=&v"(gr[3]), "=&v"(ag[0][0]), "=&v"(ag[0][1]), "=&v"(ag[0][2]), "=&v"(ag[0][3]), "=&v"(ag[1][0]),
+          "=&v"(ag[1][1]), "=&v"(ag[1][2]), "=&v"(ag[1][3]), "=&v"(ag[2][0]), "=&v"(ag[2][1]), "=&v"(ag[2][2]),
+          "=&v"(ag[2][3]), "=&v"(cf[0]), "=&v"(cf[1]), "=&v"(cf[2]), "=&v"(cf[3])
+        : "v"(xa), "v"(la), "v"(cfa)
+        : "memory");
+  }
+}
+
+// The same reads for H = 2: xr / gr are the 8 bytes of the lane's 4 columns
+// (xa, lx: their addresses in unit X + 4w and unit 0), ag / cf as above (la).
+__device__ __forceinline__ void dma_tile_reads_h2(u32x2 (&xr)[4], u32x2 (&gr)[4], u32x4 (&ag)[3][4],
+                                                  u32x4 (&cf)[4], uint32_t xa, uint32_t lx, uint32_t la,
+                                                  uint32_t cfa) {
+  asm volatile(
+      "ds_read_b64 %0, %24\n\t"
+      "ds_read_b64 %1, %24 offset:1024\n\t"
+      "ds_read_b64 %2, %24 offset:2048\n\t"
+      "ds_read_b64 %3, %24 offset:3072\n\t"
+      "ds_read_b64 %4, %25 offset:16384\n\t"
+      "ds_read_b64 %5, %25 offset:17408\n\t"
+      "ds_read_b64 %6, %25 offset:18432\n\t"
+      "ds_read_b64 %7, %25 offset:19456\n\t"
+      "ds_read_b128 %8, %26 offset:20480\n\t"
+      "ds_read_b128 %9, %26 offset:21504\n\t"
+      "ds_read_b128 %10, %26 offset:22528\n\t"
+      "ds_read_b128 %11, %26 offset:23552\n\t"
+      "ds_read_b128 %12, %26 offset:24576\n\t"
+      "ds_read_b128 %13, %26 offset:25600\n\t"
+      "ds_read_b128 %14, %26 offset:26624\n\t"
+      "ds_read_b128 %15, %26 offset:27648\n\t"
+      "ds_read_b128 %16, %26 offset:28672\n\t"
+      "ds_read_b128 %17, %26 offset:29696\n\t"
+      "ds_read_b128 %18, %26 offset:30720\n\t"
+      "ds_read_b128 %19, %26 offset:31744\n\t"
+      "ds_read_b128 %20, %27\n\t"
+      "ds_read_b128 %21, %27 offset:64\n\t"
+      "ds_read_b128 %22, %27 offset:128\n\t"
+      "ds_read_b128 %23, %27 offset:192\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(xr[0]), "=&v"(xr[1]), "=&v"(xr[2]), "=&v"(xr[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
+        "=&v"(gr[3]), "=&v"(ag[0][0]), "=&v"(ag[0][1]), "=&v"(ag[0][2]), "=&v"(ag[0][3]), "=&v"(ag[1][0]),
+        "=&v"(ag[1][1]), "=&v"(ag[1][2]), "=&v"(ag[1][3]), "=&v"(ag[2][0]), "=&v"(ag[2][1]), "=&v"(ag[2][2]),
+        "=&v"(ag[2][3]), "=&v"(cf[0]), "=&v"(cf[1]), "=&v"(cf[2]), "=&v"(cf[3])
+      : "v"(xa), "v"(lx), "v"(la), "v"(cfa)
+      : "memory");
+}
+
+template <int N, int P, int S, bool ACC, int H = 1>
+__global__ __launch_bounds__(64 * DmaCfg<N>::G * H) void pre_bwd_dma_kernel(PreBwdDmaArgs a) {
   using C = DmaCfg<N>;
   using PD = PreDims<N>;
   constexpr int M = PD::M, MT = PD::MT, MK = PD::MK, MP32 = PD::MP32;
-  constexpr int VC = C::VC, VD = C::VD, DW = C::DW, TT = C::TT;
+  constexpr int VC = C::VC / H, VD = C::VD / H, DW = C::DW, TT = C::TT;
   constexpr int UNITS = ACC ? C::UNITS_ACC : C::UNITS;
-  constexpr int LMIN = C::LMIN + (ACC ? 4 : 0);             // grad_x_in: 4 more loads a wave
+  static_assert(H == 1 || (H == 2 && N == 8 && P == 1 && !ACC && C::SHARED % (C::G * H) == 0),
+                "column halves: N = 8, one phi plane, no grad_x_in, shared units split evenly");
+  constexpr int XL = 4 / H;                                  // x loads of a wave per tile
+  constexpr int LMIN = XL + C::SHARED / (C::G * H) + (ACC ? 4 : 0);  // grad_x_in: 4 more loads a wave
   constexpr int VM_START = (S - 2) * LMIN;                  // before any grad_x store
   constexpr int VM_STEADY = (S - 2) * LMIN + (S - 1) * 4;
   static_assert(S >= 2 && VM_STEADY < 64, "pipeline shape");
   __shared__ u32x4 ring[S * UNITS * kWave];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave: stream of the group
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = wid % C::G, h = wid / C::G;  // stream of the group, column half
   const int grp = (int)(blockIdx.x % C::NG), cb = (int)(blockIdx.x / C::NG);
   const int n = grp * C::G + w;
   const int r = lane & 15, q = lane >> 4;
@@ -879,8 +1005,10 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
   const int64_t tstep = gridDim.y;
   const int64_t cnt = (ntiles - blockIdx.y + tstep - 1) / tstep;
   if (cnt <= 0) return;  // uniform over the block
-  const int dl = cb * DW + VC * r;  // first column of this lane
+  const int dl = cb * DW + (DW / H) * h + VC * r;  // first column this lane computes
   const bool colok = dl < D;
+  const int dld = cb * DW + 8 * r;  // first column this lane's 16-byte loads move
+  const bool ldok = dld < D;
 
   int64_t itile = blockIdx.y;  // next tile to load
   auto issue = [&](int64_t j) {
@@ -890,8 +1018,8 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
     u32x4* st = ring + (int)(j % S) * UNITS * kWave;
     const auto rx = rows_rsrc(a.x + tb * K, (int64_t)nv * K * 2);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
+    for (int e = XL * h; e < XL * h + XL; ++e) {
+      const uint32_t off = ldok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dld) * 2) : kBufferOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(st + (C::X + 4 * w + e) * kWave), 16,
                                                off, 0, 0, 2 /* nt */);
     }
@@ -899,18 +1027,18 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
       const auto ri = rows_rsrc(a.gin + tb * K, (int64_t)nv * K * 2);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
+        const uint32_t off = ldok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dld) * 2) : kBufferOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ri, (lds_void_t*)(st + (C::GI + 4 * w + e) * kWave), 16,
                                                  off, 0, 0, 2 /* nt */);
       }
     }
-    for (int u = w; u < C::SHARED; u += C::G) {
+    for (int u = wid; u < C::SHARED; u += C::G * H) {
       const int unit = C::GY + u;
       lds_void_t* dst = (lds_void_t*)(st + unit * kWave);
       if (unit < C::GA) {
         const int e = unit - C::GY;
         const auto rg = rows_rsrc(a.gy + tb * D, (int64_t)nv * D * 2);
-        const uint32_t off = colok ? (uint32_t)(((4 * q + e) * (int64_t)D + dl) * 2) : kBufferOob;
+        const uint32_t off = ldok ? (uint32_t)(((4 * q + e) * (int64_t)D + dld) * 2) : kBufferOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, dst, 16, off, 0, 0, 2);
       } else if (unit < C::GT) {
         const int mk = (unit - C::GA) >> 1, g = (unit - C::GA) & 1;
@@ -977,13 +1105,45 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
 
     const uint32_t sbase = ring_lds + (uint32_t)((j % S) * UNITS * kWave * 16);
     const uint32_t la = sbase + lane * 16;
-    u32x4 xr[4], gr[4], gA[MK][2], gt[MT], cfu[4];
-    lds_read4<1024>(xr, la + (C::X + 4 * w) * 1024);  // x rows of stream n, tokens 4q+e
-    lds_read4<1024>(gr, la + C::GY * 1024);           // grad_y rows
+    uint32_t xr[4][VD], gr[4][VD];  // the lane's columns of x (stream n) and grad_y, tokens 4q+e
+    u32x4 gA[MK][2], gt[MT], cfu[4];
     {
-      u32x4 ag[C::RA / 4][4];  // units GA.. four at a time: grad_mixes hi, lo per mk, then g^T blocks
+      // x rows of stream n and grad_y rows (tokens 4q+e); units GA.. four at
+      // a time: grad_mixes hi, lo per mk, then the g^T blocks; coefficients
+      // of tokens 4q+e, stream n
+      u32x4 ag[C::RA / 4][4];
+      const uint32_t xa = la + (C::X + 4 * w) * 1024, cfa = sbase + C::CF * 1024 + (4 * q * C::G + w) * 16;
+      if constexpr (H == 2) {
+        // byte 8 * r + 128 * h of the q-th 256 bytes holds columns 64h + 4r..
+        const uint32_t lx = sbase + 256 * q + 128 * h + 8 * r;
+        u32x2 x2[4], g2[4];
+        dma_tile_reads_h2(x2, g2, ag, cfu, lx + (C::X + 4 * w) * 1024, lx, la, cfa);
 #pragma unroll
-      for (int i = 0; i < C::RA / 4; ++i) lds_read4<1024>(ag[i], la + (C::GA + 4 * i) * 1024);
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int v = 0; v < VD; ++v) {
+            xr[e][v] = x2[e][v];
+            gr[e][v] = g2[e][v];
+          }
+      } else {
+        u32x4 x4[4], g4[4];
+        if constexpr (N == 8 && P == 2) {  // the single-wait form spills with two phi planes at N = 8
+          lds_read4<1024>(x4, xa);
+          lds_read4<1024>(g4, la + C::GY * 1024);
+#pragma unroll
+          for (int i = 0; i < C::RA / 4; ++i) lds_read4<1024>(ag[i], la + (C::GA + 4 * i) * 1024);
+          lds_read4<C::G * 16>(cfu, cfa);
+        } else {
+          dma_tile_reads<C::RA / 4>(x4, g4, ag, cfu, xa, la, cfa);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int v = 0; v < VD; ++v) {
+            xr[e][v] = x4[e][v];
+            gr[e][v] = g4[e][v];
+          }
+      }
 #pragma unroll
       for (int mk = 0; mk < MK; ++mk) {
         gA[mk][0] = ag[(2 * mk) / 4][(2 * mk) % 4];
@@ -992,7 +1152,6 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) gt[mt] = ag[(2 * MK + mt) / 4][(2 * MK + mt) % 4];
     }
-    lds_read4<C::G * 16>(cfu, sbase + C::CF * 1024 + (4 * q * C::G + w) * 16);  // tokens 4q+e, stream n
     u32x4 gi[4];
     if constexpr (ACC) lds_read4<1024>(gi, la + (C::GI + 4 * w) * 1024);  // grad_x_in rows, tokens 4q+e
 
@@ -1032,7 +1191,7 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
       // pre[t,n], inv[t], scale[t]
       const float fx = __uint_as_float(cfu[e][0]), fy = __uint_as_float(cfu[e][1]),
                   fz = __uint_as_float(cfu[e][2]);
-      u32x4 o;
+      uint32_t o[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
       for (int w = 0; w < VD; ++w) {
         const uint32_t xw = xr[e][w], gw = gr[e][w];
@@ -1049,7 +1208,10 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
       // rows >= nv fall outside the range and are dropped, as are columns >= D;
       // streaming (nt) stores measured 6% faster for this kernel than default ones
       const uint32_t off = colok ? (uint32_t)((((4 * q + e) * N + n) * (int64_t)D + dl) * 2) : kBufferOob;
-      __builtin_amdgcn_raw_buffer_store_b128(o, rgx, off, 0, 2 /* nt */);
+      if constexpr (H == 2)
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{o[0], o[1]}, rgx, off, 0, 2 /* nt */);
+      else
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{o[0], o[1], o[2], o[3]}, rgx, off, 0, 2 /* nt */);
     }
   }
 
@@ -1062,8 +1224,9 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G) void pre_bwd_dma_kernel(PreBwdDm
       const int m = 16 * mt + 4 * q + v;
       if (m >= M) continue;
       float4* dst = reinterpret_cast<float4*>(part + (int64_t)m * K);
-      dst[0] = float4{ph[mt][0][v], ph[mt][1][v], ph[mt][2][v], ph[mt][3][v]};
-      dst[1] = float4{ph[mt][4][v], ph[mt][5][v], ph[mt][6][v], ph[mt][7][v]};
+#pragma unroll
+      for (int c4 = 0; c4 < VC / 4; ++c4)
+        dst[c4] = float4{ph[mt][4 * c4][v], ph[mt][4 * c4 + 1][v], ph[mt][4 * c4 + 2][v], ph[mt][4 * c4 + 3][v]};
     }
 }
 
@@ -1592,6 +1755,9 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* ns
   const dim3 grid((unsigned)(ncb * NG), (unsigned)ns), block(64 * DmaCfg<N>::G);
   if (sta.gin)
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), grid, block, 0, st, da);
+  else if constexpr (N == 8 && P == 1)  // two waves per stream (column halves)
+    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, DmaCfg<N>::STAGES, false, 2>), grid, dim3(2 * block.x), 0, st,
+                       da);
   else
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, DmaCfg<N>::STAGES, false>), grid, block, 0, st, da);
   *nsplit = (int)ns;

@@ -449,46 +449,63 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
     uint32_t sw[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) sw[g] = ((4 * g + q) ^ r) << 4;
-    asm volatile(
-        "ds_read_b128 %0, %12\n\t"
-        "ds_read_b128 %1, %13\n\t"
-        "ds_read_b128 %2, %14\n\t"
-        "ds_read_b128 %3, %15\n\t"
-        "ds_read_b128 %4, %16\n\t"
-        "ds_read_b128 %5, %17\n\t"
-        "ds_read_b128 %6, %18\n\t"
-        "ds_read_b128 %7, %19\n\t"
-        "ds_read_b128 %8, %16 offset:4096\n\t"
-        "ds_read_b128 %9, %17 offset:4096\n\t"
-        "ds_read_b128 %10, %18 offset:4096\n\t"
-        "ds_read_b128 %11, %19 offset:4096\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0][0]), "=&v"(B[0][1]),
-          "=&v"(B[0][2]), "=&v"(B[0][3]), "=&v"(B[1][0]), "=&v"(B[1][1]), "=&v"(B[1][2]), "=&v"(B[1][3])
-        : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
-          "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
-        : "memory");
-    if constexpr (MT == 5) {  // N = 8: phi rows 32..79
+    if constexpr (MT == 2) {
       asm volatile(
-          "ds_read_b128 %0, %12 offset:8192\n\t"
-          "ds_read_b128 %1, %13 offset:8192\n\t"
-          "ds_read_b128 %2, %14 offset:8192\n\t"
-          "ds_read_b128 %3, %15 offset:8192\n\t"
-          "ds_read_b128 %4, %12 offset:12288\n\t"
-          "ds_read_b128 %5, %13 offset:12288\n\t"
-          "ds_read_b128 %6, %14 offset:12288\n\t"
-          "ds_read_b128 %7, %15 offset:12288\n\t"
-          "ds_read_b128 %8, %12 offset:16384\n\t"
-          "ds_read_b128 %9, %13 offset:16384\n\t"
-          "ds_read_b128 %10, %14 offset:16384\n\t"
-          "ds_read_b128 %11, %15 offset:16384\n\t"
+          "ds_read_b128 %0, %12\n\t"
+          "ds_read_b128 %1, %13\n\t"
+          "ds_read_b128 %2, %14\n\t"
+          "ds_read_b128 %3, %15\n\t"
+          "ds_read_b128 %4, %16\n\t"
+          "ds_read_b128 %5, %17\n\t"
+          "ds_read_b128 %6, %18\n\t"
+          "ds_read_b128 %7, %19\n\t"
+          "ds_read_b128 %8, %16 offset:4096\n\t"
+          "ds_read_b128 %9, %17 offset:4096\n\t"
+          "ds_read_b128 %10, %18 offset:4096\n\t"
+          "ds_read_b128 %11, %19 offset:4096\n\t"
           "s_waitcnt lgkmcnt(0)"
-          : "=&v"(B[2][0]), "=&v"(B[2][1]), "=&v"(B[2][2]), "=&v"(B[2][3]), "=&v"(B[3][0]), "=&v"(B[3][1]),
-            "=&v"(B[3][2]), "=&v"(B[3][3]), "=&v"(B[4][0]), "=&v"(B[4][1]), "=&v"(B[4][2]), "=&v"(B[4][3])
-          : "v"(cb0 + sw[0]), "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
+          : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0][0]), "=&v"(B[0][1]),
+            "=&v"(B[0][2]), "=&v"(B[0][3]), "=&v"(B[1][0]), "=&v"(B[1][1]), "=&v"(B[1][2]), "=&v"(B[1][3])
+          : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
+            "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
           : "memory");
     } else {
-      static_assert(MT == 2, "phi row blocks read above");
+      // N = 8: phi rows 32..79 as well, all 24 reads before one wait (one
+      // wave per SIMD: the LDS latency is paid once a stage)
+      static_assert(MT == 5, "phi row blocks read here");
+      asm volatile(
+          "ds_read_b128 %0, %24\n\t"
+          "ds_read_b128 %1, %25\n\t"
+          "ds_read_b128 %2, %26\n\t"
+          "ds_read_b128 %3, %27\n\t"
+          "ds_read_b128 %4, %28\n\t"
+          "ds_read_b128 %5, %29\n\t"
+          "ds_read_b128 %6, %30\n\t"
+          "ds_read_b128 %7, %31\n\t"
+          "ds_read_b128 %8, %28 offset:4096\n\t"
+          "ds_read_b128 %9, %29 offset:4096\n\t"
+          "ds_read_b128 %10, %30 offset:4096\n\t"
+          "ds_read_b128 %11, %31 offset:4096\n\t"
+          "ds_read_b128 %12, %28 offset:8192\n\t"
+          "ds_read_b128 %13, %29 offset:8192\n\t"
+          "ds_read_b128 %14, %30 offset:8192\n\t"
+          "ds_read_b128 %15, %31 offset:8192\n\t"
+          "ds_read_b128 %16, %28 offset:12288\n\t"
+          "ds_read_b128 %17, %29 offset:12288\n\t"
+          "ds_read_b128 %18, %30 offset:12288\n\t"
+          "ds_read_b128 %19, %31 offset:12288\n\t"
+          "ds_read_b128 %20, %28 offset:16384\n\t"
+          "ds_read_b128 %21, %29 offset:16384\n\t"
+          "ds_read_b128 %22, %30 offset:16384\n\t"
+          "ds_read_b128 %23, %31 offset:16384\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(A[0]), "=&v"(A[1]), "=&v"(A[2]), "=&v"(A[3]), "=&v"(B[0][0]), "=&v"(B[0][1]),
+            "=&v"(B[0][2]), "=&v"(B[0][3]), "=&v"(B[1][0]), "=&v"(B[1][1]), "=&v"(B[1][2]), "=&v"(B[1][3]),
+            "=&v"(B[2][0]), "=&v"(B[2][1]), "=&v"(B[2][2]), "=&v"(B[2][3]), "=&v"(B[3][0]), "=&v"(B[3][1]),
+            "=&v"(B[3][2]), "=&v"(B[3][3]), "=&v"(B[4][0]), "=&v"(B[4][1]), "=&v"(B[4][2]), "=&v"(B[4][3])
+          : "v"(ca + sw[0]), "v"(ca + sw[1]), "v"(ca + sw[2]), "v"(ca + sw[3]), "v"(cb0 + sw[0]),
+            "v"(cb0 + sw[1]), "v"(cb0 + sw[2]), "v"(cb0 + sw[3])
+          : "memory");
     }
     // The stage's 128 columns go through a fresh 4-step MFMA chain that is
     // then added to the running sums with round-to-nearest-even adds: a

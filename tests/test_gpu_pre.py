@@ -180,6 +180,9 @@ BWD_CASES = [
     (4, 8, 100, torch.float32, torch.float32, "baseline", 10.0, 20),
     (5, 4, 4100, torch.float16, torch.float16, "baseline", 10.0, 20),
     (70001, 8, 64, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    # N = 8 grad_x kernel with two waves per stream (64-column halves): a
+    # last column block whose second half is partly past D, a ragged last tile
+    (1000, 8, 1000, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
 ]
 
 
