@@ -612,6 +612,243 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_dma_kernel(PreFwdArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// N = 8 persistent contraction with the K steps split over waves.
+//
+// A tile of TT tokens streams through a ring of S slots in LDS, one slot per
+// stage of CW columns of K: x[TT][CW] and phi[80][CW], filled by direct-to-LDS
+// loads S - 1 stages ahead, one block of 8 waves (two per SIMD) per CU.  Wave
+// (g, kq) takes 32 tokens (two 16-row blocks) and k-step kq (32 columns) of
+// every stage against all 80 phi rows: it reads 7 KB of a slot (the 4-wave
+// kernel read all of phi for each of 4 row blocks, 24 KB a wave), and one
+// wave's waits overlap the other's MFMA and VALU work.  A 1 KB unit holds
+// 1024 / (2 CW) rows; row R keeps its chunk c (8 columns) at position
+// c ^ f(R), f(R) = R & 15 for CW = 128 and (R >> 1) & 7 for CW = 64, so the
+// 16 rows of an MFMA operand read hit 16 different 16-byte bank groups.
+// Each wave runs a fresh 4-step MFMA chain over 4 stages that is then added
+// to its running sums (one chain over all of K drifts); at a tile's last
+// stage the k-step waves hand their sums to the kq = 0 waves in a fixed
+// order through the just-read slot, and those write the tile's sums to the
+// workspace for the finalize kernel (heads, Sinkhorn).
+//   TT = 64, CW = 128 (S = 4, 36 KB slots): 48 KB of x in flight per CU.
+//   TT = 128, CW = 64 (S = 5, 26 KB slots): 64 KB of x in flight and half
+//   the phi bytes per x byte; used when every CU gets a 128-token tile.
+// ---------------------------------------------------------------------------
+constexpr int kKsWaves = 8;
+constexpr int kKsThreads = kKsWaves * kWave;
+
+template <int TT, int CW> struct KsCfg {
+  static constexpr int M = PreDims<8>::M, MT = PreDims<8>::MT;
+  static constexpr int RB = TT / 16, KS = CW / 32;           // row blocks, k-steps per stage
+  static constexpr int NG = kKsWaves / KS;                   // row-block pairs
+  static constexpr int CPR = CW / 8;                         // 16-byte chunks per row
+  static constexpr int RPU = 1024 / (2 * CW);                // rows per 1 KB unit
+  static constexpr int XU = TT / RPU, PU = M / RPU;          // x and phi units of a slot
+  static constexpr int UNITS = XU + PU;
+  static constexpr int S = CW == 128 ? 4 : 5;  // 6 slots of 26 KB measured no faster than 5
+  static_assert(RB == 2 * NG && M % RPU == 0 && XU % kKsWaves == 0, "two row blocks a wave, whole units");
+  static_assert(S * UNITS <= 144, "ring within the LDS");
+  __device__ static constexpr int swz(int row) { return CW == 128 ? (row & 15) : ((row >> 1) & 7); }
+};
+
+template <int TT, int CW>
+__global__ __launch_bounds__(kKsThreads) void pre_fwd_ks8_kernel(PreFwdArgs a) {
+  constexpr int N = 8;
+  using C = KsCfg<TT, CW>;
+  constexpr int M = C::M, MT = C::MT, S = C::S, UNITS = C::UNITS, KS = C::KS;
+  constexpr int CIMAX = (UNITS + kKsWaves - 1) / kKsWaves;
+  constexpr int CIMIN = UNITS / kKsWaves;
+  constexpr int XI = C::XU / kKsWaves;  // the first XI loads of a wave are x units
+  // Stage j's loads have landed once at most VM_C newer vector memory
+  // operations are outstanding: the loads of the S - 2 stages issued after it
+  // (at least CIMIN a wave each); the tile sums' stores only add newer ones.
+  constexpr int VM_C = (S - 2) * CIMIN;
+  static_assert(VM_C < 64 && MT == 5, "vmcnt range; five phi row blocks read below");
+  static_assert(2 * 2 * MT * kWave * 16 + 2 * 2 * 16 * 4 <= UNITS * 1024, "hand-over of two waves fits a slot");
+  __shared__ u32x4 ring[S * UNITS * kWave];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = wv % KS, g = wv / KS;
+  const int r = lane & 15, q = lane >> 4;
+  const int D = a.D;
+  const int K = N * D;
+  const int64_t T = a.T;
+  const int nst_c = (K + CW - 1) / CW;
+  const int64_t ntiles = (T + TT - 1) / TT;
+  const int64_t my_tiles = (ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x;
+  if (my_tiles <= 0) return;  // uniform over the block
+  const int64_t J = my_tiles * nst_c;
+  const bf16_t* __restrict__ x = static_cast<const bf16_t*>(a.x);
+  const auto rphi = rows_rsrc(a.phi, (int64_t)M * K * 2);
+  const int nci = wv < UNITS - CIMIN * kKsWaves ? CIMAX : CIMIN;
+
+  // ---- loads of stage j: unit u = wv + 8i (x units first, then phi);
+  // DMA lane L: row RPU * unit + L / CPR, position L % CPR
+  const int lrow = lane / C::CPR, lpos = lane % C::CPR;
+  int64_t itile = blockIdx.x;
+  int is = 0;
+  auto issue = [&](int64_t j) {
+    const int64_t tb = itile * TT;
+    const int nv = (int)(T - tb < TT ? T - tb : TT);
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * UNITS * 1024);
+    const auto rx = rows_rsrc(x + tb * K, (int64_t)nv * K * 2);
+    const int k0 = is * CW;
+#pragma unroll
+    for (int i = 0; i < CIMAX; ++i) {
+      if (i < nci) {
+        const int u = wv + kKsWaves * i;
+        const int row = C::RPU * (i < XI ? u : u - C::XU) + lrow;
+        const int k = k0 + 8 * (lpos ^ C::swz(row));
+        const uint32_t off = k < K ? (uint32_t)(((int64_t)row * K + k) * 2) : kBufferOob;
+        lds_void_t* dst = (lds_void_t*)(uintptr_t)(slot + u * 1024);
+        if (i < XI)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 2 /* nt */);
+        else
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rphi, dst, 16, off, 0, 0, 0);
+      }
+    }
+    if (++is == nst_c) {
+      is = 0;
+      itile += gridDim.x;
+    }
+  };
+
+  for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
+
+  floatx4 acc[2][MT], part[2][MT];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[b][mt] = part[b][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float ssq[2] = {0.f, 0.f};
+  // chunk KS... : lane (r, q) reads chunk 4kq + q of rows with row & 15 = r
+  // (rows 32g + 16b + r of x, 16mt + r of phi: f depends on r only)
+  const uint32_t roff = (uint32_t)(r * 2 * CW + ((4 * kq + q) ^ C::swz(r)) * 16);
+  int64_t ctile = blockIdx.x;
+  int cs = 0;  // stage of the current tile
+  for (int64_t j = 0; j < J; ++j) {
+    if (j + S - 2 < J)
+      wait_vmcnt<VM_C>();
+    else
+      wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint32_t slot = lds_addr(ring) + (uint32_t)((j % S) * UNITS * 1024);
+    // the next loads go to the slot of stage j - 1, which every wave finished
+    // reading before the barrier
+    if (j + S - 1 < J) issue(j + S - 1);
+
+    // x rows 32g + r and 32g + 16 + r, phi rows 16mt + r: chunk 4kq + q
+    u32x4 A[2], B[MT];
+    asm volatile(
+        "ds_read_b128 %0, %7\n\t"
+        "ds_read_b128 %1, %7 offset:%9\n\t"
+        "ds_read_b128 %2, %8\n\t"
+        "ds_read_b128 %3, %8 offset:%9\n\t"
+        "ds_read_b128 %4, %8 offset:%10\n\t"
+        "ds_read_b128 %5, %8 offset:%11\n\t"
+        "ds_read_b128 %6, %8 offset:%12\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(A[0]), "=&v"(A[1]), "=&v"(B[0]), "=&v"(B[1]), "=&v"(B[2]), "=&v"(B[3]), "=&v"(B[4])
+        : "v"(slot + 32 * g * 2 * CW + roff), "v"(slot + C::XU * 1024 + roff), "i"(16 * 2 * CW),
+          "i"(32 * 2 * CW), "i"(48 * 2 * CW), "i"(64 * 2 * CW)
+        : "memory");
+    if ((cs & 3) == 0) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) part[b][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(A[b][i] << 16), hi = __uint_as_float(A[b][i] & 0xffff0000u);
+        ssq[b] = fmaf(lo, lo, fmaf(hi, hi, ssq[b]));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) part[b][mt] = mfma16x16x32(as_bf16x8(A[b]), as_bf16x8(B[mt]), part[b][mt]);
+    }
+    const bool last = cs == nst_c - 1;
+    if ((cs & 3) == 3 || last) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[b][mt] += part[b][mt];
+    }
+
+    if (last) {
+      // ---- the tile's sums: lane (r, q) of acc[b][mt] holds token
+      // 32g + 16b + 4q + v, m = 16mt + r; after the shuffles the lanes of row
+      // r hold this wave's sum(x^2) of token 32g + 16b + r.  The k-step
+      // waves kq = 1.. hand theirs to wave kq = 0 of their pair in turn, two
+      // waves a round, through this stage's slot: [pair slot][b][mt][lane]
+      // floatx4, then ssq [pair slot][b][r].
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        ssq[b] += __shfl_xor(ssq[b], 16, kWave);
+        ssq[b] += __shfl_xor(ssq[b], 32, kWave);
+      }
+      floatx4* xch = reinterpret_cast<floatx4*>(ring + (size_t)(j % S) * UNITS * kWave);
+      float* xss = reinterpret_cast<float*>(xch + 2 * 2 * MT * kWave);
+#pragma unroll 1
+      for (int k = 1; k < KS; ++k) {
+#pragma unroll 1
+        for (int g0 = 0; g0 < C::NG; g0 += 2) {
+          const bool mine = g >= g0 && g < g0 + 2;
+          const int ps = g - g0;  // pair slot of this round
+          __syncthreads();        // the slot's operands or the previous hand-over have been read
+          if (mine && kq == k) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) xch[((ps * 2 + b) * MT + mt) * kWave + lane] = acc[b][mt];
+              if (q == 0) xss[(ps * 2 + b) * 16 + r] = ssq[b];
+            }
+          }
+          __syncthreads();
+          if (mine && kq == 0) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) acc[b][mt] += xch[((ps * 2 + b) * MT + mt) * kWave + lane];
+              ssq[b] += xss[(ps * 2 + b) * 16 + r];
+            }
+          }
+        }
+      }
+      if (kq == 0) {
+        const int64_t tb = ctile * TT;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int64_t tok = tb + 32 * g + 16 * b + 4 * q + v;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              if (tok < T) a.part[tok * M + 16 * mt + r] = acc[b][mt][v];
+          }
+          const int64_t tok = tb + 32 * g + 16 * b + r;
+          if (q == 0 && tok < T) a.part_ssq[tok] = ssq[b];
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[b][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ssq[b] = 0.f;
+      }
+      __syncthreads();  // the hand-over has been read before the slot is loaded again
+    }
+    if (++cs == nst_c) {
+      cs = 0;
+      ctile += gridDim.x;
+    }
+  }
+}
+
 // ---- split-K form, kernels 2 and 3 -----------------------------------------
 // Kernel 2: one N x N lane group per token sums the splits' partials in split
 // order, then computes inv_rms, mixes, heads, clamp and Sinkhorn exactly as
@@ -886,7 +1123,15 @@ static int launch_pre_fwd_dma(PreFwdArgs a, void* workspace, size_t workspace_by
   const int64_t cus = device_cu_count();
   const int64_t slots = cus * FwdDmaCfg<N>::BLOCKS_PER_CU;  // resident blocks (LDS rings)
   const int64_t grid = ntiles < slots ? ntiles : slots;
-  hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
+  if constexpr (N == 8) {
+    // 128-token tiles once they fill every CU, else 64-token tiles
+    const int64_t nt128 = (a.T + 127) / 128;
+    if (nt128 >= cus)
+      hipLaunchKernelGGL((pre_fwd_ks8_kernel<128, 64>), dim3((unsigned)cus), dim3(kKsThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((pre_fwd_ks8_kernel<64, 128>), dim3((unsigned)grid), dim3(kKsThreads), 0, st, a);
+  } else
+    hipLaunchKernelGGL((pre_fwd_dma_kernel<N, false>), dim3((unsigned)grid), dim3(kFwdThreads), 0, st, a);
   int rc = check_launch("pre_fwd_dma");
   if (rc) return rc;
   if constexpr (FwdDmaCfg<N>::HEADS_APART) {

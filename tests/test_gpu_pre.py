@@ -93,6 +93,15 @@ FWD_CASES = [
     (100, 4, 520, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (20000, 4, 1288, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (70, 8, 200, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),       # N = 8, partial stages
+    # N = 8 persistent kernel with the K steps split over waves (more than 256
+    # tiles): a partial last stage that ends a short 4-stage MFMA chain, a
+    # ragged last tile, blocks with one and two tiles; one stage per tile
+    (20000, 8, 200, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (16500, 8, 8, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    # 128-token tiles of 64-column stages (a tile for every CU): ragged last
+    # tile, two tiles on the first blocks, one stage per tile
+    (33000, 8, 200, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (40000, 8, 8, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     # N=4 bf16 at the model widths D = 1024..8192: ragged last 64-token
     # tiles, fewer tiles than blocks, clamp off, few Sinkhorn iterations
     (1000, 4, 7168, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
