@@ -845,6 +845,11 @@ template <int N> struct DmaCfg {
 };
 
 constexpr int kDmaAccStages = 3;               // accumulating form: 3 x 41 KB (N = 4) / 48 KB (N = 8)
+// N = 4 runs the two-waves-per-stream form up to this many tokens: measured
+// on one MI355X (whole backward, D = 2048 / 4096 / 7168 at T = 4096..32768)
+// 5-12% faster, but at T = 65536 equal (D = 4096) or 4-6% slower (D = 5120,
+// 7168) than one wave per stream.
+constexpr int64_t kDmaHalvesMaxT4 = 32768;
 constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
 
 struct PreBwdDmaArgs {
@@ -941,41 +946,69 @@ __device__ __forceinline__ void dma_tile_reads(u32x4 (&xr)[4], u32x4 (&gr)[4], u
 
 // The same reads for H = 2: xr / gr are the 8 bytes of the lane's 4 columns
 // (xa, lx: their addresses in unit X + 4w and unit 0), ag / cf as above (la).
-__device__ __forceinline__ void dma_tile_reads_h2(u32x2 (&xr)[4], u32x2 (&gr)[4], u32x4 (&ag)[3][4],
+template <int RQ>
+__device__ __forceinline__ void dma_tile_reads_h2(u32x2 (&xr)[4], u32x2 (&gr)[4], u32x4 (&ag)[RQ][4],
                                                   u32x4 (&cf)[4], uint32_t xa, uint32_t lx, uint32_t la,
                                                   uint32_t cfa) {
-  asm volatile(
-      "ds_read_b64 %0, %24\n\t"
-      "ds_read_b64 %1, %24 offset:1024\n\t"
-      "ds_read_b64 %2, %24 offset:2048\n\t"
-      "ds_read_b64 %3, %24 offset:3072\n\t"
-      "ds_read_b64 %4, %25 offset:16384\n\t"
-      "ds_read_b64 %5, %25 offset:17408\n\t"
-      "ds_read_b64 %6, %25 offset:18432\n\t"
-      "ds_read_b64 %7, %25 offset:19456\n\t"
-      "ds_read_b128 %8, %26 offset:20480\n\t"
-      "ds_read_b128 %9, %26 offset:21504\n\t"
-      "ds_read_b128 %10, %26 offset:22528\n\t"
-      "ds_read_b128 %11, %26 offset:23552\n\t"
-      "ds_read_b128 %12, %26 offset:24576\n\t"
-      "ds_read_b128 %13, %26 offset:25600\n\t"
-      "ds_read_b128 %14, %26 offset:26624\n\t"
-      "ds_read_b128 %15, %26 offset:27648\n\t"
-      "ds_read_b128 %16, %26 offset:28672\n\t"
-      "ds_read_b128 %17, %26 offset:29696\n\t"
-      "ds_read_b128 %18, %26 offset:30720\n\t"
-      "ds_read_b128 %19, %26 offset:31744\n\t"
-      "ds_read_b128 %20, %27\n\t"
-      "ds_read_b128 %21, %27 offset:64\n\t"
-      "ds_read_b128 %22, %27 offset:128\n\t"
-      "ds_read_b128 %23, %27 offset:192\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(xr[0]), "=&v"(xr[1]), "=&v"(xr[2]), "=&v"(xr[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
-        "=&v"(gr[3]), "=&v"(ag[0][0]), "=&v"(ag[0][1]), "=&v"(ag[0][2]), "=&v"(ag[0][3]), "=&v"(ag[1][0]),
-        "=&v"(ag[1][1]), "=&v"(ag[1][2]), "=&v"(ag[1][3]), "=&v"(ag[2][0]), "=&v"(ag[2][1]), "=&v"(ag[2][2]),
-        "=&v"(ag[2][3]), "=&v"(cf[0]), "=&v"(cf[1]), "=&v"(cf[2]), "=&v"(cf[3])
-      : "v"(xa), "v"(lx), "v"(la), "v"(cfa)
-      : "memory");
+  static_assert(RQ == 1 || RQ == 3, "read groups of N = 4 / N = 8");
+  if constexpr (RQ == 1) {
+    asm volatile(
+        "ds_read_b64 %0, %16\n\t"
+        "ds_read_b64 %1, %16 offset:1024\n\t"
+        "ds_read_b64 %2, %16 offset:2048\n\t"
+        "ds_read_b64 %3, %16 offset:3072\n\t"
+        "ds_read_b64 %4, %17 offset:16384\n\t"
+        "ds_read_b64 %5, %17 offset:17408\n\t"
+        "ds_read_b64 %6, %17 offset:18432\n\t"
+        "ds_read_b64 %7, %17 offset:19456\n\t"
+        "ds_read_b128 %8, %18 offset:20480\n\t"
+        "ds_read_b128 %9, %18 offset:21504\n\t"
+        "ds_read_b128 %10, %18 offset:22528\n\t"
+        "ds_read_b128 %11, %18 offset:23552\n\t"
+        "ds_read_b128 %12, %19\n\t"
+        "ds_read_b128 %13, %19 offset:64\n\t"
+        "ds_read_b128 %14, %19 offset:128\n\t"
+        "ds_read_b128 %15, %19 offset:192\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xr[0]), "=&v"(xr[1]), "=&v"(xr[2]), "=&v"(xr[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
+          "=&v"(gr[3]), "=&v"(ag[0][0]), "=&v"(ag[0][1]), "=&v"(ag[0][2]), "=&v"(ag[0][3]), "=&v"(cf[0]),
+          "=&v"(cf[1]), "=&v"(cf[2]), "=&v"(cf[3])
+        : "v"(xa), "v"(lx), "v"(la), "v"(cfa)
+        : "memory");
+  } else {
+    asm volatile(
+        "ds_read_b64 %0, %24\n\t"
+        "ds_read_b64 %1, %24 offset:1024\n\t"
+        "ds_read_b64 %2, %24 offset:2048\n\t"
+        "ds_read_b64 %3, %24 offset:3072\n\t"
+        "ds_read_b64 %4, %25 offset:16384\n\t"
+        "ds_read_b64 %5, %25 offset:17408\n\t"
+        "ds_read_b64 %6, %25 offset:18432\n\t"
+        "ds_read_b64 %7, %25 offset:19456\n\t"
+        "ds_read_b128 %8, %26 offset:20480\n\t"
+        "ds_read_b128 %9, %26 offset:21504\n\t"
+        "ds_read_b128 %10, %26 offset:22528\n\t"
+        "ds_read_b128 %11, %26 offset:23552\n\t"
+        "ds_read_b128 %12, %26 offset:24576\n\t"
+        "ds_read_b128 %13, %26 offset:25600\n\t"
+        "ds_read_b128 %14, %26 offset:26624\n\t"
+        "ds_read_b128 %15, %26 offset:27648\n\t"
+        "ds_read_b128 %16, %26 offset:28672\n\t"
+        "ds_read_b128 %17, %26 offset:29696\n\t"
+        "ds_read_b128 %18, %26 offset:30720\n\t"
+        "ds_read_b128 %19, %26 offset:31744\n\t"
+        "ds_read_b128 %20, %27\n\t"
+        "ds_read_b128 %21, %27 offset:64\n\t"
+        "ds_read_b128 %22, %27 offset:128\n\t"
+        "ds_read_b128 %23, %27 offset:192\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(xr[0]), "=&v"(xr[1]), "=&v"(xr[2]), "=&v"(xr[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
+          "=&v"(gr[3]), "=&v"(ag[0][0]), "=&v"(ag[0][1]), "=&v"(ag[0][2]), "=&v"(ag[0][3]), "=&v"(ag[1][0]),
+          "=&v"(ag[1][1]), "=&v"(ag[1][2]), "=&v"(ag[1][3]), "=&v"(ag[2][0]), "=&v"(ag[2][1]), "=&v"(ag[2][2]),
+          "=&v"(ag[2][3]), "=&v"(cf[0]), "=&v"(cf[1]), "=&v"(cf[2]), "=&v"(cf[3])
+        : "v"(xa), "v"(lx), "v"(la), "v"(cfa)
+        : "memory");
+  }
 }
 
 template <int N, int P, int S, bool ACC, int H = 1>
@@ -985,8 +1018,7 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G * H) void pre_bwd_dma_kernel(PreB
   constexpr int M = PD::M, MT = PD::MT, MK = PD::MK, MP32 = PD::MP32;
   constexpr int VC = C::VC / H, VD = C::VD / H, DW = C::DW, TT = C::TT;
   constexpr int UNITS = ACC ? C::UNITS_ACC : C::UNITS;
-  static_assert(H == 1 || (H == 2 && N == 8 && P == 1 && !ACC && C::SHARED % (C::G * H) == 0),
-                "column halves: N = 8, one phi plane, no grad_x_in, shared units split evenly");
+  static_assert(H == 1 || (H == 2 && P == 1 && !ACC), "column halves: one phi plane, no grad_x_in");
   constexpr int XL = 4 / H;                                  // x loads of a wave per tile
   constexpr int LMIN = XL + C::SHARED / (C::G * H) + (ACC ? 4 : 0);  // grad_x_in: 4 more loads a wave
   constexpr int VM_START = (S - 2) * LMIN;                  // before any grad_x store
@@ -1117,7 +1149,7 @@ __global__ __launch_bounds__(64 * DmaCfg<N>::G * H) void pre_bwd_dma_kernel(PreB
         // byte 8 * r + 128 * h of the q-th 256 bytes holds columns 64h + 4r..
         const uint32_t lx = sbase + 256 * q + 128 * h + 8 * r;
         u32x2 x2[4], g2[4];
-        dma_tile_reads_h2(x2, g2, ag, cfu, lx + (C::X + 4 * w) * 1024, lx, la, cfa);
+        dma_tile_reads_h2<C::RA / 4>(x2, g2, ag, cfu, lx + (C::X + 4 * w) * 1024, lx, la, cfa);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -1753,10 +1785,13 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* ns
   da.D = D;
   da.ntiles = lay.ntiles;
   const dim3 grid((unsigned)(ncb * NG), (unsigned)ns), block(64 * DmaCfg<N>::G);
+  // two waves per stream (column halves): N = 8 always; N = 4 up to
+  // kDmaHalvesMaxT4 tokens (the results are the same bits either way)
+  const bool halves = P == 1 && (N == 8 || sta.T <= kDmaHalvesMaxT4);
   if (sta.gin)
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), grid, block, 0, st, da);
-  else if constexpr (N == 8 && P == 1)  // two waves per stream (column halves)
-    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, DmaCfg<N>::STAGES, false, 2>), grid, dim3(2 * block.x), 0, st,
+  else if (halves)
+    hipLaunchKernelGGL((pre_bwd_dma_kernel<N, 1, DmaCfg<N>::STAGES, false, 2>), grid, dim3(2 * block.x), 0, st,
                        da);
   else
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, DmaCfg<N>::STAGES, false>), grid, block, 0, st, da);
