@@ -334,10 +334,11 @@ __device__ __forceinline__ u32x4 pre_sh4(uint32_t a) {
 // N = 8 (80 phi rows, 36 KB slots, one block per CU): heads and Sinkhorn of
 // a 64-token tile take 16 passes of 4 tokens (a wave per 8 x 8 token), which
 // stalled the block's ring for a third of its time (contraction 400 -> 254
-// us without them at D = 2048, T = 32768).  The persistent kernel therefore
-// writes each tile's sums to the workspace and the split form's token-
-// parallel finalize kernel runs heads and Sinkhorn over all tokens; without
-// the mixes buffer a fourth ring slot fits (3 stages of x in flight).
+// us without them at D = 2048, T = 32768).  N = 8 therefore writes each
+// tile's sums to the workspace and the split form's token-parallel finalize
+// kernel runs heads and Sinkhorn over all tokens; without the mixes buffer a
+// fourth ring slot fits.  This kernel runs N = 8 only in its split form: the
+// persistent N = 8 contraction is pre_fwd_ks8_kernel below.
 template <int N> struct FwdDmaCfg {
   static constexpr int MT = PreDims<N>::MT;
   static constexpr int UNITS = 16 + 4 * MT;
