@@ -53,6 +53,7 @@ PAIRS = [
     ((20000, 4, 1024, torch.bfloat16), 300),
     ((4133, 4, 7168, torch.bfloat16), 100),
     ((3000, 8, 2048, torch.bfloat16), 64),       # N = 8: tile sums + finalize kernel
+    ((33000, 8, 200, torch.bfloat16), 20000),    # N = 8 persistent K-split kernel: 128-, then 64-token tiles
     ((500, 4, 520, torch.float32), 37),          # fp32 phi split into bf16 planes in the scratch
 ]
 
