@@ -266,8 +266,9 @@ __global__ __launch_bounds__(kWave * kPostFwdBlockWaves) void post_fwd_block_ker
   }
 }
 
-template <int N, typename S, bool VECTOR, bool SUM = false>  // SUM as in post_bwd_kernel
-__global__ __launch_bounds__(kWave * kPostBlockWaves) void post_bwd_block_kernel(
+// MINW: waves per SIMD the registers must allow (4 = two 8-wave blocks per CU)
+template <int N, typename S, bool VECTOR, bool SUM = false, int MINW = 1>  // SUM as in post_bwd_kernel
+__global__ __launch_bounds__(kWave * kPostBlockWaves, MINW) void post_bwd_block_kernel(
     const S* __restrict__ gy, const S* __restrict__ x, const float* __restrict__ h_res,
     const S* __restrict__ h_out, const float* __restrict__ h_post, S* __restrict__ gx,
     float* __restrict__ g_hres, S* __restrict__ g_hout, float* __restrict__ g_hpost, int D,
@@ -726,7 +727,12 @@ static int launch_post_bwd(const void* gy, const void* gy2, const void* x, const
                            h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
     } else {
       if (vec)
-        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+        // N = 4: 128 registers (a 20-byte spill) let two blocks share a CU, so
+        // one token's reduction overlaps the next one's loads (c5, A/B on one
+        // box: 2231-2247 -> 2213-2219 us back to back, 2409-2412 -> 2401-2405
+        // us after a cache flush each); wider N would spill hundreds of bytes
+        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true, false, N == 4 ? 4 : 1>), gs, bs, 0, st, (const S*)gy,
+                           (const S*)x,
                            h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
       else
         hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)gy, (const S*)x,
