@@ -233,6 +233,34 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (MASK & 32) v = add_xor32(v);
   return v;
 }
+// Sums each of R values (R % 4 == 0) over the 64 lanes of the wave with two
+// values per lane swap on the xor-32 and xor-16 levels: v_permlane32_swap
+// exchanges lanes 32..63 of its first operand with lanes 0..31 of its
+// second (v_permlane16_swap the odd 16-lane rows of the first with the even
+// rows of the second), so one swap and one add combine two values, halving
+// the registers each level; then DPP adds within each 16-lane row.
+// Afterwards every lane of row rho (lanes 16rho..16rho+15) of v[k], k < R/4,
+// holds the total of value k + rho * R / 4.  2.5 R VALU instructions against
+// 8 R for group_sum<63> on each value (12 R and 6 R LDS swizzles for
+// wave_sum).
+template <int R>
+__device__ __forceinline__ void wave_sum_rows(float (&v)[R]) {
+  static_assert(R % 4 == 0, "four rows of R / 4 values");
+  constexpr int H = R / 2, Q = R / 4;
+#pragma unroll
+  for (int k = 0; k < H; ++k) {  // v[k]: value k in lanes 0..31, value k + H in 32..63
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + H]), false, false);
+    v[k] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < Q; ++k) {  // v[k]: rows 0..3 hold values k, k + Q, k + H, k + H + Q
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + Q]), false, false);
+    v[k] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < Q; ++k) v[k] = group_sum<15>(v[k]);
+}
+
 template <int MASK>
 __device__ __forceinline__ float group_max(float v) {
   if constexpr (MASK & 1) v = fmaxf(v, dpp_mov<kDppXor1>(v));

@@ -189,15 +189,24 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
     }
   }
 
+  {
+    // the wave's totals: value k + rho * RP / 4 in row rho of acc[k]
+    constexpr int R = N * N + N, RP = (R + 3) / 4 * 4;
+    float acc[RP];
 #pragma unroll
-  for (int i = 0; i < N * N; ++i) acc_r[i] = wave_sum(acc_r[i]);
+    for (int i = 0; i < RP; ++i) acc[i] = i < N * N ? acc_r[i < N * N ? i : 0] : i < R ? acc_p[i < R ? i - N * N : 0] : 0.f;
+    wave_sum_rows<RP>(acc);
+    if ((lane & 15) == 0) {
+      const int base = (lane >> 4) * (RP / 4);
 #pragma unroll
-  for (int i = 0; i < N; ++i) acc_p[i] = wave_sum(acc_p[i]);
-  if (lane == 0) {
-#pragma unroll
-    for (int i = 0; i < N * N; ++i) g_hres[t * (N * N) + i] = acc_r[i];
-#pragma unroll
-    for (int i = 0; i < N; ++i) g_hpost[t * N + i] = acc_p[i];
+      for (int k = 0; k < RP / 4; ++k) {
+        const int i = base + k;
+        if (i < N * N)
+          g_hres[t * (N * N) + i] = acc[k];
+        else if (i < R)
+          g_hpost[t * N + i - N * N] = acc[k];
+      }
+    }
   }
 }
 
@@ -354,15 +363,19 @@ __global__ __launch_bounds__(kWave * kPostBlockWaves, MINW) void post_bwd_block_
       for (int i = 0; i < N; ++i) acc_p[i] = fmaf(hv[e], gv[i][e], acc_p[i]);
     }
   }
+  {
+    // the wave's totals: value k + rho * RP / 4 in row rho of acc[k]
+    constexpr int RP = (R + 3) / 4 * 4;
+    float acc[RP];
 #pragma unroll
-  for (int i = 0; i < N * N; ++i) acc_r[i] = wave_sum(acc_r[i]);
+    for (int i = 0; i < RP; ++i) acc[i] = i < N * N ? acc_r[i < N * N ? i : 0] : i < R ? acc_p[i < R ? i - N * N : 0] : 0.f;
+    wave_sum_rows<RP>(acc);
+    if ((lane & 15) == 0) {
+      const int base = (lane >> 4) * (RP / 4);
 #pragma unroll
-  for (int i = 0; i < N; ++i) acc_p[i] = wave_sum(acc_p[i]);
-  if (lane == 0) {
-#pragma unroll
-    for (int i = 0; i < N * N; ++i) red[wave][i] = acc_r[i];
-#pragma unroll
-    for (int i = 0; i < N; ++i) red[wave][N * N + i] = acc_p[i];
+      for (int k = 0; k < RP / 4; ++k)
+        if (base + k < R) red[wave][base + k] = acc[k];
+    }
   }
   __syncthreads();
   for (int r = threadIdx.x; r < R; r += blockDim.x) {  // R = 72 > 64 threads at N = 8, W = 1
@@ -630,16 +643,25 @@ __global__ __launch_bounds__(256) void post_bwd_dma_kernel(
       for (int i = 0; i < N; ++i) acc_p[i] = fmaf(hv[e], gv[i][e], acc_p[i]);
     }
     if (++ccb == ncb) {
-      // token done: reduce the N*N + N dot products across the wave
+      // token done: reduce the N*N + N dot products across the wave (value
+      // k + rho * RP / 4 in row rho of acc[k]); these stores only add vector
+      // memory operations newer than the counted ones
+      constexpr int R2 = N * N + N, RP = (R2 + 3) / 4 * 4;
+      float acc[RP];
 #pragma unroll
-      for (int i = 0; i < N * N; ++i) acc_r[i] = wave_sum(acc_r[i]);
+      for (int i = 0; i < RP; ++i)
+        acc[i] = i < N * N ? acc_r[i < N * N ? i : 0] : i < R2 ? acc_p[i < R2 ? i - N * N : 0] : 0.f;
+      wave_sum_rows<RP>(acc);
+      if ((lane & 15) == 0) {
+        const int base = (lane >> 4) * (RP / 4);
 #pragma unroll
-      for (int i = 0; i < N; ++i) acc_p[i] = wave_sum(acc_p[i]);
-      if (lane == 0) {
-#pragma unroll
-        for (int i = 0; i < N * N; ++i) g_hres[ctok * (N * N) + i] = acc_r[i];
-#pragma unroll
-        for (int i = 0; i < N; ++i) g_hpost[ctok * N + i] = acc_p[i];
+        for (int k = 0; k < RP / 4; ++k) {
+          const int i = base + k;
+          if (i < N * N)
+            g_hres[ctok * (N * N) + i] = acc[k];
+          else if (i < R2)
+            g_hpost[ctok * N + i - N * N] = acc[k];
+        }
       }
       ccb = 0;
       ctok += W;
