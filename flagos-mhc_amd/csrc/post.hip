@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
 // faster than default loads here).  Every output element of the forward, grad_x and grad_h_out uses
 // the FMA order of the other kernels (bit-identical results); the backward's
 // N * N + N dot products are summed per lane over its chunks, across the wave
-// (wave_sum), then over the waves in order through LDS (no atomics).
+// (wave_sum_rows), then over the waves in order through LDS (no atomics).
 // ---------------------------------------------------------------------------
 constexpr int kPostBlockWaves = 8;     // backward: 132 VGPRs at N = 4 allow 8 waves
 constexpr int kPostFwdBlockWaves = 16;  // forward: 68 VGPRs
