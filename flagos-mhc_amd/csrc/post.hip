@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256, MINW) void post_bwd_kernel(
 // wave per token a call with few tokens runs a handful of waves, each
 // streaming its whole token serially (T = 1, N = 4, D = 7168: 11 us forward,
 // 19 us backward, against 3.3 and 6.4 us here).  At large T the block forms
-// also beat the LDS-pipelined kernels below for D >= 5120 (D = 7168 on one
+// also beat the LDS-pipelined kernels below for D >= 2048 (D = 7168 on one
 // MI355X: backward 2.23 against 2.50 ms, forward 1.48 against 1.60 ms): only
 // a few tokens per CU are in flight, each read as a few long contiguous
 // streams.  Inputs are read once, so loads are non-temporal (measured 3-7%
@@ -400,8 +400,12 @@ static inline int post_block_waves(int D, int V, int cap) {
 // kernels win only for D < kPostBlockMinD.  The wave-per-token backward stays
 // for N > 4 at large T (the block form needs 225 VGPRs at N = 8 and ran 1.5x
 // slower at D = 2048).
+// (A/B on one box, N = 4 bf16, forward / backward µs, LDS-pipelined -> block:
+// D = 1024 T = 16384 50 -> 55 / 80 -> 80, D = 2048 T = 32768 223 -> 199 /
+// 342 -> 314, D = 3072 161 -> 154 / 249 -> 236, D = 4096 207 -> 204 /
+// 334-343 -> 311.)
 constexpr int64_t kPostStreamMinT = 1024;
-constexpr int kPostBlockMinD = 5120;
+constexpr int kPostBlockMinD = 2048;
 
 // ---------------------------------------------------------------------------
 // LDS-pipelined forms (bf16, 16-byte aligned rows, D % 8 == 0)

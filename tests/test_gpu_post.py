@@ -109,6 +109,7 @@ CONFIGS = [
     (16384, 4, 4096, torch.bfloat16, "softmax"),
     (32768, 8, 2048, torch.bfloat16, "softmax"),
     (4133, 4, 7168, torch.bfloat16, "softmax"),    # config-5 width, ragged T
+    (20000, 4, 1032, torch.bfloat16, "softmax"),   # LDS-pipelined kernels: D < 2048, partial last chunk
     (65536, 4, 7168, torch.bfloat16, "softmax"),   # config 5 (64-bit offsets past 2^31 bytes)
     (16, 4, 64, torch.bfloat16, "randn"),
     (40, 4, 100, torch.bfloat16, "randn"),     # D % 8 != 0: scalar path
@@ -158,7 +159,8 @@ def test_post_bwd_parity(T, N, D, dtype, gates):
 SUM_CASES = [
     # (T, N, D, dtype, the summed form is the kernel mhc_post_backward runs)
     (1100, 4, 7168, torch.bfloat16, True),    # block-per-token kernel (config 5 width)
-    (1100, 4, 4096, torch.bfloat16, False),   # LDS-pipelined shape: the block kernel stands in
+    (1100, 4, 1024, torch.bfloat16, False),   # LDS-pipelined shape: the block kernel stands in
+    (1100, 4, 4096, torch.bfloat16, True),    # block-per-token kernel (c2 width)
     (1100, 8, 2048, torch.bfloat16, True),    # wave-per-token kernel (config 4 width)
     (100, 4, 512, torch.bfloat16, True),      # few tokens: block kernel
     (1030, 4, 264, torch.float32, True),      # fp32 rows
@@ -192,7 +194,8 @@ def test_post_bwd_sum_parity(T, N, D, dtype, fused):
 
 
 @pytest.mark.parametrize("N,D,dtype", [
-    (4, 4096, torch.bfloat16),   # 1100 tokens: LDS-pipelined kernels (D < 5120)
+    (4, 1024, torch.bfloat16),   # 1100 tokens: LDS-pipelined kernels (D < 2048)
+    (4, 4096, torch.bfloat16),   # 1100 tokens: block-per-token kernels
     (4, 2048, torch.bfloat16),
     (8, 2048, torch.bfloat16),   # 1100 tokens: wave-per-token backward (N > 4)
     (6, 264, torch.float32),
