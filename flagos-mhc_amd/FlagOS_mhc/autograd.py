@@ -90,7 +90,7 @@ class MhcPostPreClampSinkhornFn(torch.autograd.Function):
     backward for x_next's whole gradient: the post kernel reads the pre
     backward's grad_x beside the gradient that reaches x_next directly
     (``mhc_post_bwd_sum``).  Where the post kernel for the shape has no
-    summed form (N = 4 bf16, D < 5120), the pre backward adds that gradient
+    summed form (N = 4 bf16, D < 2048), the pre backward adds that gradient
     into its grad_x instead (``mhc_pre_bwd_acc``)."""
 
     @staticmethod

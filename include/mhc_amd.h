@@ -85,7 +85,7 @@ int mhc_post_bwd_sum(const void* grad_y, const void* grad_y2, const void* x, con
 /*
  * 1 when mhc_post_bwd_sum runs the kernel form mhc_post_bwd runs for this
  * shape (16-byte aligned rows), plus one read; 0 when that form has no
- * summed variant (N = 4 bf16, T >= 1024, D < 5120) and mhc_post_bwd_sum takes
+ * summed variant (N = 4 bf16, T >= 1024, D < 2048) and mhc_post_bwd_sum takes
  * a slower one.  No counterpart in the reference.
  */
 int mhc_post_bwd_sum_fused(int64_t T, int32_t N, int32_t D, int32_t dtype);
