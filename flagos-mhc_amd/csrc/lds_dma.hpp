@@ -56,4 +56,13 @@ __device__ __forceinline__ void lds_read4(u32x4 (&v)[4], uint32_t a) {
       : "memory");
 }
 
+// Reads the R 1 KB units of a slot (lane's 16 bytes each), complete on return.
+template <int R>
+__device__ __forceinline__ void read_slot(u32x4 (&v)[R], uint32_t base) {
+  static_assert(R % 4 == 1, "R = 4k + 1 rows");
+#pragma unroll
+  for (int i = 0; i + 4 <= R; i += 4) lds_read4<1024>(*reinterpret_cast<u32x4(*)[4]>(&v[i]), base + i * 1024);
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v[R - 1]) : "v"(base + (R - 1) * 1024) : "memory");
+}
+
 }  // namespace mhc

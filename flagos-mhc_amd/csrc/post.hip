@@ -426,15 +426,6 @@ constexpr int kPostBlockMinD = 2048;
 constexpr int kPostFwdStages = 4;  // 4 waves x 4 slots x 5 KB: two blocks per CU
 constexpr int kPostBwdStages = 4;  // 4 waves x 4 slots x 9 KB: one block per CU
 
-// Reads the R 1 KB units of a slot (lane's 16 bytes each), complete on return.
-template <int R>
-__device__ __forceinline__ void read_slot(u32x4 (&v)[R], uint32_t base) {
-  static_assert(R % 4 == 1, "R = 4k + 1 rows");
-#pragma unroll
-  for (int i = 0; i + 4 <= R; i += 4) lds_read4<1024>(*reinterpret_cast<u32x4(*)[4]>(&v[i]), base + i * 1024);
-  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v[R - 1]) : "v"(base + (R - 1) * 1024) : "memory");
-}
-
 template <int N>
 __global__ __launch_bounds__(256) void post_fwd_dma_kernel(const bf16_t* __restrict__ x,
                                                            const float* __restrict__ h_res,

@@ -6,9 +6,11 @@
 // <grad_y, y> + <grad_post_out, post_out> + <grad_comb_frag, comb_frag>.
 //
 // Kernel A (pre_bwd_small_kernel), a block per 16 tokens:
-//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (wave per token
-//   for N = 4 at T >= 16384; otherwise summed in fixed order from the
-//   partials of pre_bwd_gpre_kernel, a block per (token, 2048 columns))
+//   grad_pre[t,n] = <grad_y[t,:], x[t,n,:]>                (bf16 rows at
+//   T >= 16384: the sums of pre_bwd_gpre_dma_kernel, a wave per token over
+//   an LDS ring; smaller T: summed in fixed order from the partials of
+//   pre_bwd_gpre_kernel, a block per (token, 2048 columns); N = 4 in other
+//   dtypes at T >= 16384: a wave per token here)
 //   Sinkhorn / softmax / clamp / sigmoid-head VJP, lane per matrix element
 //   -> grad_mixes (T,M) and scale[t] = -inv^2 * <grad_mixes, mixes> / (N*D)
 //   (because <x, grad_mixes @ phi> = <grad_mixes, mixes> / inv), plus a
@@ -63,6 +65,7 @@ struct PreBwdSmallArgs {
   int64_t sink_stride;
   const float* gpre_part;  // [T][gpre_chunks][N] grad_pre partials, or null
   int gpre_chunks;
+  float* gpre_buf;         // the workspace's partials region (host side: the LDS-pipelined grad_pre)
   int comp;                // compensated (Neumaier) sums of the block partials
   int64_t T;
   int D;
@@ -133,6 +136,104 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_gpre_kernel(const void* x
       part[(tok * gridDim.y + blockIdx.y) * N + tid] = s;
     }
     __syncthreads();  // red is rewritten for the next token
+  }
+}
+
+// grad_pre for large T, LDS-pipelined (bf16, 16-byte rows): every wave of a
+// persistent grid streams its tokens w, w + W, ... through a private ring of
+// S slots, one slot = the token's N x rows and its grad_y row over 512
+// columns (one 1 KB direct-to-LDS load per row, lane l -> columns 8l..8l+7),
+// loaded S - 1 slots ahead; a wave reads back only what its own loads wrote,
+// so there are no barriers.  Each lane accumulates its columns' products in
+// kernel A's order (per 512-column chunk, fmaf over its 8 columns) and the
+// token's N sums leave through wave_sum, as in kernel A's own loop, to
+// part[t][n] (one chunk), which kernel A then reads: the same bits as its
+// wave-per-token loop, the reads at the direct-to-LDS rate.
+constexpr int kGpreDmaWaves = 4;
+template <int N> struct GpreDmaCfg {
+  static constexpr int R = N + 1;          // slot rows: x[0..N-1], grad_y
+  static constexpr int S = N == 4 ? 6 : 4;  // 4 waves x S x R KB: 120 / 144 KB
+};
+
+template <int N>
+__global__ __launch_bounds__(kWave * kGpreDmaWaves) void pre_bwd_gpre_dma_kernel(const bf16_t* __restrict__ x,
+                                                                                 const bf16_t* __restrict__ gy,
+                                                                                 float* __restrict__ part, int64_t T,
+                                                                                 int D) {
+  constexpr int R = GpreDmaCfg<N>::R, S = GpreDmaCfg<N>::S;
+  // slot j's loads have landed once at most VM newer vector memory operations
+  // are outstanding (the loads of the S - 2 slots issued after it; a token's
+  // sums stored in between only add newer ones)
+  constexpr int VM = (S - 2) * R;
+  static_assert(VM < 64 && R % 4 == 1, "vmcnt range; slot rows 4k + 1");
+  __shared__ u32x4 ring[kGpreDmaWaves * S * R * kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t gw = (int64_t)blockIdx.x * kGpreDmaWaves + wave, W = (int64_t)gridDim.x * kGpreDmaWaves;
+  const int ncb = (D + 511) / 512;
+  const int64_t ntok = (T - gw + W - 1) / W;
+  if (ntok <= 0) return;  // this wave only: no barriers below
+  const int64_t J = ntok * ncb;
+  const uint32_t wring = lds_addr(ring) + (uint32_t)(wave * S * R * 1024);
+  const int64_t ND = (int64_t)N * D;
+
+  int64_t itok = gw;
+  int icb = 0;
+  auto issue = [&](int64_t j) {
+    const uint32_t slot = wring + (uint32_t)((j % S) * R * 1024);
+    const int col = icb * 512 + 8 * lane;
+    const auto rx = rows_rsrc(x + itok * ND, ND * 2);
+    const auto rg = rows_rsrc(gy + itok * D, (int64_t)D * 2);
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(uintptr_t)(slot + n * 1024), 16,
+                                               col < D ? (uint32_t)(((int64_t)n * D + col) * 2) : kBufferOob,
+                                               0, 0, 2 /* nt */);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(uintptr_t)(slot + N * 1024), 16,
+                                             col < D ? (uint32_t)(col * 2) : kBufferOob, 0, 0, 2);
+    if (++icb == ncb) {
+      icb = 0;
+      itok += W;
+    }
+  };
+  for (int64_t j = 0; j < S - 1 && j < J; ++j) issue(j);
+
+  int64_t ctok = gw;
+  int ccb = 0;
+  float acc[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) acc[n] = 0.f;
+  for (int64_t j = 0; j < J; ++j) {
+    if (j + S - 2 < J)
+      wait_vmcnt<VM>();
+    else
+      wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    // the next loads reuse the slot this wave read (and waited for) last iteration
+    if (j + S - 1 < J) issue(j + S - 1);
+    u32x4 v[R];
+    read_slot<R>(v, wring + (uint32_t)((j % S) * R * 1024) + lane * 16);
+    float g8[8];
+    Store<bf16_t>::unpack(v[N], g8);
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      float x8[8];
+      Store<bf16_t>::unpack(v[n], x8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[n] = fmaf(g8[i], x8[i], acc[n]);
+    }
+    if (++ccb == ncb) {
+#pragma unroll
+      for (int n = 0; n < N; ++n) acc[n] = wave_sum(acc[n]);
+      if (lane == 0) {
+#pragma unroll
+        for (int n = 0; n < N; ++n) part[ctok * N + n] = acc[n];
+      }
+#pragma unroll
+      for (int n = 0; n < N; ++n) acc[n] = 0.f;
+      ccb = 0;
+      ctok += W;
+    }
   }
 }
 
@@ -1593,6 +1694,9 @@ struct BwdLayout {
 // the GPU time still drops (28.0 -> 24.9 us from graph replays) while an
 // eager call pays about 2 us more host time for the extra launch.
 constexpr int64_t kGpreSplitMinT = 1, kGpreSplitMaxT = 16384;
+// From this many tokens bf16 rows take the LDS-pipelined grad_pre kernel
+// (a wave per token, so it needs many tokens to fill the chip).
+constexpr int64_t kGpreDmaMinT = 16384;
 
 static int64_t dma_max_splits(int D) {
   const int64_t ncb = (D + DmaCfg<4>::DW - 1) / DmaCfg<4>::DW;
@@ -1649,8 +1753,8 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   // A's own wave-per-token grad_pre loop)
   const int64_t max_t = N == 8 ? INT64_MAX : kGpreSplitMaxT;
   b.gpre_chunks = (T >= kGpreSplitMinT && T < max_t) ? (int)((D + kGpreCols - 1) / kGpreCols) : 0;
-  b.off_gpre = off;
-  off += align256((size_t)T * b.gpre_chunks * N * 4);
+  b.off_gpre = off;  // at least one chunk: the LDS-pipelined grad_pre kernel's sums
+  off += align256((size_t)T * (b.gpre_chunks > 0 ? b.gpre_chunks : 1) * N * 4);
   b.off_gpl = off;  // compensated mode: g planes, 3 bf16 per (token, padded m)
   off += align256((size_t)((T + kCompTile - 1) / kCompTile) * kCompTile * b.MP * kCompPlanesG * 2);
   b.total = off;
@@ -1828,7 +1932,15 @@ static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwd
     sa.coef = nullptr;
   }
   int rc;
-  if (sa.gpre_part) {
+  if (streaming && sa.T >= kGpreDmaMinT) {
+    // grad_pre through the LDS-pipelined kernel: one chunk of sums per token
+    sa.gpre_part = sa.gpre_buf;
+    sa.gpre_chunks = 1;
+    hipLaunchKernelGGL((pre_bwd_gpre_dma_kernel<N>), dim3((unsigned)device_cu_count()), dim3(kWave * kGpreDmaWaves),
+                       0, st, static_cast<const bf16_t*>(sa.x), static_cast<const bf16_t*>(sa.gy), sa.gpre_buf,
+                       sa.T, sa.D);
+    if ((rc = check_launch("pre_bwd_gpre_dma"))) return rc;
+  } else if (sa.gpre_part) {
     const dim3 gG((unsigned)(sa.T < kGpreGridT ? sa.T : kGpreGridT), (unsigned)lay.gpre_chunks);
     float* part = const_cast<float*>(sa.gpre_part);
     if (vec)
@@ -1958,6 +2070,7 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
   sa.sink_stride = lay.nblkA * kBwdTile * lay.L;
   sa.gpre_part = lay.gpre_chunks ? reinterpret_cast<float*>(ws + lay.off_gpre) : nullptr;
   sa.gpre_chunks = lay.gpre_chunks;
+  sa.gpre_buf = reinterpret_cast<float*>(ws + lay.off_gpre);
   sa.comp = (flags & MHC_PRE_BWD_COMPENSATED) ? 1 : 0;
   sa.T = T;
   sa.D = D;
