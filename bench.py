@@ -81,7 +81,7 @@ def run_chain(m, x, phi, alpha, base, h_out, gup, kw, _pre_forward):
 # (the pre operators run two or more kernels)
 SINGLE_KERNEL_OPS = {
     "post_fwd": "post_fwd_block_kernel<4, bf16_t, true>",
-    "post_bwd": "post_bwd_block_kernel<4, bf16_t, true, false, 4>",
+    "post_bwd": "post_bwd_block_kernel<4, bf16_t, true, false, 1>",
 }
 
 

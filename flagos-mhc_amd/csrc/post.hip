@@ -400,10 +400,10 @@ static inline int post_block_waves(int D, int V, int cap) {
 // kernels win only for D < kPostBlockMinD.  The wave-per-token backward stays
 // for N > 4 at large T (the block form needs 225 VGPRs at N = 8 and ran 1.5x
 // slower at D = 2048).
-// (A/B on one box, N = 4 bf16, forward / backward µs, LDS-pipelined -> block:
-// D = 1024 T = 16384 50 -> 55 / 80 -> 80, D = 2048 T = 32768 223 -> 199 /
-// 342 -> 314, D = 3072 161 -> 154 / 249 -> 236, D = 4096 207 -> 204 /
-// 334-343 -> 311.)
+// (A/B on one box, N = 4 bf16, forward / backward us, LDS-pipelined -> block:
+// bench.py at D = 2048 T = 32768 216 -> 202 / 331-336 -> 293, D = 4096
+// T = 16384 208 -> 206 / 325 -> 319; a timing loop at D = 1024 T = 16384
+// 50 -> 55 / 80 -> 80, D = 3072 161 -> 154 / 249 -> 236.)
 constexpr int64_t kPostStreamMinT = 1024;
 constexpr int kPostBlockMinD = 2048;
 
@@ -743,17 +743,24 @@ static int launch_post_bwd(const void* gy, const void* gy2, const void* x, const
         hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
                            h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
     } else {
-      if (vec)
-        // N = 4: 128 registers (a 20-byte spill) let two blocks share a CU, so
-        // one token's reduction overlaps the next one's loads (c5, A/B on one
-        // box: 2231-2247 -> 2213-2219 us back to back, 2409-2412 -> 2401-2405
-        // us after a cache flush each); wider N would spill hundreds of bytes
-        hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true, false, N == 4 ? 4 : 1>), gs, bs, 0, st, (const S*)gy,
-                           (const S*)x,
-                           h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
-      else
+      if (vec) {
+        // N = 4 with exactly one 512-column chunk per wave (D in (3584, 4096]):
+        // capped at 128 registers (a 20-byte spill) two blocks share a CU and
+        // one token's reduction overlaps the next one's loads (bench.py at D =
+        // 4096, T = 16384: 337-342 -> 319-322 us); with two chunks a wave (D =
+        // 7168: 2.19-2.22 -> 2.32-2.33 ms) or four waves (D = 2048: 293 -> 311
+        // us) the cap is slower
+        if (N == 4 && (D + 511) / 512 == kPostBlockWaves)
+          hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true, false, 4>), gs, bs, 0, st, (const S*)gy,
+                             (const S*)x, h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost,
+                             D, g2);
+        else
+          hipLaunchKernelGGL((post_bwd_block_kernel<N, S, true>), gs, bs, 0, st, (const S*)gy, (const S*)x,
+                             h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
+      } else {
         hipLaunchKernelGGL((post_bwd_block_kernel<N, S, false>), gs, bs, 0, st, (const S*)gy, (const S*)x,
                            h_res, (const S*)h_out, h_post, (S*)gx, g_hres, (S*)g_hout, g_hpost, D, g2);
+      }
     }
     return check_launch("post_bwd_block");
   }
