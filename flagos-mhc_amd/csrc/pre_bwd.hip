@@ -946,11 +946,12 @@ template <int N> struct DmaCfg {
 };
 
 constexpr int kDmaAccStages = 3;               // accumulating form: 3 x 41 KB (N = 4) / 48 KB (N = 8)
-// N = 4 runs the two-waves-per-stream form up to this many tokens: measured
-// on one MI355X (whole backward, D = 2048 / 4096 / 7168 at T = 4096..32768)
-// 5-12% faster, but at T = 65536 equal (D = 4096) or 4-6% slower (D = 5120,
-// 7168) than one wave per stream.
-constexpr int64_t kDmaHalvesMaxT4 = 32768;
+// N = 4 keeps one wave per stream: two (the column-halves form N = 8 runs)
+// measured 5-12% faster in a back-to-back timing loop at T <= 32768, where
+// part of x stays in the MALL between calls, but 3-4% slower in bench.py,
+// which evicts the caches before every call (D = 4096, T = 16384: 329-333
+// against 342-344 us), and 4-6% slower at T = 65536 either way.
+constexpr int64_t kDmaHalvesMaxT4 = 0;
 constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
 
 struct PreBwdDmaArgs {
@@ -1889,8 +1890,8 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* ns
   da.D = D;
   da.ntiles = lay.ntiles;
   const dim3 grid((unsigned)(ncb * NG), (unsigned)ns), block(64 * DmaCfg<N>::G);
-  // two waves per stream (column halves): N = 8 always; N = 4 up to
-  // kDmaHalvesMaxT4 tokens (the results are the same bits either way)
+  // two waves per stream (column halves): N = 8 (the results are the same
+  // bits either way)
   const bool halves = P == 1 && (N == 8 || sta.T <= kDmaHalvesMaxT4);
   if (sta.gin)
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), grid, block, 0, st, da);
