@@ -946,12 +946,11 @@ template <int N> struct DmaCfg {
 };
 
 constexpr int kDmaAccStages = 3;               // accumulating form: 3 x 41 KB (N = 4) / 48 KB (N = 8)
-// N = 4 keeps one wave per stream: two (the column-halves form N = 8 runs)
+// Only N = 8 runs the two-waves-per-stream (column halves) form.  At N = 4 it
 // measured 5-12% faster in a back-to-back timing loop at T <= 32768, where
 // part of x stays in the MALL between calls, but 3-4% slower in bench.py,
-// which evicts the caches before every call (D = 4096, T = 16384: 329-333
-// against 342-344 us), and 4-6% slower at T = 65536 either way.
-constexpr int64_t kDmaHalvesMaxT4 = 0;
+// which evicts the caches before every call (D = 4096, T = 16384: 342-344
+// against 329-333 us), and 4-6% slower at T = 65536 either way.
 constexpr int kDmaMaxBlocks = 512;             // bounds the token splits of small D
 
 struct PreBwdDmaArgs {
@@ -1890,12 +1889,11 @@ static int launch_dma(const BwdLayout& lay, const PreBwdStreamArgs& sta, int* ns
   da.D = D;
   da.ntiles = lay.ntiles;
   const dim3 grid((unsigned)(ncb * NG), (unsigned)ns), block(64 * DmaCfg<N>::G);
-  // two waves per stream (column halves): N = 8 (the results are the same
-  // bits either way)
-  const bool halves = P == 1 && (N == 8 || sta.T <= kDmaHalvesMaxT4);
+  // two waves per stream (column halves) at N = 8 (the results are the same
+  // bits as with one)
   if (sta.gin)
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, P, kDmaAccStages, true>), grid, block, 0, st, da);
-  else if (halves)
+  else if constexpr (N == 8 && P == 1)
     hipLaunchKernelGGL((pre_bwd_dma_kernel<N, 1, DmaCfg<N>::STAGES, false, 2>), grid, dim3(2 * block.x), 0, st,
                        da);
   else
