@@ -15,7 +15,9 @@ functions are the pure-PyTorch references of the same semantics.
 Beyond the reference: ``mhc_post_pre_clamp_sinkhorn`` (and its autograd
 form) fuses mhc_post of one layer with mhc_pre_clamp_sinkhorn of the next;
 ``mhc_post_backward_sum`` is mhc_post_backward for a gradient given as two
-summands (the fused layer's backward).
+summands (the fused layer's backward); ``check_errors`` raises if an earlier
+single-pass pre forward gave up one of its bounded waits (the pre backward
+and every later pre forward check that too).
 
 Importing the package also registers the operators as torch.ops.flagos_mhc.*
 (``FlagOS_mhc.library``) for torch.compile and HIP-graph capture.
@@ -40,6 +42,7 @@ from .autograd import (
     mhc_post_pre_clamp_sinkhorn_fn,
 )
 from .mhc_post_pre import mhc_post_pre_clamp_sinkhorn
+from ._lib import check_errors
 from . import library  # registers torch.ops.flagos_mhc.* (torch.compile / HIP graphs)
 
 __all__ = [
@@ -61,4 +64,6 @@ __all__ = [
     "mhc_post_pre_clamp_sinkhorn_fn",
     # beyond the reference: mhc_post_backward for a gradient given as two summands
     "mhc_post_backward_sum",
+    # beyond the reference: reports a single-pass pre forward that gave up a bounded wait
+    "check_errors",
 ]

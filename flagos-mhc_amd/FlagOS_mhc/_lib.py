@@ -7,6 +7,7 @@ are not on a HIP device, the operators raise instead of computing on the CPU.
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import os
 import threading
@@ -35,6 +36,10 @@ _SIGNATURES = {
     "mhc_pre_fwd": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                _i64, _i32, _i32, _vp]),
+    "mhc_pre_fwd_ex": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
+                                  _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp,
+                                  _i64, _i32, _i32, _vp]),
+    "mhc_debug_set_wait_limit": (None, [_i64]),
     "mhc_pre_fwd_noalloc": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32, _f32, _i32,
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
     "mhc_pre_bwd_acc": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -113,3 +118,76 @@ def dtype_code(what: str, dt: torch.dtype) -> int:
         return DTYPE_CODE[dt]
     except KeyError:
         raise NotImplementedError(f"{what}: dtype {dt} not supported (float32, bfloat16, float16)")
+
+
+class SinglePassStatus:
+    """Where the single-pass pre forward reports its bounded waits.
+
+    That kernel waits for the other CUs of its group with a limit (0.25 s
+    without progress); if a wait gives up, the call's outputs are NaN and the
+    kernels write a failure code to the status word of ``mhc_pre_fwd_ex``.
+    Each call gets a word in a ring of pinned host memory (written by the GPU
+    with a system-scope store, read by the host once the call's event has
+    completed), so no call waits for the GPU.  ``check`` raises for a failed
+    call: without blocking at the start of every operator call (calls whose
+    work has finished), blocking in the pre backward and in
+    ``FlagOS_mhc.check_errors``."""
+
+    SLOTS = 64
+
+    def __init__(self):
+        self._lock = threading.RLock()
+        self._words = None
+        self._busy = [False] * self.SLOTS
+        self._next = 0
+        self._pending = collections.deque()  # (slot, event), oldest first
+
+    def acquire(self):
+        """A zeroed word for the next call: (slot, its address).  A word is
+        reused only after the call that reported into it was checked."""
+        with self._lock:
+            if self._words is None:
+                self._words = torch.zeros(self.SLOTS, dtype=torch.int32, pin_memory=True)
+            while self._busy[self._next]:
+                self.check(block=True)
+            slot = self._next
+            self._next = (slot + 1) % self.SLOTS
+            self._words[slot] = 0
+            return slot, self._words.data_ptr() + 4 * slot
+
+    def commit(self, slot, stream) -> None:
+        """The call that got `slot` was enqueued on `stream`."""
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        with self._lock:
+            self._busy[slot] = True
+            self._pending.append((slot, ev))
+
+    def check(self, block: bool) -> None:
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            return
+        with self._lock:
+            while self._pending:
+                slot, ev = self._pending[0]
+                if not block and not ev.query():
+                    return
+                ev.synchronize()
+                self._pending.popleft()
+                self._busy[slot] = False
+                code = int(self._words[slot])
+                if code:
+                    raise RuntimeError(
+                        f"mhc_pre_clamp_sinkhorn: an earlier single-pass forward call gave up a "
+                        f"bounded wait for the other CUs of its group (status {code}: the GPU stalled "
+                        "longer than the wait limit); that call's outputs are NaN")
+
+
+SINGLE_PASS = SinglePassStatus()
+
+
+def check_errors(block: bool = True) -> None:
+    """Raise RuntimeError if an earlier single-pass pre forward gave up a
+    bounded wait (its outputs are then NaN).  With ``block`` (the default)
+    wait for every such call's work to finish first; without it, look only
+    at calls that have finished."""
+    SINGLE_PASS.check(block)

@@ -27,6 +27,7 @@ import torch
 from . import _lib
 
 SUPPORTED_N = (4, 8)
+SINGLE_PASS_MIN_T = 8192  # fewest tokens the single-pass form takes (csrc/pre_fwd_coop.hpp)
 
 
 def _flatten(x):
@@ -53,6 +54,7 @@ def _check_params(N, D, phi, alpha, base):
 def _pre_forward(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, iter_times,
                  need_backward, want_x_scaled):
     _lib.require_device("mhc_pre_clamp_sinkhorn", x, phi, alpha, base)
+    _lib.SINGLE_PASS.check(block=False)  # earlier calls' bounded waits, where finished
     xf, yshape = _flatten(x)
     T, N, D = xf.shape
     M = _check_params(N, D, phi, alpha, base)
@@ -79,15 +81,24 @@ def _pre_forward(x, phi, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max, it
         lib = _lib.load()
         ws_bytes = int(lib.mhc_pre_fwd_workspace_size(T, N, D, pcode))
         ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+        # the shapes the single-pass form can take (N = 4, bf16, T >= 8192;
+        # never under stream capture) report its bounded waits into a status word
+        slot = status = None
+        if (N == 4 and T >= SINGLE_PASS_MIN_T and xf.dtype == torch.bfloat16
+                and phi_c.dtype == torch.bfloat16 and not torch.cuda.is_current_stream_capturing()):
+            slot, status = _lib.SINGLE_PASS.acquire()
+        stream = _lib.stream_of(xf)
         with torch.cuda.device(dev):
-            rc = lib.mhc_pre_fwd(
+            rc = lib.mhc_pre_fwd_ex(
                 xf.data_ptr(), xcode, phi_c.data_ptr(), pcode, alpha_c.data_ptr(),
                 base_c.data_ptr(), float(norm_eps), float(hc_eps), float(clamp_min),
                 float(clamp_max), int(iter_times), y.data_ptr(), post_out.data_ptr(),
                 comb.data_ptr(), _lib.ptr(inv_rms), _lib.ptr(mixes), _lib.ptr(logits),
-                _lib.ptr(pre), _lib.ptr(x_scaled), ws.data_ptr(), ws_bytes, T, N, D,
-                _lib.stream_of(xf))
+                _lib.ptr(pre), _lib.ptr(x_scaled), ws.data_ptr(), ws_bytes, status, T, N, D,
+                stream)
         _lib.check(rc, "mhc_pre_clamp_sinkhorn")
+        if slot is not None:
+            _lib.SINGLE_PASS.commit(slot, torch.cuda.current_stream(dev))
     result = {"y": y.reshape(yshape), "post_out": post_out, "comb_frag": comb}
     if need_backward:
         result.update(inv_rms=inv_rms, x_scaled=x_scaled, mixes=mixes, h_res_logits=logits,

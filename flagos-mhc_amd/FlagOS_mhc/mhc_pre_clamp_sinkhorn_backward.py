@@ -73,6 +73,9 @@ def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_ou
     del norm_eps  # folded into inv_rms
     _lib.require_device("mhc_pre_clamp_sinkhorn_backward", x, phi, alpha, base, inv_rms, mixes,
                         pre, grad_y, grad_post_out, grad_comb_frag, grad_x_in)
+    # a forward whose single pass gave up a bounded wait left NaN inputs for
+    # this call: raise here rather than propagate them
+    _lib.SINGLE_PASS.check(block=True)
     if x.dim() not in (3, 4):
         raise ValueError(f"unsupported x.dim()={x.dim()}")
     shape = tuple(x.shape)

@@ -62,7 +62,9 @@ struct PreFwdArgs {
   float* inv_ws;
   // single-pass form: its status word (nonzero when a bounded wait timed
   // out); the finalize kernel then writes NaN to every output of the call
+  // and copies the word to status_out (the caller's, may be null)
   const uint32_t* co_status;
+  int32_t* status_out;
 };
 
 template <int N, typename S, bool VEC, int P>
@@ -876,7 +878,12 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
   }
   // a failed single-pass run makes every output of the call NaN (y and
   // x_scaled rows included) rather than leave wrong values behind
-  const bool failed = a.co_status && *a.co_status != 0u;
+  const uint32_t co_st = a.co_status ? *a.co_status : 0u;
+  const bool failed = co_st != 0u;
+  // the caller's status word, which may live in host memory: a system-scope
+  // store writes through to it
+  if (a.co_status && a.status_out && blockIdx.x == 0 && tid == 0)
+    __hip_atomic_store(a.status_out, (int32_t)co_st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   const float inv = failed ? __builtin_nanf("") : rms_inv(ssq, K, a.norm_eps);
   const float mix_l = acc_l * inv, mix_h = acc_h * inv;
   if (failed) {
@@ -1200,13 +1207,13 @@ extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, in
   return coop && kPreFwdWsBase + coop > base ? kPreFwdWsBase + coop : base;
 }
 
-extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
-                           const float* alpha, const float* base, float norm_eps, float hc_eps,
-                           float clamp_min, float clamp_max, int32_t iter_times, void* y,
-                           float* post_out, float* comb_frag, float* inv_rms, float* mixes,
-                           float* h_res_logits, float* pre, float* x_scaled, void* workspace,
-                           size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
-                           void* stream) {
+extern "C" int mhc_pre_fwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                              const float* alpha, const float* base, float norm_eps, float hc_eps,
+                              float clamp_min, float clamp_max, int32_t iter_times, void* y,
+                              float* post_out, float* comb_frag, float* inv_rms, float* mixes,
+                              float* h_res_logits, float* pre, float* x_scaled, void* workspace,
+                              size_t workspace_bytes, int32_t* status, int64_t T, int32_t N, int32_t D,
+                              void* stream) {
   clear_error();
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_fwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
@@ -1242,6 +1249,7 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
   a.x_scaled = x_scaled;
   a.T = T;
   a.D = D;
+  a.status_out = status;
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(y) && (!x_scaled || aligned16(x_scaled));
   const size_t y_ws = fwd_y_ws_bytes(T, N), ha_ws = heads_apart_bytes(T, N);
   const size_t dma_ws = kPreFwdWsBase + (ha_ws > y_ws ? ha_ws : y_ws);
@@ -1254,6 +1262,22 @@ extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int3
     case MHC_DTYPE_F32: return dispatch_pre_fwd<float>(N, a, vec, st);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_fwd: x dtype %d not supported", x_dtype);
+}
+
+extern "C" int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                           const float* alpha, const float* base, float norm_eps, float hc_eps,
+                           float clamp_min, float clamp_max, int32_t iter_times, void* y,
+                           float* post_out, float* comb_frag, float* inv_rms, float* mixes,
+                           float* h_res_logits, float* pre, float* x_scaled, void* workspace,
+                           size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                           void* stream) {
+  return mhc_pre_fwd_ex(x, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
+                        iter_times, y, post_out, comb_frag, inv_rms, mixes, h_res_logits, pre, x_scaled,
+                        workspace, workspace_bytes, nullptr, T, N, D, stream);
+}
+
+extern "C" void mhc_debug_set_wait_limit(int64_t ticks) {
+  coop_wait_limit_slot().store(ticks < 0 ? -1 : ticks, std::memory_order_relaxed);
 }
 
 // ---- allocation-free variant ------------------------------------------------

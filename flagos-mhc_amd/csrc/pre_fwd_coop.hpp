@@ -47,9 +47,15 @@
 // which skip the reader's CU L1 (it may hold stale copies of the ring) and
 // find them in that L2: every member of a group sits on one XCC.
 // Membership comes from the XCC_ID hardware register at the start of the
-// kernel (a grid-wide registration, so all blocks must be resident:
-// cooperative launch, one block per CU), so it holds whichever CU the
-// dispatcher chose for a block.
+// kernel (a grid-wide registration, so all blocks must be resident: the
+// grid is one block per CU and a block's LDS leaves no room for a second on
+// its CU, so on a device with no other work every block is resident at
+// once), so it holds whichever CU the dispatcher chose for a block.  The
+// launch is an ordinary one: a cooperative launch (hipLaunchCooperativeKernel)
+// gave the same residency but left the HIP runtime's teardown at process
+// exit to crash under rocprofv3.  A block that is not resident in time
+// (other work occupying CUs) only delays the others, and their bounded waits
+// turn a long delay into a reported failure.
 //
 // Progress.  L-waves reuse an LDS slot once the Y-waves copied it; P-waves
 // reuse their LDS slot once the Y-waves read it; records of tile q are
@@ -57,7 +63,9 @@
 // tile q (kCoR >= 2 S + 2 kCoLag + 2 tiles, see CoCfg).  Every wait is
 // bounded: after kCoTimeout of s_memrealtime without progress a wave sets the
 // block's abort flag and the status word, and every wave leaves; the finalize
-// kernel then writes NaN to every output of the call.
+// kernel then writes NaN to every output of the call and copies the status
+// word to the caller's status location (mhc_pre_fwd_ex), so the host learns
+// of it when the call's work has finished.
 #pragma once
 
 namespace mhc {
@@ -790,25 +798,38 @@ inline size_t coop_ws_bytes(int64_t T, int N, int D) {
          align256((size_t)T * 24 * 4) + align256((size_t)T * 4) + fwd_y_ws_bytes(T, 4);
 }
 
-// Per-device: can the single-pass kernel run co-resident on every CU?
-inline bool coop_supported(const void* kernel, int threads, int nch) {
+// Per-device: does one block of the single-pass kernel fit a CU (so a grid
+// of one block per CU is resident at once on an otherwise idle device)?
+inline bool coop_fits(const void* kernel, int threads, int nch) {
   static std::atomic<int> cache[64][2];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
   std::atomic<int>& slot = cache[dev][nch == 32];
   int v = slot.load(std::memory_order_relaxed);
   if (v) return v > 0;
-  int coop = 0, nb = 0;
-  bool ok = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess && coop &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1;
+  int nb = 0;
+  const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1;
   (void)hipGetLastError();
   slot.store(ok ? 1 : -1, std::memory_order_relaxed);
   return ok;
 }
 
+// Limit of every bounded wait, in s_memrealtime ticks (100 MHz): kCoTimeout
+// unless mhc_debug_set_wait_limit set another (a test hook that forces the
+// failure path; it is never read from the environment).
+inline std::atomic<int64_t>& coop_wait_limit_slot() {
+  static std::atomic<int64_t> v{-1};
+  return v;
+}
+inline uint64_t coop_wait_limit() {
+  const int64_t v = coop_wait_limit_slot().load(std::memory_order_relaxed);
+  return v < 0 ? kCoTimeout : (uint64_t)v;
+}
+
 // Runs the single-pass form when it applies (N = 4 bf16 fast path, D with a
 // slice geometry, T >= kCoopMinT, enough workspace, not under stream capture,
-// cooperative launch available); *used says whether it ran.
+// a block fits a CU); *used says whether it ran.  The finalize kernel copies
+// the status word to a.status_out (when set).
 template <bool XS>
 static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace_bytes, hipStream_t st,
                                   bool* used) {
@@ -824,19 +845,14 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   }
   const void* kfn = (const void*)pre_fwd_coop_kernel<32, XS>;
   const int threads = CoCfg<32>::THREADS;
-  if (!coop_supported(kfn, threads, nch)) return MHC_OK;
+  if (!coop_fits(kfn, threads, nch)) return MHC_OK;
   char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
   CoopArgs ca;
   ca.ctl = reinterpret_cast<uint32_t*>(w);
   w += align256((size_t)kCoCtlWords * 4);
   ca.rec = reinterpret_cast<u32x4*>(w);
   ca.maxg = coop_max_groups(G);
-  // MHC_PRE_FWD_COOP_TIMEOUT (s_memrealtime ticks, 100 MHz) shortens the
-  // bounded waits: the tests set it to 0 to force the failure path (every
-  // wait that is not already satisfied gives up at once, the status word is
-  // set and the outputs become NaN)
-  ca.timeout = kCoTimeout;
-  if (const char* env = getenv("MHC_PRE_FWD_COOP_TIMEOUT")) ca.timeout = strtoull(env, nullptr, 10);
+  ca.timeout = coop_wait_limit();
   const size_t rec_bytes = align256((size_t)ca.maxg * kCoR * G * kCoRecWords * 16);
   w += rec_bytes;
   a.part = reinterpret_cast<float*>(w);
@@ -852,12 +868,8 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   hipLaunchKernelGGL(co_zero_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(ca.ctl), words);
   int rc = check_launch("pre_fwd_coop_zero");
   if (rc) return rc;
-  void* args[] = {&ca};
-  const hipError_t e = hipLaunchCooperativeKernel(kfn, dim3((unsigned)device_cu_count()), dim3(threads), args, 0, st);
-  if (e != hipSuccess) {  // not co-resident after all: the caller runs the two-pass forms
-    (void)hipGetLastError();
-    return MHC_OK;
-  }
+  hipLaunchKernelGGL((pre_fwd_coop_kernel<32, XS>), dim3((unsigned)device_cu_count()), dim3(threads), 0, st, ca);
+  if ((rc = check_launch("pre_fwd_coop"))) return rc;
   *used = true;
   a.co_status = ca.ctl + kCtlStatus;  // a timed-out wait turns every output of the call into NaN
   hipLaunchKernelGGL((pre_fwd_finalize_kernel<4>), dim3((unsigned)((a.T + 15) / 16)), dim3(kFwdThreads), 0, st, a, 1);

@@ -116,6 +116,37 @@ int mhc_pre_fwd(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dty
                 int32_t D, void* stream);
 
 /*
+ * mhc_pre_fwd with a status word.  The single-pass form's waits for the other
+ * CUs of its group are bounded (0.25 s without progress); if one gives up
+ * (the GPU was preempted or shared for that long), every output of the call
+ * is NaN, and the kernels write the failure code (> 0) to *status, or 0 when
+ * every wait was satisfied.  Other forms have no such waits and leave *status
+ * untouched, so the caller zeroes it first.  `status` may be a device pointer
+ * or host-mapped pinned memory (hipHostMalloc); it is written when the call's
+ * work runs, so the caller reads it after synchronising with `stream`.
+ * mhc_pre_fwd is this call with status == NULL: it returns MHC_OK before the
+ * kernels run and cannot report such a failure.  No counterpart in the
+ * reference (its Triton kernels have no cross-CU waits; its failures are
+ * host exceptions, src/mhc_pre_clamp_sinkhorn.py:884-889).  Other arguments
+ * as in mhc_pre_fwd.
+ */
+int mhc_pre_fwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
+                   const float* alpha, const float* base, float norm_eps, float hc_eps,
+                   float clamp_min, float clamp_max, int32_t iter_times, void* y, float* post_out,
+                   float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits, float* pre,
+                   float* x_scaled, void* workspace, size_t workspace_bytes, int32_t* status,
+                   int64_t T, int32_t N, int32_t D, void* stream);
+
+/*
+ * Test hook, no counterpart in the reference: sets the limit of the
+ * single-pass form's bounded waits to `ticks` of the GPU's 100 MHz clock for
+ * every later call in this process (0 makes every wait that is not already
+ * satisfied give up at once, which forces the failure path above); a
+ * negative value restores the default (0.25 s).  Nothing else sets it.
+ */
+void mhc_debug_set_wait_limit(int64_t ticks);
+
+/*
  * mhc_pre_fwd without a workspace argument.  No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  It calls

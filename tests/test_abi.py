@@ -137,8 +137,9 @@ def test_ops_refuse_cpu_tensors():
 
 def test_public_api_names():
     """The reference's twelve names (src/__init__.py:34-47) come first and
-    unchanged; the additions are the fused post+pre operator and the post
-    backward for a gradient given as two summands."""
+    unchanged; the additions are the fused post+pre operator, the post
+    backward for a gradient given as two summands and the single-pass
+    forward's failure check."""
     import FlagOS_mhc as m
     assert m.__all__[:12] == [
         "mhc_post", "mhc_post_ref", "mhc_post_backward", "mhc_post_backward_ref",
@@ -148,7 +149,7 @@ def test_public_api_names():
     ]
     assert m.__all__[12:] == [
         "mhc_post_pre_clamp_sinkhorn", "MhcPostPreClampSinkhornFn", "mhc_post_pre_clamp_sinkhorn_fn",
-        "mhc_post_backward_sum",
+        "mhc_post_backward_sum", "check_errors",
     ]
     for name in m.__all__:
         assert callable(getattr(m, name))

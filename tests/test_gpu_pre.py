@@ -181,14 +181,17 @@ BWD_CASES = [
     (17, 4, 40000, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     # few column blocks: many more token splits of the grad_phi partials
     (4000, 4, 256, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
-    # N = 4 at T >= 16384 takes grad_pre from a wave per token in kernel A;
-    # smaller T and every N = 8 call from the split (token, 2048-column)
-    # partials, whose grid holds at most 65536 token blocks (70001 tokens:
-    # blocks loop over several tokens)
+    # grad_pre: bf16 rows with 16-byte alignment at T >= 16384 (N = 4 and 8)
+    # take the LDS-pipelined pre_bwd_gpre_dma_kernel (70001 x 8 x 64); N = 4
+    # in other dtypes at T >= 16384 a wave per token in kernel A; everything
+    # else the split (token, 2048-column) partials of pre_bwd_gpre_kernel,
+    # whose grid holds at most 65536 token blocks, so at 70001 tokens with
+    # unaligned rows (D = 60) its blocks loop over several tokens
     (3, 4, 7168, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     (4, 8, 100, torch.float32, torch.float32, "baseline", 10.0, 20),
     (5, 4, 4100, torch.float16, torch.float16, "baseline", 10.0, 20),
     (70001, 8, 64, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
+    (70001, 8, 60, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),
     # N = 8 grad_x kernel with two waves per stream (64-column halves): a
     # last column block whose second half is partly past D, a ragged last tile
     (1000, 8, 1000, torch.bfloat16, torch.bfloat16, "baseline", 10.0, 20),

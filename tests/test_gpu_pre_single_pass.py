@@ -11,8 +11,11 @@ Checked against
   * itself: a second call is bit-identical (fixed reduction order), and so
     is mhc_pre_fwd_noalloc, whose 64 MiB scratch has room for the ring.
 The control words at the start of the workspace's single-pass region show
-that the path ran (every block registered) and that no bounded wait timed
-out (status 0)."""
+that the path ran (every block registered), and the status word of
+mhc_pre_fwd_ex (pinned host memory the kernels write) that no bounded wait
+timed out (status 0).  A forced timeout (the waits' limit set to zero through
+the mhc_debug_set_wait_limit test hook) must surface as a nonzero status and
+as a RuntimeError from the package's operators."""
 
 from __future__ import annotations
 
@@ -27,6 +30,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 CTL = 256          # byte offset of the single-pass control words in the workspace
 ARRIVED, STATUS = 16, 17
+STATUS_OUT = 63    # (test only) where _run puts mhc_pre_fwd_ex's status word
 
 
 def _inputs(T, N, D, seed):
@@ -58,6 +62,7 @@ def _run(mode, x, phi, alpha, base, xs, clamp=10.0, iters=20):
             -clamp, clamp, iters) + tuple(_lib.ptr(o[k]) for k in o)
     stream = torch.cuda.current_stream().cuda_stream
     ws = None
+    status = torch.full((1,), -7, dtype=torch.int32, pin_memory=True)  # the kernels overwrite it
     if mode == "noalloc":
         rc = lib.mhc_pre_fwd_noalloc(*head, T, N, D, stream)
     else:
@@ -65,10 +70,13 @@ def _run(mode, x, phi, alpha, base, xs, clamp=10.0, iters=20):
         if mode == "two-pass":
             assert TWO_PASS_WS < full  # the single-pass form would need more
         ws = torch.zeros(full if mode == "full" else TWO_PASS_WS, dtype=torch.uint8, device=DEV)
-        rc = lib.mhc_pre_fwd(*head, ws.data_ptr(), ws.numel(), T, N, D, stream)
+        rc = lib.mhc_pre_fwd_ex(*head, ws.data_ptr(), ws.numel(), status.data_ptr(), T, N, D, stream)
     _lib.check(rc, mode)
     torch.cuda.synchronize()
     ctl = ws[CTL:CTL + 256].view(torch.int32).cpu().numpy() if ws is not None else None
+    if ctl is not None:
+        ctl = ctl.copy()
+        ctl[STATUS_OUT] = int(status[0])  # the caller's copy of the status word
     return o, ctl
 
 
@@ -90,7 +98,9 @@ def test_single_pass_matches_two_pass_and_oracle(T, D, xs):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     assert ctl[ARRIVED] == cus, f"single-pass path did not run: {ctl[ARRIVED]} of {cus} blocks registered"
     assert ctl[STATUS] == 0, f"a bounded wait timed out (status {ctl[STATUS]})"
-    tp, _ = _run("two-pass", x, phi, alpha, base, xs)
+    assert ctl[STATUS_OUT] == 0, "the caller's status word was not written"
+    tp, ctl_tp = _run("two-pass", x, phi, alpha, base, xs)
+    assert ctl_tp[STATUS_OUT] == -7, "the two-pass forms leave the status word alone"
     # two-pass vs single-pass: fp32 sums in other orders
     for k, atol, rtol in (("mixes", 2e-4, 1e-4), ("inv_rms", 0.0, 2e-5), ("pre", 1e-5, 1e-5),
                           ("post_out", 1e-5, 1e-5), ("comb_frag", 1e-5, 1e-5), ("h_res_logits", 2e-4, 1e-4)):
@@ -136,23 +146,52 @@ def test_two_pass_workspace_is_not_the_single_pass():
     assert torch.allclose(sp["mixes"], tp["mixes"], rtol=1e-4, atol=2e-4)
 
 
-def test_single_pass_failure_is_loud(monkeypatch):
+def test_single_pass_failure_is_loud():
     """With the waits' limit forced to zero ticks from the host (the
-    MHC_PRE_FWD_COOP_TIMEOUT hook), the single-pass kernel gives up at its
-    first unsatisfied wait and every kernel still exits; the status word is
-    set and every output of the call is NaN, never silently wrong.  The next
-    call with the normal limit is correct again."""
+    mhc_debug_set_wait_limit test hook), the single-pass kernel gives up at
+    its first unsatisfied wait and every kernel still exits: the status word
+    is set, every output of the call is NaN, never silently wrong, and the
+    package's operators raise RuntimeError (check_errors, the next forward,
+    and the backward of an autograd forward that failed).  With the normal
+    limit restored the next call is correct again."""
+    import FlagOS_mhc as m
+
     T, N, D = 8192, 4, 7168
     x, phi, alpha, base = _inputs(T, N, D, seed=9)
+    lib = _lib.load()
     good, ctl = _run("full", x, phi, alpha, base, True)
-    assert ctl[STATUS] == 0
-    monkeypatch.setenv("MHC_PRE_FWD_COOP_TIMEOUT", "0")
-    bad, ctl_bad = _run("full", x, phi, alpha, base, True)
-    assert ctl_bad[STATUS] != 0
-    for k, v in bad.items():
-        assert bool(torch.isnan(v.float()).all()), k
-    monkeypatch.delenv("MHC_PRE_FWD_COOP_TIMEOUT")
+    assert ctl[STATUS] == 0 and ctl[STATUS_OUT] == 0
+    m.check_errors()  # nothing pending that failed
+    try:
+        lib.mhc_debug_set_wait_limit(0)
+        bad, ctl_bad = _run("full", x, phi, alpha, base, True)
+        assert ctl_bad[STATUS] != 0
+        assert ctl_bad[STATUS_OUT] == ctl_bad[STATUS], "the caller's status word carries the failure"
+        for k, v in bad.items():
+            assert bool(torch.isnan(v.float()).all()), k
+        # the package: the call itself returns (its kernels have not run yet) ...
+        out = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, clamp_min=-10.0, clamp_max=10.0)
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(out["y"].float()).all())
+        # ... and the failure is raised at the next check
+        with pytest.raises(RuntimeError, match="bounded wait"):
+            m.check_errors()
+        m.check_errors()  # reported once
+        # the next forward raises for an earlier failed call whose work has finished
+        m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, clamp_min=-10.0, clamp_max=10.0)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="bounded wait"):
+            m.mhc_pre_clamp_sinkhorn(x[:64], phi, alpha, base)
+        # the backward of a failed autograd forward raises instead of propagating NaN
+        xg = x.clone().requires_grad_(True)
+        y, po, cf = m.mhc_pre_clamp_sinkhorn_fn(xg, phi, alpha, base, clamp_min=-10.0, clamp_max=10.0)
+        with pytest.raises(RuntimeError, match="bounded wait"):
+            (y.float().sum() + po.sum() + cf.sum()).backward()
+    finally:
+        lib.mhc_debug_set_wait_limit(-1)
+        torch.cuda.synchronize()
+    m.check_errors()
     again, ctl2 = _run("full", x, phi, alpha, base, True)
-    assert ctl2[STATUS] == 0
+    assert ctl2[STATUS] == 0 and ctl2[STATUS_OUT] == 0
     for k in good:
         assert torch.equal(good[k], again[k]), k
