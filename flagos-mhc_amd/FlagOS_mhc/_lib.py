@@ -18,7 +18,9 @@ _LIB_NAME = "libmhc_amd.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-PRE_BWD_COMPENSATED = 1  # mhc_pre_bwd_ex flag (include/mhc_amd.h)
+PRE_BWD_COMPENSATED = 1  # mhc_pre_bwd_ex flags (include/mhc_amd.h)
+PRE_BWD_TWO_PASS = 2
+PRE_BWD_SINGLE_PASS = 4
 
 _c = ctypes
 _vp, _i32, _i64, _f32, _sz = _c.c_void_p, _c.c_int32, _c.c_int64, _c.c_float, _c.c_size_t
@@ -47,7 +49,7 @@ _SIGNATURES = {
                                    _i64, _i32, _i32, _vp]),
     "mhc_pre_bwd_ex": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _f32, _f32, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _c.c_uint32, _vp,
-                                  _sz, _i64, _i32, _i32, _vp]),
+                                  _vp, _sz, _i64, _i32, _i32, _vp]),
     "mhc_post_pre_fwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "mhc_post_pre_fwd": (_c.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
                                     _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
@@ -121,11 +123,12 @@ def dtype_code(what: str, dt: torch.dtype) -> int:
 
 
 class SinglePassStatus:
-    """Where the single-pass pre forward reports its bounded waits.
+    """Where the single-pass pre forward and backward report their bounded waits.
 
-    That kernel waits for the other CUs of its group with a limit (0.25 s
+    Those kernels wait for the other CUs of their group with a limit (0.25 s
     without progress); if a wait gives up, the call's outputs are NaN and the
-    kernels write a failure code to the status word of ``mhc_pre_fwd_ex``.
+    kernels write a failure code to the status word of ``mhc_pre_fwd_ex`` /
+    ``mhc_pre_bwd_ex``.
     Each call gets a word in a ring of pinned host memory (written by the GPU
     with a system-scope store, read by the host once the call's event has
     completed), so no call waits for the GPU.  ``check`` raises for a failed
@@ -177,17 +180,17 @@ class SinglePassStatus:
                 code = int(self._words[slot])
                 if code:
                     raise RuntimeError(
-                        f"mhc_pre_clamp_sinkhorn: an earlier single-pass forward call gave up a "
-                        f"bounded wait for the other CUs of its group (status {code}: the GPU stalled "
-                        "longer than the wait limit); that call's outputs are NaN")
+                        f"mhc_pre_clamp_sinkhorn: an earlier single-pass forward or backward call gave "
+                        f"up a bounded wait for the other CUs of its group (status {code}: the GPU "
+                        "stalled longer than the wait limit); that call's outputs are NaN")
 
 
 SINGLE_PASS = SinglePassStatus()
 
 
 def check_errors(block: bool = True) -> None:
-    """Raise RuntimeError if an earlier single-pass pre forward gave up a
-    bounded wait (its outputs are then NaN).  With ``block`` (the default)
+    """Raise RuntimeError if an earlier single-pass pre forward or backward
+    gave up a bounded wait (its outputs are then NaN).  With ``block`` (the default)
     wait for every such call's work to finish first; without it, look only
     at calls that have finished."""
     SINGLE_PASS.check(block)

@@ -27,7 +27,7 @@ import torch
 from . import _lib
 
 SUPPORTED_N = (4, 8)
-SINGLE_PASS_MIN_T = 8192  # fewest tokens the single-pass form takes (csrc/pre_fwd_coop.hpp)
+SINGLE_PASS_MIN_T = 8192  # fewest tokens the single-pass forms take (csrc/pre_fwd_coop.hpp, pre_bwd_coop.hpp)
 
 
 def _flatten(x):

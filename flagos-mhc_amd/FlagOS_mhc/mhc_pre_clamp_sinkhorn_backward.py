@@ -30,7 +30,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .mhc_pre_clamp_sinkhorn import SUPPORTED_N, _flatten
+from .mhc_pre_clamp_sinkhorn import SINGLE_PASS_MIN_T, SUPPORTED_N, _flatten
 
 
 def mhc_pre_clamp_sinkhorn_backward(
@@ -65,11 +65,14 @@ def mhc_pre_clamp_sinkhorn_backward(
 
 def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out, grad_comb_frag,
                   norm_eps, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in=None,
-                  compensated=False):
-    """mhc_pre_clamp_sinkhorn_backward; with ``grad_x_in`` (shaped and typed
-    like x) the returned grad_x is grad_x_in + dL/dx, accumulated inside the
-    kernel (``mhc_pre_bwd_acc``); ``compensated`` selects the compensated
-    T-reductions (``mhc_pre_bwd_ex``)."""
+                  compensated=False, single_pass=None):
+    """mhc_pre_clamp_sinkhorn_backward (``mhc_pre_bwd_ex``); with ``grad_x_in``
+    (shaped and typed like x) the returned grad_x is grad_x_in + dL/dx,
+    accumulated inside the kernel; ``compensated`` selects the compensated
+    T-reductions.  ``single_pass``: None lets the library choose (the
+    single-pass form from T >= 32768 where it applies), False keeps the
+    two-pass forms, True takes the single-pass form wherever it applies (from
+    T >= 8192)."""
     del norm_eps  # folded into inv_rms
     _lib.require_device("mhc_pre_clamp_sinkhorn_backward", x, phi, alpha, base, inv_rms, mixes,
                         pre, grad_y, grad_post_out, grad_comb_frag, grad_x_in)
@@ -117,18 +120,25 @@ def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_ou
               inv_c.data_ptr(), mixes_c.data_ptr(), pre_c.data_ptr(), gy.data_ptr(),
               gpost.data_ptr(), gcomb.data_ptr(), float(hc_eps), float(clamp_min),
               float(clamp_max), int(iter_times))
-    tail = (grad_x.data_ptr(), grad_phi.data_ptr(), grad_alpha.data_ptr(), grad_base.data_ptr(),
-            ws.data_ptr(), ws_bytes, T, N, D, _lib.stream_of(xf))
     gin = None if grad_x_in is None else grad_x_in.reshape(T, N * D).to(xf.dtype).contiguous()
+    flags = _lib.PRE_BWD_COMPENSATED if compensated else 0
+    if single_pass is not None:
+        flags |= _lib.PRE_BWD_SINGLE_PASS if single_pass else _lib.PRE_BWD_TWO_PASS
+    # the shapes the single-pass form can take (N = 4, bf16, T >= 8192, no
+    # grad_x_in, not compensated; never under stream capture) report its
+    # bounded waits into a status word
+    slot = status = None
+    if (single_pass is not False and N == 4 and T >= SINGLE_PASS_MIN_T and xf.dtype == torch.bfloat16
+            and phi_c.dtype == torch.bfloat16 and gin is None and not compensated
+            and not torch.cuda.is_current_stream_capturing()):
+        slot, status = _lib.SINGLE_PASS.acquire()
     with torch.cuda.device(dev):
-        if compensated:
-            rc = lib.mhc_pre_bwd_ex(*common, _lib.ptr(gin), *tail[:4], _lib.PRE_BWD_COMPENSATED,
-                                    *tail[4:])
-        elif gin is None:
-            rc = lib.mhc_pre_bwd(*common, *tail)
-        else:
-            rc = lib.mhc_pre_bwd_acc(*common, gin.data_ptr(), *tail)
+        rc = lib.mhc_pre_bwd_ex(*common, _lib.ptr(gin), grad_x.data_ptr(), grad_phi.data_ptr(),
+                                grad_alpha.data_ptr(), grad_base.data_ptr(), flags, status,
+                                ws.data_ptr(), ws_bytes, T, N, D, _lib.stream_of(xf))
     _lib.check(rc, "mhc_pre_clamp_sinkhorn_backward")
+    if slot is not None:
+        _lib.SINGLE_PASS.commit(slot, torch.cuda.current_stream(dev))
     return grad_x.view(*shape), grad_phi.reshape(phi.shape), grad_alpha, grad_base
 
 

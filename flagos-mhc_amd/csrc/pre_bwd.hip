@@ -66,6 +66,7 @@ struct PreBwdSmallArgs {
   const float* gpre_part;  // [T][gpre_chunks][N] grad_pre partials, or null
   int gpre_chunks;
   float* gpre_buf;         // the workspace's partials region (host side: the LDS-pipelined grad_pre)
+  float* coefX;            // single-pass form (N = 4): (T, 16) per-token records, see below
   int comp;                // compensated (Neumaier) sums of the block partials
   int64_t T;
   int D;
@@ -237,8 +238,17 @@ __global__ __launch_bounds__(kWave * kGpreDmaWaves) void pre_bwd_gpre_dma_kernel
   }
 }
 
-template <int N, typename S, bool VEC>
+// SP (the single-pass backward, pre_bwd_coop.hpp): grad_pre is not known
+// yet, so the pre head's part of grad_mixes is left to the single-pass
+// kernel: grad_mixes[t, n < N] and its terms of scale, grad_alpha[0] and
+// grad_base[n < N] are zero here, and coefX[t] = {pre[0..3],
+// sp(1 - sp)[0..3] (sp = sigmoid(mixes[n] * alpha[0] + base[n])),
+// mixes[0..3], inv_rms, scale without the pre head, 0, 0} carries what the
+// single-pass kernel needs to add them (grad_mixes[t, n] = grad_pre[t, n] *
+// alpha[0] * sp(1 - sp)).
+template <int N, typename S, bool VEC, bool SP = false>
 __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallArgs a) {
+  static_assert(!SP || N == 4, "single-pass records hold four streams");
   using PD = PreDims<N>;
   constexpr int M = PD::M, L = N * N, C = 3 + M;
   __shared__ float gp_sh[kBwdTile][N];
@@ -253,7 +263,9 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
   const int64_t t0 = (int64_t)blockIdx.x * kBwdTile;
 
   // ---- grad_pre: summed from the split kernel's partials, or a wave per token
-  if (a.gpre_part) {
+  if constexpr (SP) {
+    if (tid < kBwdTile * N) gp_sh[tid / N][tid % N] = 0.f;
+  } else if (a.gpre_part) {
     if (tid < kBwdTile * N) {
       const int tt = tid / N, n = tid % N;
       const int64_t tok = t0 + tt;
@@ -327,6 +339,13 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
         const float sp = sigmoidf_(mh * a0 + a.base[e]);
         dz = gp_sh[tt][e] * sp * (1.0f - sp);
         gmh = dz * a0;
+        if constexpr (SP) {
+          if (ok) {
+            a.coefX[tok * 16 + e] = a.pre[tok * N + e];
+            a.coefX[tok * 16 + 4 + e] = sp * (1.0f - sp);
+            a.coefX[tok * 16 + 8 + e] = mh;
+          }
+        }
       } else {
         const float so = sigmoidf_(mh * a1 + a.base[e]);
         const float gpo = ok ? a.gpost[tok * N + (e - N)] : 0.f;
@@ -386,6 +405,9 @@ __global__ __launch_bounds__(kBwdThreads) void pre_bwd_small_kernel(PreBwdSmallA
     const float c2 = group_sum<L - 1>(dlc * ml);
     const float scale = -inv * inv * sdot / (float)K;
     if (ok && a.coef && e < N) a.coef[tok * N + e] = float4{a.pre[tok * N + e], inv, scale, 0.f};
+    if constexpr (SP) {
+      if (ok && e == 0) *reinterpret_cast<float4*>(a.coefX + tok * 16 + 12) = float4{inv, scale, 0.f, 0.f};
+    }
     if (e == 0) {
       if (ok && a.scale) a.scale[tok] = scale;
       contrib[tt][0] = c0;
@@ -721,7 +743,7 @@ __global__ __launch_bounds__(64 * N) void pre_bwd_stream_kernel(PreBwdStreamArgs
   using PD = PreDims<N>;
   using Tile = StreamTile<N>;
   typedef typename Tile::Row Row;
-  constexpr int M = PD::M, MT = PD::MT, MP = PD::MP, MK = PD::MK, MP32 = PD::MP32;
+  constexpr int M = PD::M, MT = PD::MT, MK = PD::MK, MP32 = PD::MP32;
   constexpr int VC = StreamCfg<N>::VC, DW = StreamCfg<N>::DW, VD = VC / 2;
   constexpr int TT = kStreamTile;
 
@@ -1639,10 +1661,13 @@ __global__ void sum_splits_comp_kernel(const float* __restrict__ part, float* __
 // comp: each thread sums its rows with Neumaier's compensation, then the 256
 // (sum, compensation) pairs are added pairwise with the exact error of each
 // addition (TwoSum) carried into the compensation.
+// status (may be null): the single-pass kernel's status word; nonzero (a
+// timed-out wait) makes the outputs NaN.
 __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ partial,
                                                        int64_t rows, int C,
                                                        float* __restrict__ out_alpha,
-                                                       float* __restrict__ out_base, int comp) {
+                                                       float* __restrict__ out_base, int comp,
+                                                       const uint32_t* status) {
   __shared__ float red[256], redc[256];
   const int c = blockIdx.x;
   float s = 0.f, cc = 0.f;
@@ -1667,12 +1692,25 @@ __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__
     __syncthreads();
   }
   if (threadIdx.x == 0 && comp) red[0] += redc[0];
+  if (threadIdx.x == 0 && status && *status) red[0] = __builtin_nanf("");
   if (threadIdx.x == 0) {
     if (c < 3)
       out_alpha[c] = red[0];
     else
       out_base[c - 3] = red[0];
   }
+}
+
+}  // namespace mhc
+
+#include "pre_bwd_coop.hpp"
+
+namespace mhc {
+
+__global__ void zero_kernel(float* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -1683,7 +1721,22 @@ struct BwdLayout {
   int64_t K, nblkA, tok_per_split, ntiles;
   size_t off_phiT, off_gm, off_scale, off_partial, off_gphi, off_sink, off_gpre, off_gpl;
   size_t off_gmP, off_gTw, off_coef, total;
+  // single-pass form (0 when it cannot apply): G members per group, control
+  // words + exchange ring, contribution rows after kernel A's
+  int bcG, bcMaxg;
+  int64_t bc_rows;
+  size_t off_bc_ctl, bc_ring_bytes;
 };
+
+// The single-pass backward: N = 4, bf16 phi, a slice geometry for D and
+// at least kBcMinT tokens (MHC_PRE_BWD_SINGLE_PASS), kBcAutoT without a pass
+// flag.  Measured on MI355X (bf16, D = 7168 unless noted, backward ms,
+// single / two-pass): T = 8192 0.343 / 0.306, T = 16384 at D = 4096 0.346 /
+// 0.340, T = 65536 2.30 / 2.43.
+constexpr int64_t kBcMinT = 8192, kBcAutoT = 32768;
+inline bool bc_shape(int64_t T, int N, int D, int32_t phi_dtype, int* G) {
+  return N == 4 && phi_dtype == MHC_DTYPE_BF16 && T >= kBcMinT && coop_nch(D, G);
+}
 
 // Token splits of the grad_phi partials: kMaxSplits for the split kernels,
 // more for the LDS-pipelined kernel when D has few 128-column blocks.
@@ -1736,8 +1789,16 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   off += align256((size_t)T * b.M * 4);
   b.off_scale = off;
   off += align256((size_t)T * 4);
+  b.bcG = 0;
+  if (bc_shape(T, N, D, phi_dtype, &b.bcG)) {
+    b.bcMaxg = coop_max_groups(b.bcG);
+    b.bc_rows = device_cu_count();
+  } else {
+    b.bcG = b.bcMaxg = 0;
+    b.bc_rows = 0;
+  }
   b.off_partial = off;
-  off += align256((size_t)b.nblkA * b.C * 4);
+  off += align256((size_t)(b.nblkA + b.bc_rows) * b.C * 4);
   b.off_gphi = off;
   off += align256((size_t)dma_max_splits(D) * b.M * b.K * 4);  // grad_phi split partials
   b.off_gmP = off;
@@ -1757,6 +1818,9 @@ static BwdLayout bwd_layout(int64_t T, int N, int D, int32_t phi_dtype, int iter
   off += align256((size_t)T * (b.gpre_chunks > 0 ? b.gpre_chunks : 1) * N * 4);
   b.off_gpl = off;  // compensated mode: g planes, 3 bf16 per (token, padded m)
   off += align256((size_t)((T + kCompTile - 1) / kCompTile) * kCompTile * b.MP * kCompPlanesG * 2);
+  b.off_bc_ctl = off;  // control words, then the exchange ring (contiguous: zeroed together)
+  b.bc_ring_bytes = b.bcG ? (size_t)b.bcMaxg * kBcR * b.bcG * kBcRecWords * 16 : 0;
+  if (b.bcG) off += align256((size_t)kCoCtlWords * 4) + align256(b.bc_ring_bytes);
   b.total = off;
   return b;
 }
@@ -1792,9 +1856,10 @@ static unsigned reduce_grid(int64_t n) {
 }
 
 static int sum_alpha_base(const BwdLayout& lay, const PreBwdSmallArgs& sa, float* grad_alpha,
-                          float* grad_base, hipStream_t st) {
+                          float* grad_base, hipStream_t st, int64_t extra_rows = 0,
+                          const uint32_t* status = nullptr) {
   hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)lay.C), dim3(256), 0, st, sa.partial,
-                     lay.nblkA, lay.C, grad_alpha, grad_base, sa.comp);
+                     lay.nblkA + extra_rows, lay.C, grad_alpha, grad_base, sa.comp, status);
   return check_launch("pre_bwd_sum_rows");
 }
 
@@ -1916,12 +1981,81 @@ static int add_into(void* out, const void* in, int64_t n, hipStream_t st) {
   return check_launch("pre_bwd_add_into");
 }
 
+// The single-pass form (pre_bwd_coop.hpp) where it applies: kernel A's SP
+// form, the single-pass kernel, then grad_phi and grad_alpha / grad_base in
+// fixed order.  *used says whether it ran.
+static int launch_pre_bwd_coop(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwdStreamArgs& sta,
+                               float* grad_phi, float* grad_alpha, float* grad_base, char* ws,
+                               int32_t* status_out, hipStream_t st, bool* used) {
+  *used = false;
+  if (!lay.bcG || stream_capturing(st)) return MHC_OK;
+  if (!coop_fits((const void*)pre_bwd_coop_kernel, kBcThreads, 1)) return MHC_OK;
+  const int grid = device_cu_count();
+  if ((int64_t)lay.bcMaxg * lay.bcG > lay.bc_rows) return MHC_OK;  // a contribution row per member
+  uint32_t* ctl = reinterpret_cast<uint32_t*>(ws + lay.off_bc_ctl);
+  u32x4* ring = reinterpret_cast<u32x4*>(ws + lay.off_bc_ctl + align256((size_t)kCoCtlWords * 4));
+  const int64_t words = (int64_t)((align256((size_t)kCoCtlWords * 4) + lay.bc_ring_bytes) / 16);
+  hipLaunchKernelGGL(co_zero_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<u32x4*>(ctl), words);
+  int rc = check_launch("pre_bwd_coop_zero");
+  if (rc) return rc;
+  // the members' contribution rows (group * G + member; rows of groups that
+  // do not form stay zero)
+  hipLaunchKernelGGL(zero_kernel, dim3(32), dim3(256), 0, st, sa.partial + lay.nblkA * lay.C, lay.bc_rows * lay.C);
+  if ((rc = check_launch("pre_bwd_coop_zero_rows"))) return rc;
+  // kernel A without the pre head: grad_mixes rows (fp32) and coefX
+  sa.gmP = nullptr;
+  sa.gTw = nullptr;
+  sa.coef = nullptr;
+  sa.scale = nullptr;
+  sa.gpre_part = nullptr;
+  sa.coefX = reinterpret_cast<float*>(ws + lay.off_coef);
+  hipLaunchKernelGGL((pre_bwd_small_kernel<4, bf16_t, true, true>), dim3((unsigned)lay.nblkA), dim3(kBwdThreads), 0,
+                     st, sa);
+  if ((rc = check_launch("pre_bwd_small_sp"))) return rc;
+  BwdCoopArgs ca{};
+  ca.x = sta.x;
+  ca.gy = sta.gy;
+  ca.gx = sta.gx;
+  ca.phiT = sta.phiT;
+  ca.gm = sa.gm;
+  ca.coefX = sa.coefX;
+  ca.alpha = sa.alpha;
+  ca.part = sta.gphi_part;
+  ca.contrib = sa.partial + lay.nblkA * lay.C;
+  ca.ctl = ctl;
+  ca.rec = ring;
+  ca.T = sa.T;
+  ca.D = sa.D;
+  ca.G = lay.bcG;
+  ca.maxg = lay.bcMaxg;
+  ca.timeout = coop_wait_limit();
+  hipLaunchKernelGGL(pre_bwd_coop_kernel, dim3((unsigned)grid), dim3(kBcThreads), 0, st, ca);
+  if ((rc = check_launch("pre_bwd_coop"))) return rc;
+  *used = true;
+  const int64_t n = (int64_t)lay.M * lay.K;
+  hipLaunchKernelGGL(bc_sum_kernel, dim3(reduce_grid(n)), dim3(256), 0, st, sta.gphi_part, grad_phi, n, ctl, sta.gx,
+                     sa.T * lay.K, status_out);
+  if ((rc = check_launch("pre_bwd_coop_sum"))) return rc;
+  return sum_alpha_base(lay, sa, grad_alpha, grad_base, st, lay.bc_rows, ctl + kCtlStatus);
+}
+
 template <int N, typename S>
 static int launch_pre_bwd(const BwdLayout& lay, PreBwdSmallArgs sa, const PreBwdMainArgs& ma,
                           PreBwdStreamArgs sta, float* grad_phi, float* grad_alpha,
-                          float* grad_base, bool vec, const void* gin, uint16_t* gpl, hipStream_t st) {
+                          float* grad_base, bool vec, const void* gin, uint16_t* gpl, hipStream_t st,
+                          char* ws, int sp_mode, int32_t* status_out) {
   const dim3 gA((unsigned)lay.nblkA), bA(kBwdThreads);
   const bool streaming = vec && std::is_same<S, bf16_t>::value;
+  if constexpr (N == 4 && std::is_same<S, bf16_t>::value) {
+    // sp_mode: 0 never, 1 from kBcAutoT tokens, 2 from kBcMinT (the layout's
+    // condition)
+    const bool single_pass = sp_mode == 2 || (sp_mode == 1 && sa.T >= kBcAutoT);
+    if (single_pass && streaming && !gin && !sa.comp && lay.P == 1 && dma_usable<N>(sta.D)) {
+      bool used = false;
+      const int rc = launch_pre_bwd_coop(lay, sa, sta, grad_phi, grad_alpha, grad_base, ws, status_out, st, &used);
+      if (rc || used) return rc;
+    }
+  }
   if (streaming) {
     if (!sa.comp) sa.gm = nullptr;  // the compensated grad_phi reads fp32 grad_mixes
     sa.scale = nullptr;
@@ -1983,18 +2117,16 @@ template <typename S>
 static int dispatch_pre_bwd(int N, const BwdLayout& lay, const PreBwdSmallArgs& sa,
                             const PreBwdMainArgs& ma, const PreBwdStreamArgs& sta, float* gphi,
                             float* galpha, float* gbase, bool vec, const void* gin, uint16_t* gpl,
-                            hipStream_t st) {
+                            hipStream_t st, char* ws, int sp_mode, int32_t* status_out) {
   switch (N) {
-    case 4: return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, gpl, st);
-    case 8: return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, gpl, st);
+    case 4:
+      return launch_pre_bwd<4, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, gpl, st, ws, sp_mode,
+                                  status_out);
+    case 8:
+      return launch_pre_bwd<8, S>(lay, sa, ma, sta, gphi, galpha, gbase, vec, gin, gpl, st, ws, sp_mode,
+                                  status_out);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: N=%d not supported (4, 8)", N);
-}
-
-__global__ void zero_kernel(float* p, int64_t n) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0.f;
 }
 
 }  // namespace mhc
@@ -2013,10 +2145,12 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
                          const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
                          int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
                          float* grad_alpha, float* grad_base, void* workspace, size_t workspace_bytes,
-                         int64_t T, int32_t N, int32_t D, uint32_t flags, void* stream) {
+                         int64_t T, int32_t N, int32_t D, uint32_t flags, int32_t* status, void* stream) {
   clear_error();
-  if (flags & ~(uint32_t)MHC_PRE_BWD_COMPENSATED)
+  if (flags & ~(uint32_t)(MHC_PRE_BWD_COMPENSATED | MHC_PRE_BWD_TWO_PASS | MHC_PRE_BWD_SINGLE_PASS))
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: unknown flags 0x%x", (unsigned)flags);
+  if ((flags & MHC_PRE_BWD_TWO_PASS) && (flags & MHC_PRE_BWD_SINGLE_PASS))
+    return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: MHC_PRE_BWD_TWO_PASS and MHC_PRE_BWD_SINGLE_PASS together");
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_pre_bwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
   if (int rc = check_tokens(T, "mhc_pre_bwd")) return rc;
@@ -2108,13 +2242,17 @@ static int pre_bwd_entry(const void* x, int32_t x_dtype, const void* phi, int32_
   const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(grad_y) && aligned16(grad_x) &&
                    (!grad_x_in || aligned16(grad_x_in));
   uint16_t* gpl = reinterpret_cast<uint16_t*>(ws + lay.off_gpl);
+  const int sp = (flags & MHC_PRE_BWD_TWO_PASS) ? 0 : (flags & MHC_PRE_BWD_SINGLE_PASS) ? 2 : 1;
   switch (x_dtype) {
     case MHC_DTYPE_BF16:
-      return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st);
+      return dispatch_pre_bwd<bf16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st,
+                                      ws, sp, status);
     case MHC_DTYPE_F16:
-      return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st);
+      return dispatch_pre_bwd<f16_t>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st,
+                                     ws, sp, status);
     case MHC_DTYPE_F32:
-      return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st);
+      return dispatch_pre_bwd<float>(N, lay, sa, ma, sta, grad_phi, grad_alpha, grad_base, vec, grad_x_in, gpl, st,
+                                     ws, sp, status);
   }
   return set_error(MHC_ERR_UNSUPPORTED, "mhc_pre_bwd: x dtype %d not supported", x_dtype);
 }
@@ -2129,7 +2267,7 @@ extern "C" int mhc_pre_bwd(const void* x, int32_t x_dtype, const void* phi, int3
                            void* stream) {
   return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                        grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, nullptr, grad_x, grad_phi,
-                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, 0u, stream);
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, 0u, nullptr, stream);
 }
 
 // grad_x_in (nullable) must not overlap grad_x
@@ -2155,7 +2293,7 @@ extern "C" int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, 
   if (int rc = check_gin(grad_x_in, grad_x, T, N, D, x_dtype, "mhc_pre_bwd_acc")) return rc;
   return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                        grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in, grad_x, grad_phi,
-                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, 0u, stream);
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, 0u, nullptr, stream);
 }
 
 extern "C" int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
@@ -2163,11 +2301,12 @@ extern "C" int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, i
                               const float* pre, const void* grad_y, const float* grad_post_out,
                               const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
                               int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
-                              float* grad_alpha, float* grad_base, uint32_t flags, void* workspace,
-                              size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream) {
+                              float* grad_alpha, float* grad_base, uint32_t flags, int32_t* status,
+                              void* workspace, size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                              void* stream) {
   clear_error();
   if (int rc = check_gin(grad_x_in, grad_x, T, N, D, x_dtype, "mhc_pre_bwd_ex")) return rc;
   return pre_bwd_entry(x, x_dtype, phi, phi_dtype, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_out,
                        grad_comb_frag, hc_eps, clamp_min, clamp_max, iter_times, grad_x_in, grad_x, grad_phi,
-                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, flags, stream);
+                       grad_alpha, grad_base, workspace, workspace_bytes, T, N, D, flags, status, stream);
 }

@@ -1,0 +1,844 @@
+// mhc_pre_clamp_sinkhorn backward in one HBM pass over x and grad_y: N = 4,
+// bf16 x, grad_y and phi, D = 256 G with the forward's slice geometry
+// (coop_nch: G = 16 or 28 <= G <= 32).  Included by pre_bwd.hip.
+//
+// Semantics: torch autograd of mhc_pre_clamp_sinkhorn_ref, as the
+// reference's mhc_pre_clamp_sinkhorn_backward_ref
+// (src/mhc_pre_clamp_sinkhorn_backward.py:1397-1453).  The passes it replaces
+// are the reference's grad_pre pass (_y_bwd_kernel_hc4, :68-155) and its
+// rms-backward / combine pass (_fused_ybwd_rmsbwd_kernel, :217-341, with the
+// two torch.mm of :1372-1373), which read x and grad_y twice.
+//
+// Only the pre head's part of grad_mixes needs grad_pre[t, n] = <grad_y[t],
+// x[t, n]>, a reduction over the whole N*D row of a token:
+//   grad_mixes[t, n] = grad_pre[t, n] * alpha[0] * sp (1 - sp)  (n < 4)
+// the other 20 entries, the Sinkhorn / softmax / clamp and post-head VJPs,
+// come from kernel A (pre_bwd_small_kernel, SP form) before this kernel,
+// with the per-token record coefX (pre, sp (1 - sp), mixes[0..3], inv_rms,
+// the scale without the pre head).  Then
+//   grad_x[t, n, d] = grad_y[t, d] pre[t, n] + inv[t] gs[t, n, d] + scale[t] x[t, n, d]
+//   gs = grad_mixes @ phi,  scale = -inv^2 <grad_mixes, mixes> / (N D)
+//   grad_phi += (grad_mixes inv)^T @ x
+// all need that row reduction finished before a column of the row can be
+// written.  So, as in the single-pass forward, G CUs of one XCC form a group
+// that shares every 16-token tile: member c owns columns [256 c, 256 c + 256)
+// of the four streams (32 KB of x and 8 KB of grad_y per tile) and keeps them
+// on chip from their one HBM read until grad_x of those columns is written.
+//
+// A block (one per CU) has eight waves, wave w = n + 4 h owning stream n,
+// columns 128 h .. 128 h + 127 of the slice; lane (r, q) holds tokens
+// 4 q .. 4 q + 3 and columns 8 r .. 8 r + 7 of them (the lane layout of the
+// two-pass kernel B, pre_bwd_dma_kernel).  Per tile j:
+//   * waves 0..3 land tile j + 2's x and tile j + 2's grad_y / per-token data
+//     in LDS slots with direct-to-LDS loads (x: 3 slots of 32 KB; grad_y,
+//     grad_mixes rows and coefX: 4 slots of 11 KB);
+//   * phase 1, every wave: copy its x of tile j into a ring of three tiles of
+//     registers (freeing the x slot) and sum grad_y x over its 8 columns per
+//     token, then over the 16 lanes of a row (DPP); the tile's publisher wave
+//     adds the two halves per stream in order and stores the member's record
+//     (64 sums as 22 16-byte words (v, v, v, tag)) to the group's ring;
+//   * phase 2 of tile u = j - 2: the tile's poller wave (one of waves 4..7,
+//     polls issued a tile ahead) reads every member's record of tile u from
+//     L2 (direct-to-LDS loads), adds them in member order, and forms each
+//     token's grad_mixes[0..3], g = grad_mixes inv and scale in LDS; then
+//     every wave builds its MFMA operands from them and kernel A's rows,
+//     accumulates grad_phi (16x16x16, both bf16 planes of g) and gs
+//     (16x16x32) on the matrix cores and writes grad_x once.
+// The records are the only data that cross CUs (352 bytes per member and
+// tile), and they stay in the XCC's L2: tags (tile sequence + 1) carried in
+// every 16-byte word tell a reader that a word has arrived; a word is written
+// by one store and read by one load, so it never tears.  Each group writes
+// its own grad_phi partial [group][M][K]; the member that owns a tile (tile
+// sequence % G) adds the tile's grad_alpha[0] / grad_base[0..3] terms to its
+// row of contributions.  Both are summed in fixed order afterwards
+// (deterministic; no atomics on data).
+//
+// Memory-counter accounting.  Vector memory operations complete in issue
+// order.  Waves 0..3 issue the direct-to-LDS loads and their grad_x stores,
+// nothing else, and wait for a tile's loads with s_waitcnt vmcnt(n), n the
+// exact number of operations they issued after them.  Waves 4..7 issue their
+// grad_x stores, the records and the polls (direct-to-LDS, so no load
+// result is held in registers) and wait only for their polls, likewise by
+// exact count; the poll for tile u is issued before that wave's stores of
+// tile u - 1, so it completes without waiting for them.
+#pragma once
+
+#include "coop_common.hpp"
+
+namespace mhc {
+
+constexpr int kBcTT = 16;                 // tokens per tile
+constexpr int kBcWaves = 4;               // one per stream
+constexpr int kBcLag = 2;                 // phase 2 of tile j - 2 while tile j lands
+constexpr int kBcSx = 3;                  // x slots of 32 KB
+constexpr int kBcSg = 4;                  // grad_y / per-token slots of 11 KB
+constexpr int kBcGSlot = 11 * 1024;       // grad_y (8 KB) + coefX (1 KB) + grad_mixes rows (1.5 KB) + pad
+constexpr int kBcCoef = 8 * 1024;         // offset of coefX in a grad_y slot
+constexpr int kBcGm = 9 * 1024;           // offset of the grad_mixes rows [16][24] fp32
+constexpr int kBcRS = 2;                  // ready slots (per-token results of the exchange)
+constexpr int kBcR = 16;                  // exchange ring: tiles per group
+constexpr int kBcDataWords = 6;           // a record chunk: 16 sums (4 tokens x 4 streams) as (v, v, v, tag) words,
+constexpr int kBcChunkWords = 8;          // at a stride of 8 words (words 6, 7 never written or read)
+constexpr int kBcRecWords = 4 * kBcChunkWords;  // a member's record of a tile: 4 chunks
+constexpr int kBcPollKB = kCoMaxG * kBcChunkWords / 64;  // a wave's poll buffer, 1 KB units (4): 8 members each
+constexpr int kBcMaxGroups = kCoMaxGroups;
+constexpr int kBcThreads = kBcWaves * kWave;
+// status codes: the wait that timed out
+constexpr uint32_t kBcStLanded = 3, kBcStCopied = 4, kBcStPread = 5, kBcStPcnt = 6, kBcStPoll = 7,
+                   kBcStReady = 8, kBcStGdone = 9, kBcStRdone = 10;
+static_assert(kBcR >= 2 * kBcLag + 4, "exchange ring shorter than the skew it must cover");
+static_assert((kBcR & (kBcR - 1)) == 0 && (kBcSg & (kBcSg - 1)) == 0, "slot indices are masks");
+
+struct BwdCoopArgs {
+  const bf16_t* x;       // (T, 4, D)
+  const bf16_t* gy;      // (T, D)
+  bf16_t* gx;            // (T, 4, D)
+  const uint16_t* phiT;  // [K][32] bf16, m padded to 32 with zeros
+  const float* gm;       // (T, 24) grad_mixes without the pre head (kernel A, SP form)
+  const float* coefX;    // (T, 16) per-token records of kernel A
+  const float* alpha;
+  float* part;           // [maxg][24][K] grad_phi partial of each group
+  float* contrib;        // [maxg * G][27] grad_alpha / grad_base terms of each member (zeroed before the launch)
+  uint32_t* ctl;         // kCoCtlWords control words, zeroed before the launch
+  u32x4* rec;            // [maxg][kBcR][4 chunks][G][kBcChunkWords], zeroed before the launch
+  int64_t T;
+  int D;
+  int G;
+  int maxg;
+  uint64_t timeout;
+};
+
+// s_waitcnt vmcnt(BASE + KG * kg + pub) for wave-uniform kg in {2, 3} and
+// pub in {0, 1}: the steady-state counts of the main loop's two waits
+template <int BASE, int KG>
+__device__ __forceinline__ void bc_wait_steady(int kg, bool pub) {
+  static_assert(BASE + 3 * KG + 1 < 64, "vmcnt range");
+  if (kg == 3) {
+    if (pub)
+      wait_vmcnt<BASE + 3 * KG + 1>();
+    else
+      wait_vmcnt<BASE + 3 * KG>();
+  } else {
+    if (pub)
+      wait_vmcnt<BASE + 2 * KG + 1>();
+    else
+      wait_vmcnt<BASE + 2 * KG>();
+  }
+}
+
+__device__ __forceinline__ float bc_ld(uint32_t a) { return __uint_as_float(co_lds_ld(a)); }
+
+// An opaque copy of a wave-uniform value: what derives from it (LDS slot and
+// counter addresses) is recomputed where it is used, a scalar add, instead of
+// every derived value being kept live across the main loop, where the
+// scalar registers run out and the values go to VGPR lanes.
+__device__ __forceinline__ uint32_t bc_opq(uint32_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// c + a.lo b.lo + a.hi b.hi for two bf16 pairs (v_dot2c_f32_bf16: the bf16
+// products are exact in fp32)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// eight 16-byte reads at a + i * 16 * STRIDE (i = 0..7), complete on return
+template <int STRIDE>
+__device__ __forceinline__ void bc_rd8(u32x4 (&v)[8], uint32_t a) {
+  static_assert(7 * 16 * STRIDE < 65536, "ds_read offset field");
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:%9\n\t"
+      "ds_read_b128 %2, %8 offset:%10\n\t"
+      "ds_read_b128 %3, %8 offset:%11\n\t"
+      "ds_read_b128 %4, %8 offset:%12\n\t"
+      "ds_read_b128 %5, %8 offset:%13\n\t"
+      "ds_read_b128 %6, %8 offset:%14\n\t"
+      "ds_read_b128 %7, %8 offset:%15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+      : "v"(a), "i"(16 * STRIDE), "i"(32 * STRIDE), "i"(48 * STRIDE), "i"(64 * STRIDE), "i"(80 * STRIDE),
+        "i"(96 * STRIDE), "i"(112 * STRIDE)
+      : "memory");
+}
+
+__device__ __forceinline__ u32x4 bc_rd1(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+
+// Phase 1: the lane's x of both halves (8 units from xa, 1 KB apart) and
+// grad_y of both halves (4 units from g0 and 4 from g0 + 4 KB), one wait.
+__device__ __forceinline__ void bc_rd_phase1(u32x4 (&x)[2][4], u32x4 (&g)[2][4], uint32_t xa, uint32_t ga) {
+  asm volatile(
+      "ds_read_b128 %0, %16\n\t"
+      "ds_read_b128 %1, %16 offset:1024\n\t"
+      "ds_read_b128 %2, %16 offset:2048\n\t"
+      "ds_read_b128 %3, %16 offset:3072\n\t"
+      "ds_read_b128 %4, %16 offset:4096\n\t"
+      "ds_read_b128 %5, %16 offset:5120\n\t"
+      "ds_read_b128 %6, %16 offset:6144\n\t"
+      "ds_read_b128 %7, %16 offset:7168\n\t"
+      "ds_read_b128 %8, %17\n\t"
+      "ds_read_b128 %9, %17 offset:1024\n\t"
+      "ds_read_b128 %10, %17 offset:2048\n\t"
+      "ds_read_b128 %11, %17 offset:3072\n\t"
+      "ds_read_b128 %12, %17 offset:4096\n\t"
+      "ds_read_b128 %13, %17 offset:5120\n\t"
+      "ds_read_b128 %14, %17 offset:6144\n\t"
+      "ds_read_b128 %15, %17 offset:7168\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x[0][0]), "=&v"(x[0][1]), "=&v"(x[0][2]), "=&v"(x[0][3]), "=&v"(x[1][0]), "=&v"(x[1][1]),
+        "=&v"(x[1][2]), "=&v"(x[1][3]), "=&v"(g[0][0]), "=&v"(g[0][1]), "=&v"(g[0][2]), "=&v"(g[0][3]),
+        "=&v"(g[1][0]), "=&v"(g[1][1]), "=&v"(g[1][2]), "=&v"(g[1][3])
+      : "v"(xa), "v"(ga)
+      : "memory");
+}
+
+// sixteen 16-byte reads at a + i * 16 * STRIDE, one wait
+template <int STRIDE>
+__device__ __forceinline__ void bc_rd16(u32x4 (&v)[16], uint32_t a) {
+  static_assert(15 * 16 * STRIDE < 65536, "ds_read offset field");
+  asm volatile(
+      "ds_read_b128 %0, %16\n\t"
+      "ds_read_b128 %1, %16 offset:%17\n\t"
+      "ds_read_b128 %2, %16 offset:%18\n\t"
+      "ds_read_b128 %3, %16 offset:%19\n\t"
+      "ds_read_b128 %4, %16 offset:%20\n\t"
+      "ds_read_b128 %5, %16 offset:%21\n\t"
+      "ds_read_b128 %6, %16 offset:%22\n\t"
+      "ds_read_b128 %7, %16 offset:%23\n\t"
+      "ds_read_b128 %8, %16 offset:%24\n\t"
+      "ds_read_b128 %9, %16 offset:%25\n\t"
+      "ds_read_b128 %10, %16 offset:%26\n\t"
+      "ds_read_b128 %11, %16 offset:%27\n\t"
+      "ds_read_b128 %12, %16 offset:%28\n\t"
+      "ds_read_b128 %13, %16 offset:%29\n\t"
+      "ds_read_b128 %14, %16 offset:%30\n\t"
+      "ds_read_b128 %15, %16 offset:%31\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
+        "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]),
+        "=&v"(v[15])
+      : "v"(a), "i"(16 * STRIDE), "i"(32 * STRIDE), "i"(48 * STRIDE), "i"(64 * STRIDE), "i"(80 * STRIDE),
+        "i"(96 * STRIDE), "i"(112 * STRIDE), "i"(128 * STRIDE), "i"(144 * STRIDE), "i"(160 * STRIDE),
+        "i"(176 * STRIDE), "i"(192 * STRIDE), "i"(208 * STRIDE), "i"(224 * STRIDE), "i"(240 * STRIDE)
+      : "memory");
+}
+
+// Phase 2, first batch: grad_mixes of token r (m = 8 q ..: two reads at ga),
+// the exchange's pre-head grad_mixes of token r (gg), the inv_rms of tokens
+// 4 q .. 4 q + 3 (ia + 64 i), pre[r][n], inv_rms[r] and scale[r] of token r
+// (pr, ir, sr), and the half-1 grad_y units (g1, 1 KB apart); one wait.
+__device__ __forceinline__ void bc_rd_phase2a(u32x4& gl, u32x4& gh, u32x4& g4, float (&inv)[4], float& pre_r,
+                                              float& inv_r, float& sc_r, u32x4 (&gr)[4], uint32_t ga, uint32_t gg,
+                                              uint32_t ia, uint32_t pr, uint32_t ir, uint32_t sr, uint32_t g1) {
+  uint32_t iv[4], p, i, c;
+  asm volatile(
+      "ds_read_b128 %0, %14\n\t"
+      "ds_read_b128 %1, %14 offset:16\n\t"
+      "ds_read_b128 %2, %15\n\t"
+      "ds_read_b32 %3, %16\n\t"
+      "ds_read_b32 %4, %16 offset:64\n\t"
+      "ds_read_b32 %5, %16 offset:128\n\t"
+      "ds_read_b32 %6, %16 offset:192\n\t"
+      "ds_read_b32 %7, %17\n\t"
+      "ds_read_b32 %8, %18\n\t"
+      "ds_read_b32 %9, %19\n\t"
+      "ds_read_b128 %10, %20\n\t"
+      "ds_read_b128 %11, %20 offset:1024\n\t"
+      "ds_read_b128 %12, %20 offset:2048\n\t"
+      "ds_read_b128 %13, %20 offset:3072\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(gl), "=&v"(gh), "=&v"(g4), "=&v"(iv[0]), "=&v"(iv[1]), "=&v"(iv[2]), "=&v"(iv[3]), "=&v"(p),
+        "=&v"(i), "=&v"(c), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]), "=&v"(gr[3])
+      : "v"(ga), "v"(gg), "v"(ia), "v"(pr), "v"(ir), "v"(sr), "v"(g1)
+      : "memory");
+#pragma unroll
+  for (int k = 0; k < 4; ++k) inv[k] = __uint_as_float(iv[k]);
+  pre_r = __uint_as_float(p);
+  inv_r = __uint_as_float(i);
+  sc_r = __uint_as_float(c);
+}
+
+// The A operand of a 16x16x32 MFMA holding diag(v) over a tile's 16 tokens in
+// both bf16 planes (k = 8 q + 2 e + p: token 4 q + e, plane p; paired with a
+// bc_col2 B operand): lane (r, q) holds row r, so only the lane with
+// q == r / 4 has a nonzero dword, e = r % 4, the planes' bits hi | lo << 16.
+__device__ __forceinline__ u32x4 bc_diag2(float v, int r, int q) {
+  uint32_t hi, lo;
+  split2_bf16(v, hi, lo);
+  const uint32_t d = q == (r >> 2) ? (hi | (lo << 16)) : 0u;
+  const int e = r & 3;
+  return u32x4{e == 0 ? d : 0u, e == 1 ? d : 0u, e == 2 ? d : 0u, e == 3 ? d : 0u};
+}
+
+// Column c of a lane's 4-token x 8-column block of bf16 (m[e][c / 2] holds
+// columns 2 (c / 2), + 1 of token e) as the B operand of a 16x16x32 MFMA
+// whose k = 2 e + p runs over the lane's tokens e and two planes p of the A
+// operand: dword e = the token's value twice.
+template <int C>
+__device__ __forceinline__ u32x4 bc_col2(const u32x4 (&m)[4]) {
+  constexpr uint32_t sel = (C & 1) ? 0x03020302u : 0x01000100u;
+  const int w = C >> 1;
+  return u32x4{__builtin_amdgcn_perm(m[0][w], m[0][w], sel), __builtin_amdgcn_perm(m[1][w], m[1][w], sel),
+               __builtin_amdgcn_perm(m[2][w], m[2][w], sel), __builtin_amdgcn_perm(m[3][w], m[3][w], sel)};
+}
+
+// Phase 2, second batch: for tokens 4 q + i, the exchange's g of row r (ra +
+// 16 i), grad_mixes rows r (ma + 96 i) and 16 + r % 8 (mb + 96 i), and the
+// half-0 grad_y units (g0, 1 KB apart); one wait.
+__device__ __forceinline__ void bc_rd_phase2b(float (&ge)[4], float (&m0)[4], float (&m1)[4], u32x4 (&gr)[4],
+                                              uint32_t ra, uint32_t ma, uint32_t mb, uint32_t g0) {
+  uint32_t a[4], b[4], c[4];
+  asm volatile(
+      "ds_read_b32 %0, %16\n\t"
+      "ds_read_b32 %1, %16 offset:16\n\t"
+      "ds_read_b32 %2, %16 offset:32\n\t"
+      "ds_read_b32 %3, %16 offset:48\n\t"
+      "ds_read_b32 %4, %17\n\t"
+      "ds_read_b32 %5, %17 offset:96\n\t"
+      "ds_read_b32 %6, %17 offset:192\n\t"
+      "ds_read_b32 %7, %17 offset:288\n\t"
+      "ds_read_b32 %8, %18\n\t"
+      "ds_read_b32 %9, %18 offset:96\n\t"
+      "ds_read_b32 %10, %18 offset:192\n\t"
+      "ds_read_b32 %11, %18 offset:288\n\t"
+      "ds_read_b128 %12, %19\n\t"
+      "ds_read_b128 %13, %19 offset:1024\n\t"
+      "ds_read_b128 %14, %19 offset:2048\n\t"
+      "ds_read_b128 %15, %19 offset:3072\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]),
+        "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
+        "=&v"(gr[3])
+      : "v"(ra), "v"(ma), "v"(mb), "v"(g0)
+      : "memory");
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ge[i] = __uint_as_float(a[i]);
+    m0[i] = __uint_as_float(b[i]);
+    m1[i] = __uint_as_float(c[i]);
+  }
+}
+
+// four 4-byte reads (cz, mix, inv, scale without the pre head), one wait
+__device__ __forceinline__ void bc_rd_coef(float& cz, float& mix, float& inv, float& sk, uint32_t ca, uint32_t cb) {
+  uint32_t v[4];
+  asm volatile(
+      "ds_read_b32 %0, %4 offset:16\n\t"
+      "ds_read_b32 %1, %4 offset:32\n\t"
+      "ds_read_b32 %2, %5 offset:48\n\t"
+      "ds_read_b32 %3, %5 offset:52\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(ca), "v"(cb)
+      : "memory");
+  cz = __uint_as_float(v[0]);
+  mix = __uint_as_float(v[1]);
+  inv = __uint_as_float(v[2]);
+  sk = __uint_as_float(v[3]);
+}
+
+__global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a) {
+  constexpr int M = 24, C = 3 + M;
+  __shared__ __align__(1024) u32x4 xs[kBcSx * 32 * kWave];           // 96 KB: [slot][stream][h][e] 1 KB units
+  __shared__ __align__(1024) u32x4 gsl[kBcSg * kBcGSlot / 16];       // 44 KB
+  __shared__ __align__(1024) u32x4 pbuf[kBcWaves * kBcPollKB * kWave];  // 16 KB: each wave's poll
+  __shared__ __align__(16) float rdy[kBcRS][144];                    // gm[16][4], g[16][4], scale[16]
+  __shared__ __align__(16) float pp[2][kBcWaves][kBcTT];             // phase-1 partials
+  __shared__ __align__(16) float red[kBcWaves][8];                   // end: the waves' contributions
+  // counters: landed_x[3] 0, landed_g[4] 3, copied[3] 7, pcnt[2] 10,
+  // pread[2] 12, ready[2] 14, rdone[2] 16, gdone[4] 18, abort 22
+  __shared__ uint32_t cnt[32];
+  __shared__ int info[4];
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = stream n
+  const int n = wave;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t T = a.T;
+  const int D = a.D, G = a.G;
+  const int64_t K = 4 * (int64_t)D;
+  const uint64_t to = a.timeout;
+  uint32_t* status = a.ctl + kCtlStatus;
+
+  if (tid < 32) cnt[tid] = 0u;
+  if (tid == 0) co_register(a.ctl, G, a.maxg, to, info);
+  __syncthreads();
+  const int group = info[0], ngroups = info[1], member = info[2];
+  if (group < 0) return;  // uniform over the block: not a member of a group
+  if (tid == 0) __hip_atomic_store(a.ctl + kCtlGroups, (uint32_t)ngroups, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // tile and loop indices fit 32 bits (the host bounds T)
+  const int ntiles = (int)((T + kBcTT - 1) / kBcTT);
+  const int nqr = (ntiles - group + ngroups - 1) / ngroups;  // tiles of this group
+  const int nq = nqr > 0 ? nqr : 0;
+  const int slice0 = member * 256;
+  u32x4* recw = a.rec + (size_t)group * kBcR * G * kBcRecWords;
+  const auto ring = rows_rsrc(recw, (int64_t)kBcR * G * kBcRecWords * 16);
+  const uint32_t xs_l = lds_addr(xs), gs_l = lds_addr(gsl), pb_l = lds_addr(pbuf) + wave * kBcPollKB * 1024;
+  const uint32_t rdy_l = lds_addr(&rdy[0][0]), pp_l = lds_addr(&pp[0][0][0]);
+  const uint32_t c_lx = lds_addr(cnt), c_lg = c_lx + 12, c_cp = c_lx + 28, c_pc = c_lx + 40, c_pr = c_lx + 48,
+                 c_rd = c_lx + 56, c_rdone = c_lx + 64, c_gd = c_lx + 72, c_ab = c_lx + 88;
+  const int kg = wave < 3 ? 3 : 2;  // grad_y / per-token loads this wave issues per tile
+  constexpr int npoll = kBcPollKB;  // poll loads a wave issues per tile
+  const float a0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(a.alpha[0])));
+  const float invK = 1.0f / (float)K;
+  auto t0_of = [&](int qi) { return (int64_t)(group + qi * ngroups) * kBcTT; };
+  auto nv_of = [&](int64_t t0) { return (int)(T - t0 < kBcTT ? T - t0 : kBcTT); };
+  // the publisher of tile j's record (wave w polls and totals chunk w of every
+  // tile): wave (j + 1) % 4
+
+  // ---- loads: tile qi's x units of this stream (8), its grad_y units (h, e =
+  // wave) and (waves 0..2) a third of the per-token data: wave 0 grad_mixes
+  // bytes [0, 1024), wave 1 [1024, 1536) (lanes past 1536 read zeros into the
+  // slot's padding), wave 2 coefX
+  auto issue_x = [&](int qi) {
+    const int64_t t0 = t0_of(qi);
+    const int nv = nv_of(t0);
+    const auto rx = rows_rsrc(a.x + (t0 * 4 + n) * (int64_t)D + slice0, ((int64_t)(nv - 1) * K + 256) * 2);
+    const uint32_t slot = bc_opq(xs_l) + ((uint32_t)qi % (uint32_t)kBcSx) * 32 * 1024 + (uint32_t)n * 8192;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int tok = 4 * q + e;
+        const uint32_t off = tok < nv ? (uint32_t)(((int64_t)tok * K + 128 * hh + 8 * r) * 2) : kBufferOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(uintptr_t)(slot + (hh * 4 + e) * 1024), 16, off,
+                                                 0, 0, 2 /* nt */);
+      }
+  };
+  auto issue_g = [&](int qi) {
+    const int64_t t0 = t0_of(qi);
+    const int nv = nv_of(t0);
+    const uint32_t slot = bc_opq(gs_l) + (uint32_t)(qi & (kBcSg - 1)) * kBcGSlot;
+    const auto rg = rows_rsrc(a.gy + t0 * D + slice0, ((int64_t)(nv - 1) * D + 256) * 2);
+    const int tok = 4 * q + wave;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint32_t off = tok < nv ? (uint32_t)(((int64_t)tok * D + 128 * hh + 8 * r) * 2) : kBufferOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(uintptr_t)(slot + (4 * hh + wave) * 1024), 16,
+                                               off, 0, 0, 2 /* nt */);
+    }
+    if (wave < 2) {
+      const auto rm = rows_rsrc(a.gm + t0 * M, (int64_t)nv * M * 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void_t*)(uintptr_t)(slot + kBcGm + wave * 1024), 16,
+                                               (uint32_t)(wave * 1024 + 16 * lane), 0, 0, 0);
+    } else if (wave == 2) {
+      const auto rc = rows_rsrc(a.coefX + t0 * 16, (int64_t)nv * 64);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_void_t*)(uintptr_t)(slot + kBcCoef), 16,
+                                               (uint32_t)(16 * lane), 0, 0, 0);
+    }
+  };
+  // ---- poll: chunk `wave` of every member's record of tile u into this
+  // wave's poll buffer (member i's word w at (6 i + w) * 16) ----------------
+  auto issue_poll = [&](int u) {
+#pragma unroll
+    for (int k = 0; k < npoll; ++k) {
+      // lane l: word l % 8 of member 8 k + l / 8 (words past kBcDataWords and
+      // members past G read zeros)
+      const int f = 64 * k + lane, i = f / kBcChunkWords;
+      const uint32_t off = i < G && (lane & (kBcChunkWords - 1)) < kBcDataWords
+                               ? (uint32_t)((((u & (kBcR - 1)) * 4 + wave) * G * kBcChunkWords + f) * 16)
+                               : kBufferOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ring, (lds_void_t*)(uintptr_t)(bc_opq(pb_l) + k * 1024), 16, off, 0, 0,
+                                               kCoPolicySc1);
+    }
+  };
+
+  // phi^T operands of the lane's columns (B of gs: m = 8 q .. 8 q + 7) and the
+  // grad_phi accumulators (rows 16 mt + 4 q + v, column c of the lane's 8 in
+  // half h)
+  u32x4 pb[2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int64_t kcol = (int64_t)n * D + slice0 + 128 * hh + 8 * r;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) pb[hh][c] = ld16(a.phiT + (kcol + c) * 32 + 8 * q);
+  }
+  floatx4 ph[2][2][8];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ph[hh][mt][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float acc_c0 = 0.f, acc_b = 0.f;  // the owner's grad_alpha[0] / grad_base[n] terms
+  wait_vmcnt<0>();  // phi operands in registers before any direct-to-LDS load is issued
+  asm volatile("" ::: "memory");
+
+  // prologue, in the order the loop would have issued them (a tile's grad_y
+  // loads before its x loads)
+  if (nq > 0) issue_g(0);
+  if (nq > 0) issue_x(0);
+  if (nq > 1) issue_g(1);
+  if (nq > 1) issue_x(1);
+
+  int own = 0;  // (tile u) % G: the member that owns tile u's grad_alpha / grad_base terms
+  // Iteration j, with u = j - 2:
+  //   (E) this wave's share of the exchange of tile u (chunk `wave`: tokens
+  //       4 wave .. 4 wave + 3), (F) wait for all four shares, (G) this
+  //       wave's poll of tile u + 1, (H) phase 2 of tile u from Xr with its
+  //       stores, (I) tile j + 2's grad_y loads into tile u's slot,
+  //   (A) tile j landed, (B) phase 1 of tile j into Xr (the registers phase
+  //       2 just released), (D) the record of tile j (its publisher), (C)
+  //       tile j + 2's x loads.
+  // So only two tiles of x sit in registers at a time.  The poll is issued
+  // before this iteration's stores and loads, so it completes after older
+  // work only.  Every index is a 32-bit scalar; every wait on a counter is a
+  // scalar branch.  A wait that gives up (abort flag and status set) lets
+  // the iteration run to its end on whatever the buffers hold, every later
+  // wait returns at once, and the loop stops after the iteration: the sum
+  // kernel then replaces the outputs with NaN.
+  auto step = [&](int j, u32x4 (&Xr)[2][4]) {
+    const int u = j - kBcLag;
+    const bool pub_prev = (j & 3) == wave;  // this wave published tile j - 1's record
+    if (u >= 0 && u < nq) {
+      const int rs = u & 1;
+      const uint32_t rslot = bc_opq(rdy_l) + (uint32_t)(rs * 144 * 4);
+      const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
+      // ---- (E) this wave's share of the exchange of tile u -------------------
+      {
+        // operations issued after the poll (iteration j - 1: stores of tile
+        // u - 1 (8), grad_y loads of tile j + 1 (kg), the record of tile j - 1
+        // (its publisher), x loads of tile j + 1 (8)); away from the steady
+        // state all of them
+        if (j >= 3 && j + 1 < nq)
+          bc_wait_steady<16, 1>(kg, pub_prev);
+        else
+          wait_vmcnt<0>();
+        const uint32_t tag = (uint32_t)(u + 1);
+        uint64_t deadline = 0;
+        float s0, s1, s2;
+        for (;;) {
+          // lane l: word w = l % 8 of members l / 8 + 8 k, k = 0..3; every
+          // valid word of the G members must carry this tile's tag
+          u32x4 v[4];
+          lds_read4<1024>(v, bc_opq(pb_l) + (uint32_t)(16 * lane));
+          uint32_t cur = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) cur += (uint32_t)__popcll(__ballot(v[k][3] == tag));
+          if (cur == (uint32_t)(kBcDataWords * G)) {
+            // members past G and words past kBcDataWords are zeros; the sum
+            // runs over k, then over the lanes of the same word (l ^ 8,
+            // l ^ 16, l ^ 32): a fixed order
+            s0 = (__uint_as_float(v[0][0]) + __uint_as_float(v[1][0])) + (__uint_as_float(v[2][0]) + __uint_as_float(v[3][0]));
+            s1 = (__uint_as_float(v[0][1]) + __uint_as_float(v[1][1])) + (__uint_as_float(v[2][1]) + __uint_as_float(v[3][1]));
+            s2 = (__uint_as_float(v[0][2]) + __uint_as_float(v[1][2])) + (__uint_as_float(v[2][2]) + __uint_as_float(v[3][2]));
+            s0 = group_sum<56>(s0);
+            s1 = group_sum<56>(s1);
+            s2 = group_sum<56>(s2);
+            break;
+          }
+          s0 = s1 = s2 = 0.f;
+          if (deadline == 0) deadline = co_now() + to;
+          if (co_lds_ld_u(bc_opq(c_ab))) break;
+          if (co_now() > deadline) {
+            co_lds_inc(bc_opq(c_ab));
+            co_fail(status, kBcStPoll);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          issue_poll(u);
+          wait_vmcnt<0>();
+        }
+        // lane v < 16: value v of the chunk (token t = 4 wave + v / 4, stream v % 4),
+        // from lane v / 3 (word v / 3), component v % 3
+        const int src = (lane & 15) / 3, cmp = (lane & 15) % 3;
+        const float f0 = __shfl(s0, src, kWave), f1 = __shfl(s1, src, kWave), f2 = __shfl(s2, src, kWave);
+        const float gp = cmp == 0 ? f0 : (cmp == 1 ? f1 : f2);
+        const int t = 4 * wave + ((lane & 15) >> 2), nn = lane & 3;
+        const uint32_t cf = gslot + kBcCoef + (uint32_t)(t * 64);
+        float cz, mix, inv, sk;
+        bc_rd_coef(cz, mix, inv, sk, cf + 4 * nn, cf);
+        const float gz = gp * cz;
+        const float gmv = gz * a0;
+        const float sd = group_sum<3>(gmv * mix);
+        const float sc = sk - inv * inv * sd * invK;
+        co_wait_ge(bc_opq(c_rdone) + 4 * (uint32_t)rs, (uint32_t)(kBcWaves * (u >> 1)), bc_opq(c_ab), status, kBcStRdone, to);
+        const bool owner = own == member;  // the tile's owner adds its grad_alpha[0] / grad_base terms
+        if (lane < 16) {
+          co_lds_st(rslot + (uint32_t)(4 * (4 * t + nn)), gmv);
+          co_lds_st(rslot + (uint32_t)(256 + 4 * (4 * t + nn)), gmv * inv);
+          if (nn == 0) co_lds_st(rslot + (uint32_t)(512 + 4 * t), sc);
+        }
+        if (owner && lane < 16) {
+          acc_c0 = fmaf(gz, mix, acc_c0);
+          acc_b += gz;
+        }
+        co_lds_inc(bc_opq(c_rd) + 4 * (uint32_t)rs);
+      }
+      // ---- (F) wait for the four shares -------------------------------------
+      co_wait_ge(bc_opq(c_rd) + 4 * (uint32_t)rs, (uint32_t)(kBcWaves * ((u >> 1) + 1)), bc_opq(c_ab), status, kBcStReady, to);
+    }
+    // ---- (G) the next tile's poll (this wave's buffer is free once it has
+    // totalled tile u) ---------------------------------------------------------
+    if (u + 1 >= 0 && u + 1 < nq) issue_poll(u + 1);
+    if (u >= 0 && u < nq) {
+      // ---- (H) phase 2 of tile u --------------------------------------------
+      const int rs = u & 1;
+      const uint32_t rslot = bc_opq(rdy_l) + (uint32_t)(rs * 144 * 4);
+      const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
+      const uint32_t gmb = gslot + kBcGm, cfb = gslot + kBcCoef;
+      // operands from the slot and the exchange, in two batches of reads:
+      // gA = grad_mixes * inv of token r, m = 8 q .. 8 q + 7 (hi / lo planes;
+      // m < 4 from the exchange, m >= 24 zero); gt[mt] = g = grad_mixes * inv
+      // of row m = 16 mt + r for tokens 4 q .. 4 q + 3 (dword e: token e's hi
+      // and lo planes; m < 4 from the exchange); diag(pre[., n]) and
+      // diag(scale) over the tile's tokens; grad_y of both halves
+      u32x4 gA0, gA1, gt[2], grh[2][4], dpre, dsc;
+      {
+        u32x4 gl, gh, g4;
+        float inv_e[4], pre_r, inv_r, sc_r;
+        bc_rd_phase2a(gl, gh, g4, inv_e, pre_r, inv_r, sc_r, grh[1],
+                      gmb + (uint32_t)((r * M + 8 * (q < 3 ? q : 2)) * 4), rslot + (uint32_t)(16 * r),
+                      cfb + (uint32_t)(256 * q + 48), cfb + (uint32_t)(64 * r + 4 * n), cfb + (uint32_t)(64 * r + 48),
+                      rslot + (uint32_t)(512 + 4 * r), gslot + (uint32_t)(4096 + 16 * lane));
+        float ge[4], m0[4], m1[4];
+        bc_rd_phase2b(ge, m0, m1, grh[0], rslot + (uint32_t)(256 + 64 * q + 4 * (r & 3)),
+                      gmb + (uint32_t)((96 * 4 * q) + 4 * r), gmb + (uint32_t)((96 * 4 * q) + 64 + 4 * (r & 7)),
+                      gslot + (uint32_t)(16 * lane));
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f[i] = (q == 0 ? __uint_as_float(g4[i]) : (q < 3 ? __uint_as_float(gl[i]) : 0.f)) * inv_r;
+          f[4 + i] = (q < 3 ? __uint_as_float(gh[i]) : 0.f) * inv_r;
+        }
+        split8(f, gA0, gA1);
+        uint32_t hi[2][4], lo[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g0 = r < 4 ? ge[i] : m0[i] * inv_e[i];
+          const float g1 = r < 8 ? m1[i] * inv_e[i] : 0.f;
+          split2_bf16(g0, hi[0][i], lo[0][i]);
+          split2_bf16(g1, hi[1][i], lo[1][i]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          gt[mt] = u32x4{hi[mt][0] | (lo[mt][0] << 16), hi[mt][1] | (lo[mt][1] << 16), hi[mt][2] | (lo[mt][2] << 16),
+                         hi[mt][3] | (lo[mt][3] << 16)};
+        dpre = bc_diag2(pre_r, r, q);
+        dsc = bc_diag2(sc_r, r, q);
+      }
+      const int64_t t0 = t0_of(u);
+      const int nv = nv_of(t0);
+      const auto rgx = rows_rsrc(a.gx + t0 * K, (int64_t)nv * K * 2);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        // per column c of the lane's 8: grad_phi partial += g^T @ x over the
+        // tile's 16 tokens, and grad_x = diag(pre) y + diag(scale) x +
+        // (grad_mixes inv) @ phi in one 16x16 accumulator; every MFMA is
+        // 16x16x32 (k over tokens x planes for the first three, over m for gs)
+        uint32_t o[4][4];
+        auto col = [&](auto cc) -> floatx4 {
+          constexpr int c = decltype(cc)::value;
+          const u32x4 xd = bc_col2<c>(Xr[hh]), yd = bc_col2<c>(grh[hh]);
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) ph[hh][mt][c] = mfma16x16x32(as_bf16x8(gt[mt]), as_bf16x8(xd), ph[hh][mt][c]);
+          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = mfma16x16x32(as_bf16x8(dpre), as_bf16x8(yd), acc);
+          acc = mfma16x16x32(as_bf16x8(dsc), as_bf16x8(xd), acc);
+          acc = mfma16x16x32(as_bf16x8(gA0), as_bf16x8(pb[hh][c]), acc);
+          acc = mfma16x16x32(as_bf16x8(gA1), as_bf16x8(pb[hh][c]), acc);
+          return acc;
+        };
+        auto pair = [&](auto ww) {
+          constexpr int w = decltype(ww)::value;
+          const floatx4 c0 = col(std::integral_constant<int, 2 * w>{});
+          const floatx4 c1 = col(std::integral_constant<int, 2 * w + 1>{});
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e][w] = pack_bf16x2(c0[e], c1[e]);
+        };
+        pair(std::integral_constant<int, 0>{});
+        pair(std::integral_constant<int, 1>{});
+        pair(std::integral_constant<int, 2>{});
+        pair(std::integral_constant<int, 3>{});
+        const int colh = slice0 + 128 * hh + 8 * r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // rows >= nv fall outside the range and are dropped
+          const uint32_t off = (uint32_t)((((4 * q + e) * 4 + n) * D + colh) * 2);
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{o[e][0], o[e][1], o[e][2], o[e][3]}, rgx, off, 0, 2 /* nt */);
+        }
+      }
+      co_lds_inc(bc_opq(c_gd) + 4 * (uint32_t)(u & (kBcSg - 1)));
+      co_lds_inc(bc_opq(c_rdone) + 4 * (uint32_t)rs);
+      // ---- (I) grad_y / per-token data of tile j + 2 into this slot ---------
+      if (j + 2 < nq) {
+        co_wait_ge(bc_opq(c_gd) + 4 * (uint32_t)(u & (kBcSg - 1)), (uint32_t)(kBcWaves * ((u >> 2) + 1)), bc_opq(c_ab), status,
+                        kBcStGdone, to);
+        issue_g(j + 2);
+      }
+      own = own + 1 == G ? 0 : own + 1;
+    } else if (j + 2 < nq) {
+      issue_g(j + 2);  // (I) a slot not used before
+    }
+    if (j < nq) {
+      // ---- (A) tile j landed ---------------------------------------------
+      // operations this wave issued after tile j's x loads (iteration j - 1:
+      // poll (3), stores (8), grad_y loads (kg), record (its publisher), x
+      // loads (8); iteration j: poll (3), stores (8), grad_y loads (kg));
+      // away from the steady state all of them
+      if (j >= 3 && j + 2 < nq)
+        bc_wait_steady<30, 2>(kg, pub_prev);
+      else
+        wait_vmcnt<0>();
+      const uint32_t jm3 = (uint32_t)j % 3u, jd3 = (uint32_t)j / 3u;
+      co_lds_inc(bc_opq(c_lx) + 4 * jm3);
+      co_lds_inc(bc_opq(c_lg) + 4 * (uint32_t)(j & (kBcSg - 1)));
+      co_wait_ge(bc_opq(c_lx) + 4 * jm3, (uint32_t)kBcWaves * (jd3 + 1), bc_opq(c_ab), status, kBcStLanded, to);
+      co_wait_ge(bc_opq(c_lg) + 4 * (uint32_t)(j & (kBcSg - 1)), (uint32_t)(kBcWaves * ((j >> 2) + 1)), bc_opq(c_ab), status,
+                 kBcStLanded, to);
+      // ---- (B) phase 1: copy x, grad_pre partial -------------------------
+      const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(j & (kBcSg - 1)) * kBcGSlot;
+      const uint32_t xslot = bc_opq(xs_l) + jm3 * 32 * 1024 + (uint32_t)(n * 8192 + 16 * lane);
+      u32x4 gr1[2][4];
+      bc_rd_phase1(Xr, gr1, xslot, gslot + (uint32_t)(16 * lane));
+      co_lds_inc(bc_opq(c_cp) + 4 * jm3);
+      float pe[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pe[e] = 0.f;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x4 (&gr)[4] = gr1[hh];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) pe[e] = dot2_bf16(gr[e][w], Xr[hh][e][w], pe[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pe[e] = group_sum<15>(pe[e]);  // the 16 lanes of row q: token 4 q + e
+      const int pbi = j & 1;
+      co_wait_ge(bc_opq(c_pr) + 4 * (uint32_t)pbi, (uint32_t)(j >> 1), bc_opq(c_ab), status, kBcStPread, to);
+      if (r == 0) co_lds_st4(bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + n) * kBcTT + 4 * q) * 4), floatx4{pe[0], pe[1], pe[2], pe[3]});
+      co_lds_inc(bc_opq(c_pc) + 4 * (uint32_t)pbi);
+      // ---- (D) the record of tile j -----------------------------------------
+      if (wave == ((j + 1) & 3)) {
+        co_wait_ge(bc_opq(c_pc) + 4 * (uint32_t)pbi, (uint32_t)(kBcWaves * ((j >> 1) + 1)), bc_opq(c_ab), status, kBcStPcnt, to);
+        // lane l < 24: chunk c = l / 6, word w = l % 6 holds values 3 w .. 3 w + 2
+        // of the chunk, value v = 4 (token - 4 c) + stream (v < 16)
+        const int ck = lane / kBcDataWords, wd = lane % kBcDataWords;
+        u32x4 word;
+        {
+          uint32_t ad[3];
+#pragma unroll
+          for (int k = 0; k < 3; ++k) {
+            const int v = 3 * wd + k, vv = v < 16 ? v : 15;
+            ad[k] = bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + (vv & 3)) * kBcTT + 4 * (ck & 3) + (vv >> 2)) * 4);
+          }
+          uint32_t w0, w1, w2;
+          asm volatile(
+              "ds_read_b32 %0, %3\n\t"
+              "ds_read_b32 %1, %4\n\t"
+              "ds_read_b32 %2, %5\n\t"
+              "s_waitcnt lgkmcnt(0)"
+              : "=&v"(w0), "=&v"(w1), "=&v"(w2)
+              : "v"(ad[0]), "v"(ad[1]), "v"(ad[2])
+              : "memory");
+          word[0] = 3 * wd < 16 ? w0 : 0u;
+          word[1] = 3 * wd + 1 < 16 ? w1 : 0u;
+          word[2] = 3 * wd + 2 < 16 ? w2 : 0u;
+        }
+        word[3] = (uint32_t)(j + 1);
+        co_lds_inc(bc_opq(c_pr) + 4 * (uint32_t)pbi);
+        const uint32_t off =
+            lane < 4 * kBcDataWords
+                ? (uint32_t)(((((j & (kBcR - 1)) * 4 + ck) * G + member) * kBcChunkWords + wd) * 16)
+                : kBufferOob;
+        // default policy: the line stays in this XCC's L2, where the readers' loads find it
+        __builtin_amdgcn_raw_buffer_store_b128(word, ring, off, 0, 0);
+      }
+      // ---- (C) x of tile j + 2 into the slot of tile j - 1 --------------------
+      if (j + 2 < nq) {
+        const uint32_t j2 = (uint32_t)(j + 2);
+        co_wait_ge(bc_opq(c_cp) + 4 * (j2 % 3u), (uint32_t)kBcWaves * (j2 / 3u), bc_opq(c_ab), status, kBcStCopied, to);
+        issue_x(j + 2);
+      }
+    }
+  };
+
+  {
+    // two tiles of x in registers: XP holds tile j - 2 on entry to iteration
+    // j and tile j on exit, XQ tile j - 1; they swap after each iteration
+    u32x4 XP[2][4], XQ[2][4];
+    const int iters = nq + kBcLag;
+    for (int j = 0; j < iters; ++j) {
+      step(j, XP);
+      if (co_lds_ld_u(bc_opq(c_ab))) break;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u32x4 t = XP[hh][e];
+          XP[hh][e] = XQ[hh][e];
+          XQ[hh][e] = t;
+        }
+    }
+  }
+  wait_vmcnt<0>();  // no direct-to-LDS load may outlive the block
+
+  // ---- this group's grad_phi partial: rows 16 mt + 4 q + v < 24 -----------
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    float* part = a.part + (int64_t)group * M * K + (int64_t)n * D + slice0 + 128 * hh + 8 * r;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 16 * mt + 4 * q + v;
+        if (m >= M) continue;
+        float4* dst = reinterpret_cast<float4*>(part + (int64_t)m * K);
+        dst[0] = float4{ph[hh][mt][0][v], ph[hh][mt][1][v], ph[hh][mt][2][v], ph[hh][mt][3][v]};
+        dst[1] = float4{ph[hh][mt][4][v], ph[hh][mt][5][v], ph[hh][mt][6][v], ph[hh][mt][7][v]};
+      }
+  }
+  // ---- grad_alpha[0] / grad_base[0..3] terms of the tiles this member owns
+  {
+    const float c0 = group_sum<63>(acc_c0);
+    const float b = group_sum<60>(acc_b);  // lanes with the same stream m = lane % 4
+    if (lane < 4) red[wave][1 + lane] = b;
+    if (lane == 0) red[wave][0] = c0;
+  }
+  __syncthreads();
+  if (tid < C) {
+    float v = 0.f;
+    if (tid == 0 || (tid >= 3 && tid < 7)) {
+      const int k = tid == 0 ? 0 : tid - 2;
+      v = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
+    }
+    // row (group, member): the same row holds the same tiles' terms whichever
+    // CU the member runs on, so the fixed-order sum is reproducible
+    a.contrib[((int64_t)group * G + member) * C + tid] = v;
+  }
+}
+
+// grad_phi = sum over the groups that formed (read from the control words)
+// of their partials, in group order; after a timed-out wait (status word
+// nonzero) grad_phi and grad_x become NaN instead.  Block 0 copies the status
+// word to the caller's (status_out, may be null; a system-scope store, so it
+// may be host memory).
+__global__ __launch_bounds__(256) void bc_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                      int64_t n, const uint32_t* ctl, bf16_t* gx, int64_t ngx,
+                                                      int32_t* status_out) {
+  const uint32_t st = ctl[kCtlStatus];
+  const int ng = (int)ctl[kCtlGroups];
+  const int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+  if (blockIdx.x == 0 && threadIdx.x == 0 && status_out)
+    __hip_atomic_store(status_out, (int32_t)st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (st) {
+    for (int64_t i = i0; i < n; i += stride) out[i] = __builtin_nanf("");
+    uint16_t* g = reinterpret_cast<uint16_t*>(gx);
+    for (int64_t i = i0; i < ngx; i += stride) g[i] = 0x7FC0u;  // bf16 NaN
+    return;
+  }
+  for (int64_t i = i0; i < n; i += stride) {
+    float s = 0.f;
+    for (int g = 0; g < ng; ++g) s += part[(int64_t)g * n + i];
+    out[i] = s;
+  }
+}
+
+}  // namespace mhc

@@ -68,6 +68,8 @@
 // of it when the call's work has finished.
 #pragma once
 
+#include "coop_common.hpp"
+
 namespace mhc {
 
 constexpr int kCoTT = 16;                          // tokens per tile
@@ -80,19 +82,12 @@ constexpr int kCoR = 16;                           // exchange ring: tiles per g
 constexpr int kCoVals = 25;                        // sums per token: 24 mixes + sum(x^2)
 constexpr int kCoRecWords = kCoTT * kCoVals / 2;   // 16-byte words of a record (200)
 constexpr int kCoYWords = kCoTT * 5 / 2;           // words y needs: 4 pre mixes + sum(x^2) (40)
-constexpr int kCoMaxGroups = 16;
-constexpr int kCoMinG = 16;                        // fewest members per group
 constexpr int kCoMaxHW = (160 + kCoMinG - 1) / kCoMinG;  // head words a member totals, at most (10)
-constexpr int kCoMaxG = 32;
-constexpr int kCoCtlWords = 64;
-constexpr uint64_t kCoTimeout = 25000000ull;       // 0.25 s of s_memrealtime (100 MHz)
-// control words: [0..15] blocks registered per XCC, then
-constexpr int kCtlArrived = 16, kCtlStatus = 17;
-// status (first failure wins): 1 registration, 2 no group formed, then the
-// wait that timed out: 3 L slot copied, 4 L partial buffer, 5 Y tile landed,
+// forward status codes after the common ones (coop_common.hpp): the wait
+// that timed out: 3 L slot copied, 4 L partial buffer, 5 Y tile landed,
 // 6 P exchange poll, 7 Y sums, 8 P own publish, 9 P sums slot
-constexpr uint32_t kStReg = 1, kStNoGroup = 2, kStLCopied = 3, kStLPread = 4, kStYLanded = 5, kStPPoll = 6,
-                   kStYSums = 7, kStPPub = 8, kStPSlot = 9;
+constexpr uint32_t kStLCopied = 3, kStLPread = 4, kStYLanded = 5, kStPPoll = 6, kStYSums = 7, kStPPub = 8,
+                   kStPSlot = 9;
 
 // Value order inside a record: v * 16 + token, v = 0..3 the pre mixes
 // (m = 0..3), v = 4 the sum of squares, v = 5..24 the mixes m = 4..23, so
@@ -127,40 +122,6 @@ struct CoopArgs {
   uint64_t timeout; // s_memrealtime ticks a wait may last without progress
 };
 
-// ---- LDS accesses of the L-waves (direct-to-LDS loads in flight: inline
-// asm, see lds_dma.hpp) and LDS counters --------------------------------------
-__device__ __forceinline__ uint32_t co_lds_ld(uint32_t a) {
-  uint32_t v;
-  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-  return v;
-}
-// No wait: a wave's LDS operations are performed in issue order, so a count
-// raised after LDS writes is seen only after them, and nothing this wave
-// does next depends on the add having landed.
-__device__ __forceinline__ void co_lds_add(uint32_t a, uint32_t v) {
-  asm volatile("ds_add_u32 %0, %1" ::"v"(a), "v"(v) : "memory");
-}
-__device__ __forceinline__ uint32_t co_lds_add_rtn(uint32_t a, uint32_t v) {
-  uint32_t old;
-  asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(old) : "v"(a), "v"(v) : "memory");
-  return old;
-}
-// Counter updates from lane 0 only: a ds_add issued by the whole wave would
-// add once per active lane.  The returned old value is broadcast.
-__device__ __forceinline__ void co_lds_inc(uint32_t a) {
-  if (__lane_id() == 0) co_lds_add(a, 1u);
-}
-__device__ __forceinline__ uint32_t co_lds_inc_rtn(uint32_t a) {
-  uint32_t old = 0u;
-  if (__lane_id() == 0) old = co_lds_add_rtn(a, 1u);
-  return __builtin_amdgcn_readfirstlane(old);
-}
-__device__ __forceinline__ void co_lds_st(uint32_t a, float v) {
-  asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
-}
-__device__ __forceinline__ void co_lds_st4(uint32_t a, floatx4 v) {  // a 16-byte aligned
-  asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
-}
 // The 200 value pairs of a record from the four L-waves' partials (1600
 // bytes apart) in one batch: v[it][w] = wave w's pair of word 64 it + lane;
 // words 0..191 from a = base + 8 lane, words 192.. from a3 (lanes past the
@@ -244,44 +205,6 @@ __device__ __forceinline__ void co_lds_rd4x2(u32x4 (&v)[4], uint32_t a0, uint32_
   for (int n = 0; n < 4; ++n) v[n] = u32x4{h[2 * n][0], h[2 * n][1], h[2 * n + 1][0], h[2 * n + 1][1]};
 }
 
-__device__ __forceinline__ uint64_t co_now() { return __builtin_amdgcn_s_memrealtime(); }
-
-// Wait until the LDS counter at `a` reaches `target` (or the block aborts /
-// `timeout` ticks pass without it: then false, with the abort flag and
-// status set).
-__device__ __forceinline__ void co_fail(uint32_t* status, uint32_t code) {
-  uint32_t expected = 0u;
-  __hip_atomic_compare_exchange_strong(status, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool co_wait_ge(uint32_t a, uint32_t target, uint32_t abort_a, uint32_t* status,
-                                           uint32_t code, uint64_t timeout) {
-  if (co_lds_ld(a) >= target) return true;
-  const uint64_t deadline = co_now() + timeout;
-  for (;;) {
-    if (co_lds_ld(a) >= target) return true;
-    if (co_lds_ld(abort_a)) return false;
-    if (co_now() > deadline) {
-      co_lds_inc(abort_a);
-      co_fail(status, code);
-      return false;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
-// vmcnt(n * PER) for a run-time n in [0, MAXN]
-template <int PER, int MAXN>
-__device__ __forceinline__ void co_wait_tiles(int n) {
-  if constexpr (MAXN >= 0) {
-    if (n >= MAXN) {
-      wait_vmcnt<PER * MAXN>();
-      return;
-    }
-    co_wait_tiles<PER, MAXN - 1>(n);
-  }
-}
-
 // Poll `nm` <= PVN members' words at byte offset `off0` of the group's ring
 // (member stride kCoRecWords words) until
 // every tag equals `tag`; returns the two
@@ -289,7 +212,6 @@ __device__ __forceinline__ void co_wait_tiles(int n) {
 // The loads are device scope (sc1): they bypass this CU's L1, which may hold
 // stale copies of the ring, and read the XCD's L2, where the writers' stores
 // land.  Lanes with !active take part in the wave's retry vote only.
-constexpr int kCoPolicySc1 = 16;
 template <int PVN>
 __device__ __forceinline__ bool co_poll_sum(u32x4 (&v)[PVN], const __amdgpu_buffer_rsrc_t& ring, uint32_t off0, int nm,
                                             bool active, uint32_t tag, float& s0, float& s1, uint32_t abort_a,
@@ -344,43 +266,12 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t T = a.T;
   const int D = a.D, K = 4 * D, G = ca.G;
-  const uint64_t deadline0 = co_now(), to = ca.timeout;
+  const uint64_t to = ca.timeout;
   uint32_t* status = ca.ctl + kCtlStatus;
 
   // ---- group formation: the blocks of one XCC, in registration order ------
   if (tid < 24 + 3 * kCoPSlots) cnt[tid] = 0u;
-  if (tid == 0) {
-    uint32_t xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    xcc &= 15u;
-    const uint32_t rank = __hip_atomic_fetch_add(ca.ctl + xcc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(ca.ctl + kCtlArrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bool ok = true;
-    while (__hip_atomic_load(ca.ctl + kCtlArrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gridDim.x) {
-      if (co_now() > deadline0 + ca.timeout) {
-        ok = false;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    // an XCC with c registered blocks forms c / G groups: its block of rank r
-    // is member r % G of its group r / G (if r / G < c / G)
-    int group = -1, ngroups = 0;
-    if (ok) {
-      for (uint32_t x = 0; x < 16; ++x) {
-        const uint32_t c = __hip_atomic_load(ca.ctl + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int ng = (int)(c / (uint32_t)G) < ca.maxg - ngroups ? (int)(c / (uint32_t)G) : ca.maxg - ngroups;
-        if (x == xcc && (int)(rank / (uint32_t)G) < ng) group = ngroups + (int)(rank / (uint32_t)G);
-        ngroups += ng;
-      }
-      if (ngroups == 0) co_fail(status, kStNoGroup);
-    } else {
-      co_fail(status, kStReg);
-    }
-    info[0] = group;
-    info[1] = ngroups;
-    info[2] = (int)(rank % (uint32_t)G);
-  }
+  if (tid == 0) co_register(ca.ctl, G, ca.maxg, ca.timeout, info);
   __syncthreads();
   const int group = info[0], ngroups = info[1], member = info[2];
   if (group < 0) return;  // uniform over the block: not a member of a group
@@ -760,31 +651,6 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   }
 }
 
-// zero `n` 16-byte words (the control words and the exchange ring before a launch)
-__global__ __launch_bounds__(256) void co_zero_kernel(u32x4* p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = zero4();
-}
-
-// Slice geometry for D: 256-column slices, G = D / 256 members per group.
-// Used where it measured faster than the two-pass forms on MI355X (32-CU
-// XCCs): G = 16 (two groups per XCC, D = 4096) and 28 <= G <= 32 (one group
-// per XCC, D = 7168 .. 8192).  With G = 12, 14, 20 or 24 too many CUs idle
-// or the slices are too short, and the two-pass forms win; 0 selects them.
-inline int coop_nch(int D, int* G) {
-  if (D % 256) return 0;
-  const int g = D / 256;
-  if (g == 16 || (g >= 28 && g <= kCoMaxG)) {
-    *G = g;
-    return 32;
-  }
-  return 0;
-}
-
-// Groups the exchange ring is sized for: one per G CUs, at most kCoMaxGroups.
-inline int coop_max_groups(int G) {
-  const int g = (int)(device_cu_count() / G);
-  return g < kCoMaxGroups ? g : kCoMaxGroups;
-}
 
 constexpr int64_t kCoopMinT = 8192;  // below this the split-K forms have lower latency
 
@@ -796,34 +662,6 @@ inline size_t coop_ws_bytes(int64_t T, int N, int D) {
   if (N != 4 || T < kCoopMinT || !coop_nch(D, &G)) return 0;
   return align256((size_t)kCoCtlWords * 4) + align256((size_t)coop_max_groups(G) * kCoR * G * kCoRecWords * 16) +
          align256((size_t)T * 24 * 4) + align256((size_t)T * 4) + fwd_y_ws_bytes(T, 4);
-}
-
-// Per-device: does one block of the single-pass kernel fit a CU (so a grid
-// of one block per CU is resident at once on an otherwise idle device)?
-inline bool coop_fits(const void* kernel, int threads, int nch) {
-  static std::atomic<int> cache[64][2];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  std::atomic<int>& slot = cache[dev][nch == 32];
-  int v = slot.load(std::memory_order_relaxed);
-  if (v) return v > 0;
-  int nb = 0;
-  const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1;
-  (void)hipGetLastError();
-  slot.store(ok ? 1 : -1, std::memory_order_relaxed);
-  return ok;
-}
-
-// Limit of every bounded wait, in s_memrealtime ticks (100 MHz): kCoTimeout
-// unless mhc_debug_set_wait_limit set another (a test hook that forces the
-// failure path; it is never read from the environment).
-inline std::atomic<int64_t>& coop_wait_limit_slot() {
-  static std::atomic<int64_t> v{-1};
-  return v;
-}
-inline uint64_t coop_wait_limit() {
-  const int64_t v = coop_wait_limit_slot().load(std::memory_order_relaxed);
-  return v < 0 ? kCoTimeout : (uint64_t)v;
 }
 
 // Runs the single-pass form when it applies (N = 4 bf16 fast path, D with a
@@ -838,14 +676,10 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   const int nch = coop_nch(a.D, &G);
   const size_t need = coop_ws_bytes(a.T, 4, a.D);
   if (!nch || !need || !workspace || workspace_bytes < kPreFwdWsBase + need) return MHC_OK;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return MHC_OK;
-  }
+  if (stream_capturing(st)) return MHC_OK;
   const void* kfn = (const void*)pre_fwd_coop_kernel<32, XS>;
   const int threads = CoCfg<32>::THREADS;
-  if (!coop_fits(kfn, threads, nch)) return MHC_OK;
+  if (!coop_fits(kfn, threads, 0)) return MHC_OK;
   char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
   CoopArgs ca;
   ca.ctl = reinterpret_cast<uint32_t*>(w);

@@ -222,16 +222,36 @@ int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi
  *       bf16 planes, x in one to three) added with Neumaier's compensation;
  *       grad_alpha / grad_base partials likewise.  Results stay deterministic;
  *       grad_x is unchanged.  Costs one more read of x.
- * Unknown flag bits are an error.  Workspace: mhc_pre_bwd_workspace_size.
+ *   MHC_PRE_BWD_TWO_PASS  never the single-pass form below (for comparisons).
+ *   MHC_PRE_BWD_SINGLE_PASS  the single-pass form wherever its conditions
+ *       hold from T >= 8192 on, not only from T >= 32768.
+ * Unknown flag bits, or both pass flags, are an error.  Workspace:
+ * mhc_pre_bwd_workspace_size.
+ *
+ * Single-pass form.  For N = 4 with bf16 x, grad_y and phi, 16-byte aligned
+ * rows, D = 4096 or 7168 .. 8192, T >= 32768 (measured faster than the
+ * two-pass forms there on MI355X, slower below), no grad_x_in, no compensated
+ * mode and no stream capture, x and grad_y are read from HBM once (groups of
+ * CUs of one XCC share each 16-token tile and exchange per-token grad_pre
+ * partials through L2).  Its waits for the other CUs of a group are bounded
+ * (0.25 s without progress); if one gives up, grad_x, grad_phi, grad_alpha
+ * and grad_base are NaN and the kernels write the failure code (> 0) to
+ * *status, else 0.  Other forms leave *status untouched (the caller zeroes
+ * it first).  `status` may be NULL, a device pointer or host-mapped pinned
+ * memory; it is written when the call's work runs.  mhc_pre_bwd and
+ * mhc_pre_bwd_acc run the same forms with status == NULL.
  */
 #define MHC_PRE_BWD_COMPENSATED 1u
+#define MHC_PRE_BWD_TWO_PASS 2u
+#define MHC_PRE_BWD_SINGLE_PASS 4u
 int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
                    const float* alpha, const float* base, const float* inv_rms, const float* mixes,
                    const float* pre, const void* grad_y, const float* grad_post_out,
                    const float* grad_comb_frag, float hc_eps, float clamp_min, float clamp_max,
                    int32_t iter_times, const void* grad_x_in, void* grad_x, float* grad_phi,
-                   float* grad_alpha, float* grad_base, uint32_t flags, void* workspace,
-                   size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream);
+                   float* grad_alpha, float* grad_base, uint32_t flags, int32_t* status,
+                   void* workspace, size_t workspace_bytes, int64_t T, int32_t N, int32_t D,
+                   void* stream);
 
 /*
  * Fused forward of mhc_post (layer l) and mhc_pre_clamp_sinkhorn (layer l+1).

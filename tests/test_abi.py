@@ -111,8 +111,11 @@ def test_error_codes_without_device(lib):
     # pre backward with options: unknown flag bits, overlap, then mhc_pre_bwd's checks
     ex = lambda gin, flags: lib.mhc_pre_bwd_ex(
         dummy, 1, dummy, 1, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 1e-6, 0.0, 0.0, 20,
-        gin, gx, dummy, dummy, dummy, flags, dummy, 16, 16, 4, 64, None)
-    assert ex(None, 2) == -1 and b"flags" in lib.mhc_last_error()
+        gin, gx, dummy, dummy, dummy, flags, None, dummy, 16, 16, 4, 64, None)
+    assert ex(None, 8) == -1 and b"flags" in lib.mhc_last_error()
+    assert ex(None, 6) == -1 and b"together" in lib.mhc_last_error()   # both pass flags
+    assert ex(None, 2) == -1 and b"workspace" in lib.mhc_last_error()  # MHC_PRE_BWD_TWO_PASS is known
+    assert ex(None, 4) == -1 and b"workspace" in lib.mhc_last_error()  # MHC_PRE_BWD_SINGLE_PASS is known
     assert ex(gin_overlap, 1) == -1 and b"overlaps" in lib.mhc_last_error()
     assert ex(None, 1) == -1 and b"workspace" in lib.mhc_last_error()
     assert ex(gin_ok, 0) == -1 and b"workspace" in lib.mhc_last_error()
