@@ -102,6 +102,7 @@ struct CoCfg {
   static constexpr int STREAM = kCoTT * NCH * 16;   // bytes of one stream of a slot
   static constexpr int SLOT = 4 * STREAM;           // bytes of a slot (one tile slice)
   static constexpr int S = 131072 / SLOT;           // LDS slots: 4 or 8 (128 KB)
+  static_assert((S & (S - 1)) == 0, "slot indices are masks");
   static constexpr int A = S - 2;                   // tiles of loads issued ahead (the Y-waves may lag one more)
   static constexpr int DMA = STREAM / 1024;         // direct-to-LDS loads per stream and tile
   static constexpr int STEPS = NCH / 4;             // 32-column MFMA steps per stream
@@ -111,6 +112,7 @@ struct CoCfg {
   static_assert(YB * YW == RB, "row blocks split evenly over the Y-waves");
   static constexpr int THREADS = (kCoLW + YW + kCoPW) * kWave;
   static_assert(kCoR >= 2 * S + 2 * kCoLag + 2, "exchange ring shorter than the lag it must cover");
+  static_assert((kCoR & (kCoR - 1)) == 0 && (kCoPSlots & (kCoPSlots - 1)) == 0, "ring and slot indices are masks");
 };
 
 struct CoopArgs {
@@ -205,47 +207,6 @@ __device__ __forceinline__ void co_lds_rd4x2(u32x4 (&v)[4], uint32_t a0, uint32_
   for (int n = 0; n < 4; ++n) v[n] = u32x4{h[2 * n][0], h[2 * n][1], h[2 * n + 1][0], h[2 * n + 1][1]};
 }
 
-// Poll `nm` <= PVN members' words at byte offset `off0` of the group's ring
-// (member stride kCoRecWords words) until
-// every tag equals `tag`; returns the two
-// values summed in member order (reloading into the caller's registers `v`).
-// The loads are device scope (sc1): they bypass this CU's L1, which may hold
-// stale copies of the ring, and read the XCD's L2, where the writers' stores
-// land.  Lanes with !active take part in the wave's retry vote only.
-template <int PVN>
-__device__ __forceinline__ bool co_poll_sum(u32x4 (&v)[PVN], const __amdgpu_buffer_rsrc_t& ring, uint32_t off0, int nm,
-                                            bool active, uint32_t tag, float& s0, float& s1, uint32_t abort_a,
-                                            uint32_t* status, uint64_t timeout) {
-  const uint64_t deadline = co_now() + timeout;
-  for (;;) {
-    const uint32_t vo = active ? off0 : kBufferOob;
-#pragma unroll
-    for (int i = 0; i < PVN; ++i)
-      if (i < nm) v[i] = __builtin_amdgcn_raw_buffer_load_b128(ring, vo + (uint32_t)(i * kCoRecWords * 16), 0, kCoPolicySc1);
-    bool ok = true;
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < PVN; ++i)
-      if (i < nm) {
-        ok = ok && ((v[i][1] == tag && v[i][3] == tag) || !active);
-        a0 += __uint_as_float(v[i][0]);
-        a1 += __uint_as_float(v[i][2]);
-      }
-    if (!__any(!ok)) {
-      s0 = a0;
-      s1 = a1;
-      return true;
-    }
-    if (co_lds_ld(abort_a)) return false;
-    if (co_now() > deadline) {
-      co_lds_inc(abort_a);
-      co_fail(status, kStPPoll);
-      return false;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
 template <int NCH, bool XS>
 __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopArgs ca) {
   using C = CoCfg<NCH>;
@@ -275,9 +236,12 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   __syncthreads();
   const int group = info[0], ngroups = info[1], member = info[2];
   if (group < 0) return;  // uniform over the block: not a member of a group
-  const int64_t ntiles = (T + kCoTT - 1) / kCoTT;
-  const int64_t nq = (ntiles - group + ngroups - 1) / ngroups;  // tiles of this group
+  // tile and loop indices fit 32 bits (the host bounds T); tile sequence qi
+  // of this group starts at token t0_of(qi)
+  const int ntiles = (int)((T + kCoTT - 1) / kCoTT);
+  const int nq = (ntiles - group + ngroups - 1) / ngroups;  // tiles of this group
   if (nq <= 0) return;
+  auto t0_of = [&](int qi) { return (int64_t)(group + qi * ngroups) * kCoTT; };
   const int slice0 = member * CS;
   u32x4* recw = ca.rec + (size_t)group * kCoR * G * kCoRecWords;  // this group's ring
   const auto ring = rows_rsrc(recw, (int64_t)kCoR * G * kCoRecWords * 16);
@@ -307,11 +271,11 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     // tokens 4 (i / H) + rho (rho = lane / 16), 256 bytes each; lane rho*16 +
     // kp lands chunk 16 (i % H) + (kp ^ token) of its row (XOR swizzle: the
     // MFMA reads of 16 tokens x one chunk hit 16 different bank groups)
-    auto issue = [&](int64_t qi) {
-      const int64_t t0 = (group + qi * ngroups) * kCoTT;
+    auto issue = [&](int qi) {
+      const int64_t t0 = t0_of(qi);
       const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
       const auto rs = rows_rsrc(x + (t0 * 4 + w) * D + slice0, ((int64_t)(nv - 1) * K + CS) * 2);
-      const uint32_t slot = sbase + (uint32_t)((qi % S) * C::SLOT + w * C::STREAM);
+      const uint32_t slot = sbase + (uint32_t)((qi & (S - 1)) * C::SLOT + w * C::STREAM);
       const int rho = lane >> 4, kp = lane & 15;
 #pragma unroll
       for (int i = 0; i < DMA; ++i) {
@@ -331,20 +295,20 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     }
 
     bool alive = true;
-    for (int64_t j = 0; j < (nq < A ? nq : A); ++j) issue(j);
-    for (int64_t j = 0; j < nq && alive; ++j) {
+    for (int j = 0; j < (nq < A ? nq : A); ++j) issue(j);
+    for (int j = 0; j < nq && alive; ++j) {
       if (j + A < nq) {
-        alive = co_wait_ge(c_copied + 4 * (uint32_t)((j + A) % S), (uint32_t)(YW * ((j + A) / S)), c_abort, status,
-                           kStLCopied, to);
+        alive = co_wait_ge(c_copied + 4 * (uint32_t)((j + A) & (S - 1)), (uint32_t)(YW * ((j + A) / S)), c_abort,
+                           status, kStLCopied, to);
         if (!alive) break;
         issue(j + A);
       }
-      const int64_t after = nq - 1 - j < A ? nq - 1 - j : A;
-      co_wait_tiles<DMA, A>((int)after);
-      co_lds_inc(c_landed + 4 * (uint32_t)(j % S));
+      const int after = nq - 1 - j < A ? nq - 1 - j : A;
+      co_wait_tiles<DMA, A>(after);
+      co_lds_inc(c_landed + 4 * (uint32_t)(j & (S - 1)));
 
       // contraction of this stream's 16 x CS slice: fresh MFMA chain
-      const uint32_t sl = sbase + (uint32_t)((j % S) * C::SLOT + w * C::STREAM);
+      const uint32_t sl = sbase + (uint32_t)((j & (S - 1)) * C::SLOT + w * C::STREAM);
       // sum(x^2) on the matrix cores too: the A operand is also the B operand
       // of x x^T (the register layouts coincide), whose diagonal holds each
       // token's sum of squares
@@ -366,8 +330,8 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       const float ssq = e4 == 0 ? gram[0] : e4 == 1 ? gram[1] : e4 == 2 ? gram[2] : gram[3];
 
       // partial -> pbuf[j % 2][w]; the buffer's previous tile must be published
-      const int pb = (int)(j & 1);
-      alive = co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j / 2), c_abort, status, kStLPread, to);
+      const int pb = j & 1;
+      alive = co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j >> 1), c_abort, status, kStLPread, to);
       if (!alive) break;
       const uint32_t pw = lds_addr(&pbuf[pb][w][0]);
 #pragma unroll
@@ -378,11 +342,11 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       if (q == (r >> 2)) co_lds_st(pw + (uint32_t)((4 * kCoTT + r) * 4), ssq);
       // no wait: the count below is raised after these writes (issue order)
       const uint32_t old = co_lds_inc_rtn(c_pcnt + 4 * (uint32_t)pb);
-      if (old == 4u * (uint32_t)(j / 2) + 3u) {
+      if (old == 4u * (uint32_t)(j >> 1) + 3u) {
         // last of the four: add the partials in stream order and publish
         const uint32_t tag = (uint32_t)(j + 1);
         // ring layout [tile][member][word]: a record is one contiguous run
-        const uint32_t dst = (uint32_t)(((j % kCoR) * G + member) * kCoRecWords * 16);  // byte offset in the ring
+        const uint32_t dst = (uint32_t)(((j & (kCoR - 1)) * G + member) * kCoRecWords * 16);  // byte offset in the ring
         const uint32_t p0 = lds_addr(&pbuf[pb][0][0]);
         float2 pr[4][4];
         co_lds_rd_rec(pr, p0 + (uint32_t)(8 * lane),
@@ -442,37 +406,71 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     for (int n = 0; n < 4; ++n) base_n[n] = uniform(a.base[n]);
     const bool pact = lane < kCoYWords + nhw;
     const uint32_t poff = (uint32_t)((lane < kCoYWords ? lane : (pact ? hw0 + lane - kCoYWords : 0)) * 16);
-    auto rec_off = [&](int64_t t) { return (uint32_t)((t % kCoR) * G * kCoRecWords * 16) + poff; };
+    // tile t's records: a range of exactly G members, so loads of members
+    // past G fall outside it and read zeros
+    auto rec_rsrc = [&](int t) {
+      return rows_rsrc(recw + (size_t)(t & (kCoR - 1)) * G * kCoRecWords, (int64_t)G * kCoRecWords * 16);
+    };
     const int sl = pw;
-    for (int64_t u = pw; u < nq; u += kCoPW) {
+    for (int u = pw; u < nq; u += kCoPW) {
       if (!co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to)) break;
-      // two rounds of up to 16 members (register budget), added in member order
+      // every member's words in one round of loads (one L2 round trip),
+      // retried until every tag is this tile's; the sums run in member order
+      // over members 0..15 and 16.., then the two partial sums are added
       const uint32_t tag = (uint32_t)(u + 1);
+      const auto rr = rec_rsrc(u);
       float s0 = 0.f, s1 = 0.f;
       bool alive = true;
+      uint64_t deadline = 0;
+      for (;;) {
+        // the lane's word offset, opaque here so that the 32 member offsets
+        // are formed at each load, not held in registers across the retries
+        uint32_t vb = pact ? poff : kBufferOob;
+        asm volatile("" : "+v"(vb));
+        u32x4 PV[kCoMaxG];
 #pragma unroll
-      for (int h = 0; h < 2 && alive; ++h) {
-        const int mb = 16 * h, nmh = G - mb < 16 ? G - mb : 16;
-        const uint32_t vo = pact ? rec_off(u) + (uint32_t)(mb * kCoRecWords * 16) : kBufferOob;
-        u32x4 PV[16];
+        for (int i = 0; i < kCoMaxG; ++i)
+          PV[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, vb + (uint32_t)(i * kCoRecWords * 16), 0, kCoPolicySc1);
+        // members past G read zeros (their values add nothing, their tag 0
+        // never matches): the G members' words are all current when G tags
+        // match.  A word's two tags are written by one store and read by one
+        // load, so they are equal: one is checked.
+        uint32_t nok = 0;
+        float a0s = 0.f, a1s = 0.f, b0s = 0.f, b1s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          PV[i] = __builtin_amdgcn_raw_buffer_load_b128(ring, i < nmh ? vo : kBufferOob, i * kCoRecWords * 16, kCoPolicySc1);
-        float h0 = 0.f, h1 = 0.f;
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          ok = ok && ((PV[i][1] == tag && PV[i][3] == tag) || !(pact && i < nmh));
-          h0 += __uint_as_float(PV[i][0]);
-          h1 += __uint_as_float(PV[i][2]);
+        for (int i = 0; i < kCoMaxG; ++i) {
+          nok += PV[i][1] == tag ? 1u : 0u;
+          if (i < 16) {
+            a0s += __uint_as_float(PV[i][0]);
+            a1s += __uint_as_float(PV[i][2]);
+          } else {
+            b0s += __uint_as_float(PV[i][0]);
+            b1s += __uint_as_float(PV[i][2]);
+          }
         }
-        if (__any(!ok) && !co_poll_sum<16>(PV, ring, vo, nmh, pact, tag, h0, h1, c_abort, status, to)) alive = false;
-        s0 = h == 0 ? h0 : s0 + h0;
-        s1 = h == 0 ? h1 : s1 + h1;
+        const bool ok = !pact || nok == (uint32_t)G;
+        if (!__any(!ok)) {
+          s0 = a0s + b0s;
+          s1 = a1s + b1s;
+          break;
+        }
+        if (deadline == 0) deadline = co_now() + to;
+        if (co_lds_ld_u(c_abort)) {
+          alive = false;
+          break;
+        }
+        if (co_now() > deadline) {
+          co_lds_inc(c_abort);
+          co_fail(status, kStPPoll);
+          alive = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
       }
       if (!alive) break;
       // the slot's previous tile must be read by every Y-wave
-      if (!co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot, to)) break;
+      if (!co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot, to))
+        break;
       if (pact) {
         tot[sl][2 * lane] = s0;
         tot[sl][2 * lane + 1] = s1;
@@ -519,8 +517,9 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   auto tok_of = [&](int l, int b) -> int { return 4 * ((v + YW * b) / H) + (l >> 4); };
 
   // tile j into Xc
-  auto copy = [&](int64_t j, u32x4 (&Xc)[YB][4]) -> bool {
-    if (!co_wait_ge(c_landed + 4 * (uint32_t)(j % S), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status, kStYLanded, to))
+  auto copy = [&](int j, u32x4 (&Xc)[YB][4]) -> bool {
+    if (!co_wait_ge(c_landed + 4 * (uint32_t)(j & (S - 1)), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status,
+                    kStYLanded, to))
       return false;
 #pragma unroll
     for (int b = 0; b < YB; ++b) {
@@ -529,22 +528,22 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         // kp / 2 and 8 + kp / 2, half kp % 2, each at the lane position
         // chunk ^ token where the direct-to-LDS load put it
         const int l = lane_at_use(), k2 = (l & 15) >> 1, tk = tok_of(l, b);
-        const uint32_t o = sbase + (uint32_t)((j % S) * C::SLOT + (v + YW * b) * 1024 + (l >> 4) * 256 + 8 * (l & 1));
+        const uint32_t o = sbase + (uint32_t)((j & (S - 1)) * C::SLOT + (v + YW * b) * 1024 + (l >> 4) * 256 + 8 * (l & 1));
         co_lds_rd4x2<C::STREAM>(Xc[b], o + (uint32_t)((k2 ^ tk) * 16), o + (uint32_t)(((8 + k2) ^ tk) * 16));
       } else {
-        const uint32_t o = sbase + (uint32_t)((j % S) * C::SLOT + (v + YW * b) * 1024 + lane * 16);
+        const uint32_t o = sbase + (uint32_t)((j & (S - 1)) * C::SLOT + (v + YW * b) * 1024 + lane * 16);
         co_lds_rd4(Xc[b], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
       }
     }
-    co_lds_inc(c_copied + 4 * (uint32_t)(j % S));
+    co_lds_inc(c_copied + 4 * (uint32_t)(j & (S - 1)));
     return true;
   };
 
   // y (and x_scaled) of tile u from Xt with this lane's p / inv: buffer
   // stores against the tile's rows (scalar base, 32-bit offsets; rows past T
   // fall outside the range and are dropped)
-  auto write_y = [&](int64_t u, const u32x4 (&Xt)[YB][4]) {
-    const int64_t t0 = (group + u * ngroups) * kCoTT;
+  auto write_y = [&](int u, const u32x4 (&Xt)[YB][4]) {
+    const int64_t t0 = t0_of(u);
     const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
     const auto ys = rows_rsrc(static_cast<bf16_t*>(a.y) + t0 * D, (int64_t)nv * D * 2);
 #pragma unroll
@@ -602,11 +601,12 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   // heads' share and (designated member) the y values' totals to part.  The
   // loop body is three steps, so the ring never moves between registers.
   static_assert(kCoLag == 2, "three register buffers: tiles j - 2 .. j");
-  auto step = [&](int64_t j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) -> bool {
-    const int64_t t = j - kCoLag;
+  int own = 0;  // (tile t) % G: the member designated for tile t's totals
+  auto step = [&](int j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) -> bool {
+    const int t = j - kCoLag;
     if (j < nq && !copy(j, Xc)) return false;
     if (t >= 0 && t < nq) {
-      const int sl = (int)(t % kCoPSlots);
+      const int sl = t & (kCoPSlots - 1);
       if (!co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums, to))
         return false;
 #pragma unroll
@@ -616,14 +616,15 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         inv[b] = pinv[sl][tok[b]][4];
       }
       const int pv = (v - 1) * kWave + lane;
-      const bool des = (int)(t % G) == member && v >= 1 && pv < 5 * kCoTT;
+      const bool des = own == member && v >= 1 && pv < 5 * kCoTT;
+      own = own + 1 == G ? 0 : own + 1;
       const bool hs = v == 0 && lane < 2 * nhw;
       const float sh = hs ? tot[sl][2 * kCoYWords + lane] : 0.f;
       const float dv = des ? tot[sl][pv] : 0.f;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       co_lds_inc(c_ydone + 4 * (uint32_t)sl);  // slot read
       write_y(t, Xt);
-      const int64_t t0 = (group + t * ngroups) * kCoTT;
+      const int64_t t0 = t0_of(t);
       const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
       const auto ps = rows_rsrc(a.part + t0 * M, (int64_t)nv * M * 4);
       if (hs) {  // this member's share of the heads' values
@@ -644,7 +645,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     return true;
   };
   u32x4 XA[YB][4], XB[YB][4], XC[YB][4];
-  for (int64_t j = 0; j < nq + kCoLag; j += 3) {
+  for (int j = 0; j < nq + kCoLag; j += 3) {
     if (!step(j, XA, XB)) break;
     if (!step(j + 1, XB, XC)) break;
     if (!step(j + 2, XC, XA)) break;
