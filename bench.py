@@ -86,6 +86,37 @@ SINGLE_KERNEL_OPS = {
 
 
 PMC_SUMMARY = os.path.join("profiles", "c5_pmc_traffic.json")
+KERNEL_SUMMARY = os.path.join("profiles", "c5_chain_kernel_stats.json")
+# each operator's main kernel at the headline shape (the rest of an operator's
+# launches are zero fills, the per-token kernel A and fixed-order sums)
+MAIN_KERNEL = {
+    "pre_fwd": "pre_fwd_coop_kernel<32, false>",
+    "post_fwd": "post_fwd_block_kernel<4, bf16_t, true>",
+    "post_bwd": "post_bwd_block_kernel<4, bf16_t, true, false, 1>",
+    "pre_bwd": "pre_bwd_coop_kernel",
+}
+
+
+def profile_kernel_fracs(algo):
+    """Per main kernel: its average launch time in the committed rocprofv3
+    --kernel-trace summary of the headline chain and the fraction of 8 TB/s
+    its operator's algorithmic bytes make at that time.  Profile figures, not
+    a measurement of this run; None without a committed summary."""
+    try:
+        with open(os.path.join(ROOT, KERNEL_SUMMARY)) as f:
+            kern = json.load(f)["kernels"]
+    except (OSError, KeyError, ValueError):
+        return None
+    out = {}
+    for op, name in MAIN_KERNEL.items():
+        k = kern.get(name)
+        if not k:
+            continue
+        gbs = algo[op] / (k["avg_us"] * 1e-6) / 1e9
+        out[name] = {"op": op, "avg_us": k["avg_us"], "algo_GB": round(algo[op] / 1e9, 4),
+                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    return {"source": KERNEL_SUMMARY + " (committed rocprofv3 --kernel-trace summary of this shape, "
+                                       "not measured in this run)", "kernels": out}
 
 
 def profile_traffic():
@@ -530,6 +561,7 @@ def main():
     # roofline of the dominant kernel: the longest of the operators that run
     # as a single kernel (pre_bwd is four kernels; its largest is shorter)
     dominant = max(SINGLE_KERNEL_OPS, key=lambda k: op_stats[k]["ms"])
+    worst = min(op_stats, key=lambda k: op_stats[k]["frac_hbm"])
     dom = op_stats[dominant]
     prof = profile_traffic() if headline else {}
     traffic = prof.get(dominant, {}).get("traffic_bytes")
@@ -559,6 +591,10 @@ def main():
                      "frac": dom["frac_hbm"], "traffic": traffic,
                      "algo_bytes": algo[dominant]},
         "ops": op_stats,
+        # the operator furthest from the HBM roofline in this run (HIP events)
+        "worst_operator": {"op": worst, "frac_hbm": op_stats[worst]["frac_hbm"],
+                           "GBps": op_stats[worst]["GBps"]},
+        "kernel_fracs_profile": profile_kernel_fracs(algo) if headline else None,
         "traffic_over_algorithmic": {"source": PMC_SUMMARY + " (committed rocprofv3 --pmc summary of "
                                                "this shape, not measured in this run)",
                                      **traffic_ratio} if traffic_ratio else None,

@@ -136,7 +136,9 @@ class SinglePassStatus:
     work has finished), blocking in the pre backward and in
     ``FlagOS_mhc.check_errors``."""
 
-    SLOTS = 64
+    # enough that a caller enqueueing far ahead of the GPU never waits for a
+    # word (16 KB of pinned memory)
+    SLOTS = 4096
 
     def __init__(self):
         self._lock = threading.RLock()
