@@ -70,9 +70,9 @@ def _pre_backward(x, phi, alpha, base, inv_rms, mixes, pre, grad_y, grad_post_ou
     (shaped and typed like x) the returned grad_x is grad_x_in + dL/dx,
     accumulated inside the kernel; ``compensated`` selects the compensated
     T-reductions.  ``single_pass``: None lets the library choose (the
-    single-pass form from T >= 32768 where it applies), False keeps the
-    two-pass forms, True takes the single-pass form wherever it applies (from
-    T >= 8192)."""
+    single-pass form wherever it applies: N = 4 bf16, D = 4096 or 7168..8192,
+    T >= 8192), False keeps the two-pass forms, True asks for the single pass
+    explicitly."""
     del norm_eps  # folded into inv_rms
     _lib.require_device("mhc_pre_clamp_sinkhorn_backward", x, phi, alpha, base, inv_rms, mixes,
                         pre, grad_y, grad_post_out, grad_comb_frag, grad_x_in)

@@ -1729,11 +1729,12 @@ struct BwdLayout {
 };
 
 // The single-pass backward: N = 4, bf16 phi, a slice geometry for D and
-// at least kBcMinT tokens (MHC_PRE_BWD_SINGLE_PASS), kBcAutoT without a pass
-// flag.  Measured on MI355X (bf16, D = 7168 unless noted, backward ms,
-// single / two-pass): T = 8192 0.343 / 0.306, T = 16384 at D = 4096 0.346 /
-// 0.340, T = 65536 2.30 / 2.43.
-constexpr int64_t kBcMinT = 8192, kBcAutoT = 32768;
+// at least kBcMinT tokens (below it the two-pass forms' grid fills the chip
+// better), kBcAutoT without a pass flag.  Measured on MI355X (bf16, D = 7168
+// unless noted, backward ms, single / two-pass): T = 8192 0.294 / 0.307, T =
+// 16384 0.526 / 0.587, T = 16384 at D = 4096 0.294 / 0.341, T = 32768 0.987 /
+// 1.192, T = 65536 1.92 / 2.42.
+constexpr int64_t kBcMinT = 8192, kBcAutoT = 8192;
 inline bool bc_shape(int64_t T, int N, int D, int32_t phi_dtype, int* G) {
   return N == 4 && phi_dtype == MHC_DTYPE_BF16 && T >= kBcMinT && coop_nch(D, G);
 }

@@ -84,8 +84,7 @@ constexpr int kBcPollKB = kCoMaxG * kBcChunkWords / 64;  // a wave's poll buffer
 constexpr int kBcMaxGroups = kCoMaxGroups;
 constexpr int kBcThreads = kBcWaves * kWave;
 // status codes: the wait that timed out
-constexpr uint32_t kBcStLanded = 3, kBcStCopied = 4, kBcStPread = 5, kBcStPcnt = 6, kBcStPoll = 7,
-                   kBcStReady = 8, kBcStGdone = 9, kBcStRdone = 10;
+constexpr uint32_t kBcStPoll = 7;
 static_assert(kBcR >= 2 * kBcLag + 4, "exchange ring shorter than the skew it must cover");
 static_assert((kBcR & (kBcR - 1)) == 0 && (kBcSg & (kBcSg - 1)) == 0, "slot indices are masks");
 
@@ -127,6 +126,10 @@ __device__ __forceinline__ void bc_wait_steady(int kg, bool pub) {
 }
 
 __device__ __forceinline__ float bc_ld(uint32_t a) { return __uint_as_float(co_lds_ld(a)); }
+
+// Block barrier after this wave's LDS operations have completed; memory
+// loads in flight (the direct-to-LDS ring) are left running.
+__device__ __forceinline__ void bc_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // An opaque copy of a wave-uniform value: what derives from it (LDS slot and
 // counter addresses) is recomputed where it is used, a scalar add, instead of
@@ -325,17 +328,23 @@ __device__ __forceinline__ void bc_rd_phase2b(float (&ge)[4], float (&m0)[4], fl
   }
 }
 
-// four 4-byte reads (cz, mix, inv, scale without the pre head), one wait
-__device__ __forceinline__ void bc_rd_coef(float& cz, float& mix, float& inv, float& sk, uint32_t ca, uint32_t cb) {
+// The poll buffer's four 1 KB units (the lane's 16 bytes of each, at pa)
+// and four 4-byte reads (cz, mix, inv, scale without the pre head), one wait
+__device__ __forceinline__ void bc_rd_poll(u32x4 (&p)[4], float& cz, float& mix, float& inv, float& sk, uint32_t pa,
+                                           uint32_t ca, uint32_t cb) {
   uint32_t v[4];
   asm volatile(
-      "ds_read_b32 %0, %4 offset:16\n\t"
-      "ds_read_b32 %1, %4 offset:32\n\t"
-      "ds_read_b32 %2, %5 offset:48\n\t"
-      "ds_read_b32 %3, %5 offset:52\n\t"
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:1024\n\t"
+      "ds_read_b128 %2, %8 offset:2048\n\t"
+      "ds_read_b128 %3, %8 offset:3072\n\t"
+      "ds_read_b32 %4, %9 offset:16\n\t"
+      "ds_read_b32 %5, %9 offset:32\n\t"
+      "ds_read_b32 %6, %10 offset:48\n\t"
+      "ds_read_b32 %7, %10 offset:52\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
-      : "v"(ca), "v"(cb)
+      : "=&v"(p[0]), "=&v"(p[1]), "=&v"(p[2]), "=&v"(p[3]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(pa), "v"(ca), "v"(cb)
       : "memory");
   cz = __uint_as_float(v[0]);
   mix = __uint_as_float(v[1]);
@@ -351,8 +360,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   __shared__ __align__(16) float rdy[kBcRS][144];                    // gm[16][4], g[16][4], scale[16]
   __shared__ __align__(16) float pp[2][kBcWaves][kBcTT];             // phase-1 partials
   __shared__ __align__(16) float red[kBcWaves][8];                   // end: the waves' contributions
-  // counters: landed_x[3] 0, landed_g[4] 3, copied[3] 7, pcnt[2] 10,
-  // pread[2] 12, ready[2] 14, rdone[2] 16, gdone[4] 18, abort 22
+  // counters: abort at 22
   __shared__ uint32_t cnt[32];
   __shared__ int info[4];
 
@@ -381,8 +389,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   const auto ring = rows_rsrc(recw, (int64_t)kBcR * G * kBcRecWords * 16);
   const uint32_t xs_l = lds_addr(xs), gs_l = lds_addr(gsl), pb_l = lds_addr(pbuf) + wave * kBcPollKB * 1024;
   const uint32_t rdy_l = lds_addr(&rdy[0][0]), pp_l = lds_addr(&pp[0][0][0]);
-  const uint32_t c_lx = lds_addr(cnt), c_lg = c_lx + 12, c_cp = c_lx + 28, c_pc = c_lx + 40, c_pr = c_lx + 48,
-                 c_rd = c_lx + 56, c_rdone = c_lx + 64, c_gd = c_lx + 72, c_ab = c_lx + 88;
+  const uint32_t c_ab = lds_addr(cnt) + 88;
   const int kg = wave < 3 ? 3 : 2;  // grad_y / per-token loads this wave issues per tile
   constexpr int npoll = kBcPollKB;  // poll loads a wave issues per tile
   const float a0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(a.alpha[0])));
@@ -490,9 +497,15 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   // before this iteration's stores and loads, so it completes after older
   // work only.  Every index is a 32-bit scalar; every wait on a counter is a
   // scalar branch.  A wait that gives up (abort flag and status set) lets
-  // the iteration run to its end on whatever the buffers hold, every later
-  // wait returns at once, and the loop stops after the iteration: the sum
-  // kernel then replaces the outputs with NaN.
+  // the loop run to its end on whatever the buffers hold (every later wait
+  // returns at once, and the loads and stores stay in range); the sum
+  // kernel then replaces the outputs with NaN.  Block barriers order
+  // the waves ((F): the exchange results ready; (I): phase 2 of tile u done,
+  // which frees its grad_y slot and, for tile u + 1, the ready slot of tile
+  // u - 1; (A): tile j landed, which also frees every buffer iteration j - 1
+  // read); every wave runs the same iterations, so each barrier is reached
+  // by all four (the bounded waits end, failed or not); a fourth after
+  // (B) gives the publisher every wave's partials of tile j.
   auto step = [&](int j, u32x4 (&Xr)[2][4]) {
     const int u = j - kBcLag;
     const bool pub_prev = (j & 3) == wave;  // this wave published tile j - 1's record
@@ -513,11 +526,15 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         const uint32_t tag = (uint32_t)(u + 1);
         uint64_t deadline = 0;
         float s0, s1, s2;
+        // lane v < 16 of the chunk: token t = 4 wave + v / 4, stream v % 4
+        const int t = 4 * wave + ((lane & 15) >> 2), nn = lane & 3;
+        const uint32_t cf = gslot + kBcCoef + (uint32_t)(t * 64);
+        float cz, mix, inv, sk;
         for (;;) {
           // lane l: word w = l % 8 of members l / 8 + 8 k, k = 0..3; every
           // valid word of the G members must carry this tile's tag
           u32x4 v[4];
-          lds_read4<1024>(v, bc_opq(pb_l) + (uint32_t)(16 * lane));
+          bc_rd_poll(v, cz, mix, inv, sk, bc_opq(pb_l) + (uint32_t)(16 * lane), cf + 4 * nn, cf);
           uint32_t cur = 0;
 #pragma unroll
           for (int k = 0; k < 4; ++k) cur += (uint32_t)__popcll(__ballot(v[k][3] == tag));
@@ -550,15 +567,13 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         const int src = (lane & 15) / 3, cmp = (lane & 15) % 3;
         const float f0 = __shfl(s0, src, kWave), f1 = __shfl(s1, src, kWave), f2 = __shfl(s2, src, kWave);
         const float gp = cmp == 0 ? f0 : (cmp == 1 ? f1 : f2);
-        const int t = 4 * wave + ((lane & 15) >> 2), nn = lane & 3;
-        const uint32_t cf = gslot + kBcCoef + (uint32_t)(t * 64);
-        float cz, mix, inv, sk;
-        bc_rd_coef(cz, mix, inv, sk, cf + 4 * nn, cf);
         const float gz = gp * cz;
         const float gmv = gz * a0;
         const float sd = group_sum<3>(gmv * mix);
         const float sc = sk - inv * inv * sd * invK;
-        co_wait_ge(bc_opq(c_rdone) + 4 * (uint32_t)rs, (uint32_t)(kBcWaves * (u >> 1)), bc_opq(c_ab), status, kBcStRdone, to);
+        // ready slot rs held tile u - 2's results: every wave finished phase 2
+        // of tile u - 1 (the barrier before (I) of the last iteration), so of
+        // u - 2
         const bool owner = own == member;  // the tile's owner adds its grad_alpha[0] / grad_base terms
         if (lane < 16) {
           co_lds_st(rslot + (uint32_t)(4 * (4 * t + nn)), gmv);
@@ -569,10 +584,9 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           acc_c0 = fmaf(gz, mix, acc_c0);
           acc_b += gz;
         }
-        co_lds_inc(bc_opq(c_rd) + 4 * (uint32_t)rs);
       }
       // ---- (F) wait for the four shares -------------------------------------
-      co_wait_ge(bc_opq(c_rd) + 4 * (uint32_t)rs, (uint32_t)(kBcWaves * ((u >> 1) + 1)), bc_opq(c_ab), status, kBcStReady, to);
+      bc_sync();
     }
     // ---- (G) the next tile's poll (this wave's buffer is free once it has
     // totalled tile u) ---------------------------------------------------------
@@ -664,14 +678,10 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           __builtin_amdgcn_raw_buffer_store_b128(u32x4{o[e][0], o[e][1], o[e][2], o[e][3]}, rgx, off, 0, 2 /* nt */);
         }
       }
-      co_lds_inc(bc_opq(c_gd) + 4 * (uint32_t)(u & (kBcSg - 1)));
-      co_lds_inc(bc_opq(c_rdone) + 4 * (uint32_t)rs);
-      // ---- (I) grad_y / per-token data of tile j + 2 into this slot ---------
-      if (j + 2 < nq) {
-        co_wait_ge(bc_opq(c_gd) + 4 * (uint32_t)(u & (kBcSg - 1)), (uint32_t)(kBcWaves * ((u >> 2) + 1)), bc_opq(c_ab), status,
-                        kBcStGdone, to);
-        issue_g(j + 2);
-      }
+      // ---- (I) every wave done with tile u (its grad_y slot and ready slot),
+      // then grad_y / per-token data of tile j + 2 into the slot ---------------
+      bc_sync();
+      if (j + 2 < nq) issue_g(j + 2);
       own = own + 1 == G ? 0 : own + 1;
     } else if (j + 2 < nq) {
       issue_g(j + 2);  // (I) a slot not used before
@@ -686,18 +696,18 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         bc_wait_steady<30, 2>(kg, pub_prev);
       else
         wait_vmcnt<0>();
-      const uint32_t jm3 = (uint32_t)j % 3u, jd3 = (uint32_t)j / 3u;
-      co_lds_inc(bc_opq(c_lx) + 4 * jm3);
-      co_lds_inc(bc_opq(c_lg) + 4 * (uint32_t)(j & (kBcSg - 1)));
-      co_wait_ge(bc_opq(c_lx) + 4 * jm3, (uint32_t)kBcWaves * (jd3 + 1), bc_opq(c_ab), status, kBcStLanded, to);
-      co_wait_ge(bc_opq(c_lg) + 4 * (uint32_t)(j & (kBcSg - 1)), (uint32_t)(kBcWaves * ((j >> 2) + 1)), bc_opq(c_ab), status,
-                 kBcStLanded, to);
+      // Every wave past this point: tile j's x and grad_y slots landed (each
+      // wave's own loads, the grad_y ones issued first), and every wave is
+      // done with iteration j - 1, so with tile j - 1's x slot (refilled in
+      // (C) below) and with the publisher's reads of the partial buffer of
+      // tile j - 2 (overwritten in (B)).
+      const uint32_t jm3 = (uint32_t)j % 3u;
+      bc_sync();
       // ---- (B) phase 1: copy x, grad_pre partial -------------------------
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(j & (kBcSg - 1)) * kBcGSlot;
       const uint32_t xslot = bc_opq(xs_l) + jm3 * 32 * 1024 + (uint32_t)(n * 8192 + 16 * lane);
       u32x4 gr1[2][4];
       bc_rd_phase1(Xr, gr1, xslot, gslot + (uint32_t)(16 * lane));
-      co_lds_inc(bc_opq(c_cp) + 4 * jm3);
       float pe[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) pe[e] = 0.f;
@@ -712,12 +722,10 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
 #pragma unroll
       for (int e = 0; e < 4; ++e) pe[e] = group_sum<15>(pe[e]);  // the 16 lanes of row q: token 4 q + e
       const int pbi = j & 1;
-      co_wait_ge(bc_opq(c_pr) + 4 * (uint32_t)pbi, (uint32_t)(j >> 1), bc_opq(c_ab), status, kBcStPread, to);
       if (r == 0) co_lds_st4(bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + n) * kBcTT + 4 * q) * 4), floatx4{pe[0], pe[1], pe[2], pe[3]});
-      co_lds_inc(bc_opq(c_pc) + 4 * (uint32_t)pbi);
+      bc_sync();  // every wave's partials of tile j written
       // ---- (D) the record of tile j -----------------------------------------
       if (wave == ((j + 1) & 3)) {
-        co_wait_ge(bc_opq(c_pc) + 4 * (uint32_t)pbi, (uint32_t)(kBcWaves * ((j >> 1) + 1)), bc_opq(c_ab), status, kBcStPcnt, to);
         // lane l < 24: chunk c = l / 6, word w = l % 6 holds values 3 w .. 3 w + 2
         // of the chunk, value v = 4 (token - 4 c) + stream (v < 16)
         const int ck = lane / kBcDataWords, wd = lane % kBcDataWords;
@@ -743,7 +751,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           word[2] = 3 * wd + 2 < 16 ? w2 : 0u;
         }
         word[3] = (uint32_t)(j + 1);
-        co_lds_inc(bc_opq(c_pr) + 4 * (uint32_t)pbi);
         const uint32_t off =
             lane < 4 * kBcDataWords
                 ? (uint32_t)(((((j & (kBcR - 1)) * 4 + ck) * G + member) * kBcChunkWords + wd) * 16)
@@ -753,8 +760,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
       }
       // ---- (C) x of tile j + 2 into the slot of tile j - 1 --------------------
       if (j + 2 < nq) {
-        const uint32_t j2 = (uint32_t)(j + 2);
-        co_wait_ge(bc_opq(c_cp) + 4 * (j2 % 3u), (uint32_t)kBcWaves * (j2 / 3u), bc_opq(c_ab), status, kBcStCopied, to);
         issue_x(j + 2);
       }
     }
@@ -767,7 +772,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
     const int iters = nq + kBcLag;
     for (int j = 0; j < iters; ++j) {
       step(j, XP);
-      if (co_lds_ld_u(bc_opq(c_ab))) break;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll

@@ -224,13 +224,13 @@ int mhc_pre_bwd_acc(const void* x, int32_t x_dtype, const void* phi, int32_t phi
  *       grad_x is unchanged.  Costs one more read of x.
  *   MHC_PRE_BWD_TWO_PASS  never the single-pass form below (for comparisons).
  *   MHC_PRE_BWD_SINGLE_PASS  the single-pass form wherever its conditions
- *       hold from T >= 8192 on, not only from T >= 32768.
+ *       hold (the default choice too).
  * Unknown flag bits, or both pass flags, are an error.  Workspace:
  * mhc_pre_bwd_workspace_size.
  *
  * Single-pass form.  For N = 4 with bf16 x, grad_y and phi, 16-byte aligned
- * rows, D = 4096 or 7168 .. 8192, T >= 32768 (measured faster than the
- * two-pass forms there on MI355X, slower below), no grad_x_in, no compensated
+ * rows, D = 4096 or 7168 .. 8192, T >= 8192 (measured faster than the
+ * two-pass forms there on MI355X), no grad_x_in, no compensated
  * mode and no stream capture, x and grad_y are read from HBM once (groups of
  * CUs of one XCC share each 16-token tile and exchange per-token grad_pre
  * partials through L2).  Its waits for the other CUs of a group are bounded

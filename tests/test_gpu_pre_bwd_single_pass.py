@@ -1,7 +1,7 @@
 """The single-pass pre backward (x and grad_y read from HBM once; N = 4, bf16
-x, grad_y and phi, D = 4096 or 7168 .. 8192), which mhc_pre_bwd_ex runs
-from T >= 32768 without a pass flag and from T >= 8192 with
-MHC_PRE_BWD_SINGLE_PASS, called through the C ABI and through the package.
+x, grad_y and phi, D = 4096 or 7168 .. 8192, T >= 8192), which
+mhc_pre_bwd_ex runs unless MHC_PRE_BWD_TWO_PASS is set (also with
+MHC_PRE_BWD_SINGLE_PASS), called through the C ABI and through the package.
 
 Checked against
   * the two-pass forms (MHC_PRE_BWD_TWO_PASS) over every token: grad_pre is
@@ -103,13 +103,13 @@ def test_single_pass_bwd_parity(T, D):
 
 
 def test_single_pass_bwd_through_package():
-    """Without a pass flag the library takes the single pass from T = 32768
+    """Without a pass flag the library takes the single pass from T = 8192
     (status 0) and the two-pass forms below (status untouched); the
     package's backward (single_pass=None) equals the ABI call bit for bit,
-    single_pass=False the two-pass forms and single_pass=True the single pass
-    at T = 8192."""
+    single_pass=False the two-pass forms and single_pass=True the single
+    pass where it applies."""
     N, D = 4, 7168
-    for T, auto_single in ((32768, True), (8192, False)):
+    for T, auto_single in ((8192, True), (4096, False)):
         x, phi, alpha, base, gy, gpost, gcomb = pre_inputs(T, N, D, seed=3)
         fwd = m.mhc_pre_clamp_sinkhorn(x, phi, alpha, base, need_backward=True, **KW)
         got = m.mhc_pre_clamp_sinkhorn_backward(x, phi, alpha, base, fwd["inv_rms"], None, fwd["mixes"], None,
@@ -123,7 +123,7 @@ def test_single_pass_bwd_through_package():
             pkg = _pre_backward(x, phi, alpha, base, fwd["inv_rms"], fwd["mixes"], fwd["pre"], gy, gpost, gcomb,
                                 *kw, single_pass=sp)
             abi, st = _bwd_abi(x, phi, alpha, base, fwd, gy, gpost, gcomb, two_pass=not sp)
-            assert st == (0 if sp else UNTOUCHED)
+            assert st == (0 if sp and auto_single else UNTOUCHED)
             for a, b in zip(pkg, abi):
                 assert torch.equal(a.reshape(b.shape), b)
         del x, gy, fwd, got, auto, pkg, abi
