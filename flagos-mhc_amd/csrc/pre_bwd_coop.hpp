@@ -25,28 +25,31 @@
 // of the four streams (32 KB of x and 8 KB of grad_y per tile) and keeps them
 // on chip from their one HBM read until grad_x of those columns is written.
 //
-// A block (one per CU) has eight waves, wave w = n + 4 h owning stream n,
-// columns 128 h .. 128 h + 127 of the slice; lane (r, q) holds tokens
-// 4 q .. 4 q + 3 and columns 8 r .. 8 r + 7 of them (the lane layout of the
-// two-pass kernel B, pre_bwd_dma_kernel).  Per tile j:
-//   * waves 0..3 land tile j + 2's x and tile j + 2's grad_y / per-token data
-//     in LDS slots with direct-to-LDS loads (x: 3 slots of 32 KB; grad_y,
-//     grad_mixes rows and coefX: 4 slots of 11 KB);
-//   * phase 1, every wave: copy its x of tile j into a ring of three tiles of
-//     registers (freeing the x slot) and sum grad_y x over its 8 columns per
-//     token, then over the 16 lanes of a row (DPP); the tile's publisher wave
-//     adds the two halves per stream in order and stores the member's record
-//     (64 sums as 22 16-byte words (v, v, v, tag)) to the group's ring;
-//   * phase 2 of tile u = j - 2: the tile's poller wave (one of waves 4..7,
-//     polls issued a tile ahead) reads every member's record of tile u from
-//     L2 (direct-to-LDS loads), adds them in member order, and forms each
-//     token's grad_mixes[0..3], g = grad_mixes inv and scale in LDS; then
-//     every wave builds its MFMA operands from them and kernel A's rows,
-//     accumulates grad_phi (16x16x16, both bf16 planes of g) and gs
-//     (16x16x32) on the matrix cores and writes grad_x once.
-// The records are the only data that cross CUs (352 bytes per member and
-// tile), and they stay in the XCC's L2: tags (tile sequence + 1) carried in
-// every 16-byte word tell a reader that a word has arrived; a word is written
+// A block (one per CU) has four waves, wave n owning stream n's 256 columns
+// of the slice; lane (r, q) holds tokens 4 q .. 4 q + 3 and columns 8 r ..
+// 8 r + 7 of each 128-column half (the lane layout of the two-pass kernel B,
+// pre_bwd_dma_kernel).  Per iteration j (tile j landing, tile u = j - 2 in
+// phase 2):
+//   * direct-to-LDS loads of tile j + 2: x into 3 slots of 32 KB, grad_y,
+//     kernel A's grad_mixes rows and records into 4 slots of 11 KB;
+//   * phase 1 of tile j: copy its x into a ring of two tiles of registers
+//     (freeing the slot) and sum grad_y . x per token over the wave's
+//     columns (v_dot2_f32_bf16), then over the 16 lanes of a row (DPP); the
+//     tile's publisher wave gathers the four streams' partials into the
+//     member's record (16 tokens x 4 streams as 4 chunks of 8 16-byte words,
+//     word w of a chunk (value w, value w + 8, tag, tag)) and stores it to
+//     the group's ring;
+//   * exchange of tile u: wave w polls chunk w of every member's record (4
+//     direct-to-LDS loads, lane = (member, word)), adds over members in a
+//     fixed order and forms each token's grad_mixes[0..3], g = grad_mixes
+//     inv and scale in LDS;
+//   * phase 2 of tile u: grad_phi partial += g^T @ x and grad_x = diag(pre)
+//     grad_y + diag(scale) x + (grad_mixes inv) @ phi on the matrix cores
+//     (16x16x32 MFMAs, both bf16 planes of each fp32 factor), grad_x stored
+//     once.
+// The records are the only data that cross CUs (512 bytes per member and
+// tile), and they stay in the XCC's L2: the tag (tile sequence + 1) in every
+// 16-byte word tells a reader that the word has arrived; a word is written
 // by one store and read by one load, so it never tears.  Each group writes
 // its own grad_phi partial [group][M][K]; the member that owns a tile (tile
 // sequence % G) adds the tile's grad_alpha[0] / grad_base[0..3] terms to its
@@ -54,13 +57,9 @@
 // (deterministic; no atomics on data).
 //
 // Memory-counter accounting.  Vector memory operations complete in issue
-// order.  Waves 0..3 issue the direct-to-LDS loads and their grad_x stores,
-// nothing else, and wait for a tile's loads with s_waitcnt vmcnt(n), n the
-// exact number of operations they issued after them.  Waves 4..7 issue their
-// grad_x stores, the records and the polls (direct-to-LDS, so no load
-// result is held in registers) and wait only for their polls, likewise by
-// exact count; the poll for tile u is issued before that wave's stores of
-// tile u - 1, so it completes without waiting for them.
+// order; each wave waits for a tile's loads and for its poll with s_waitcnt
+// vmcnt(n), n the exact number of operations it issued after them in the
+// steady state (vmcnt(0) near the ends of the loop).
 #pragma once
 
 #include "coop_common.hpp"
@@ -77,8 +76,7 @@ constexpr int kBcCoef = 8 * 1024;         // offset of coefX in a grad_y slot
 constexpr int kBcGm = 9 * 1024;           // offset of the grad_mixes rows [16][24] fp32
 constexpr int kBcRS = 2;                  // ready slots (per-token results of the exchange)
 constexpr int kBcR = 16;                  // exchange ring: tiles per group
-constexpr int kBcDataWords = 6;           // a record chunk: 16 sums (4 tokens x 4 streams) as (v, v, v, tag) words,
-constexpr int kBcChunkWords = 8;          // at a stride of 8 words (words 6, 7 never written or read)
+constexpr int kBcChunkWords = 8;          // a record chunk: 16 sums (4 tokens x 4 streams), word w = (v_w, v_{w+8}, tag, tag)
 constexpr int kBcRecWords = 4 * kBcChunkWords;  // a member's record of a tile: 4 chunks
 constexpr int kBcPollKB = kCoMaxG * kBcChunkWords / 64;  // a wave's poll buffer, 1 KB units (4): 8 members each
 constexpr int kBcMaxGroups = kCoMaxGroups;
@@ -125,12 +123,6 @@ __device__ __forceinline__ void bc_wait_steady(int kg, bool pub) {
   }
 }
 
-__device__ __forceinline__ float bc_ld(uint32_t a) { return __uint_as_float(co_lds_ld(a)); }
-
-// Block barrier after this wave's LDS operations have completed; memory
-// loads in flight (the direct-to-LDS ring) are left running.
-__device__ __forceinline__ void bc_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // An opaque copy of a wave-uniform value: what derives from it (LDS slot and
 // counter addresses) is recomputed where it is used, a scalar add, instead of
 // every derived value being kept live across the main loop, where the
@@ -140,37 +132,15 @@ __device__ __forceinline__ uint32_t bc_opq(uint32_t v) {
   return v;
 }
 
+// Block barrier after this wave's LDS operations have completed; memory
+// loads in flight (the direct-to-LDS ring) are left running.
+__device__ __forceinline__ void bc_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // c + a.lo b.lo + a.hi b.hi for two bf16 pairs (v_dot2c_f32_bf16: the bf16
 // products are exact in fp32)
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-// eight 16-byte reads at a + i * 16 * STRIDE (i = 0..7), complete on return
-template <int STRIDE>
-__device__ __forceinline__ void bc_rd8(u32x4 (&v)[8], uint32_t a) {
-  static_assert(7 * 16 * STRIDE < 65536, "ds_read offset field");
-  asm volatile(
-      "ds_read_b128 %0, %8\n\t"
-      "ds_read_b128 %1, %8 offset:%9\n\t"
-      "ds_read_b128 %2, %8 offset:%10\n\t"
-      "ds_read_b128 %3, %8 offset:%11\n\t"
-      "ds_read_b128 %4, %8 offset:%12\n\t"
-      "ds_read_b128 %5, %8 offset:%13\n\t"
-      "ds_read_b128 %6, %8 offset:%14\n\t"
-      "ds_read_b128 %7, %8 offset:%15\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
-      : "v"(a), "i"(16 * STRIDE), "i"(32 * STRIDE), "i"(48 * STRIDE), "i"(64 * STRIDE), "i"(80 * STRIDE),
-        "i"(96 * STRIDE), "i"(112 * STRIDE)
-      : "memory");
-}
-
-__device__ __forceinline__ u32x4 bc_rd1(uint32_t a) {
-  u32x4 v;
-  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-  return v;
 }
 
 // Phase 1: the lane's x of both halves (8 units from xa, 1 KB apart) and
@@ -198,37 +168,6 @@ __device__ __forceinline__ void bc_rd_phase1(u32x4 (&x)[2][4], u32x4 (&g)[2][4],
         "=&v"(x[1][2]), "=&v"(x[1][3]), "=&v"(g[0][0]), "=&v"(g[0][1]), "=&v"(g[0][2]), "=&v"(g[0][3]),
         "=&v"(g[1][0]), "=&v"(g[1][1]), "=&v"(g[1][2]), "=&v"(g[1][3])
       : "v"(xa), "v"(ga)
-      : "memory");
-}
-
-// sixteen 16-byte reads at a + i * 16 * STRIDE, one wait
-template <int STRIDE>
-__device__ __forceinline__ void bc_rd16(u32x4 (&v)[16], uint32_t a) {
-  static_assert(15 * 16 * STRIDE < 65536, "ds_read offset field");
-  asm volatile(
-      "ds_read_b128 %0, %16\n\t"
-      "ds_read_b128 %1, %16 offset:%17\n\t"
-      "ds_read_b128 %2, %16 offset:%18\n\t"
-      "ds_read_b128 %3, %16 offset:%19\n\t"
-      "ds_read_b128 %4, %16 offset:%20\n\t"
-      "ds_read_b128 %5, %16 offset:%21\n\t"
-      "ds_read_b128 %6, %16 offset:%22\n\t"
-      "ds_read_b128 %7, %16 offset:%23\n\t"
-      "ds_read_b128 %8, %16 offset:%24\n\t"
-      "ds_read_b128 %9, %16 offset:%25\n\t"
-      "ds_read_b128 %10, %16 offset:%26\n\t"
-      "ds_read_b128 %11, %16 offset:%27\n\t"
-      "ds_read_b128 %12, %16 offset:%28\n\t"
-      "ds_read_b128 %13, %16 offset:%29\n\t"
-      "ds_read_b128 %14, %16 offset:%30\n\t"
-      "ds_read_b128 %15, %16 offset:%31\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7]),
-        "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]),
-        "=&v"(v[15])
-      : "v"(a), "i"(16 * STRIDE), "i"(32 * STRIDE), "i"(48 * STRIDE), "i"(64 * STRIDE), "i"(80 * STRIDE),
-        "i"(96 * STRIDE), "i"(112 * STRIDE), "i"(128 * STRIDE), "i"(144 * STRIDE), "i"(160 * STRIDE),
-        "i"(176 * STRIDE), "i"(192 * STRIDE), "i"(208 * STRIDE), "i"(224 * STRIDE), "i"(240 * STRIDE)
       : "memory");
 }
 
@@ -283,9 +222,8 @@ __device__ __forceinline__ u32x4 bc_diag2(float v, int r, int q) {
 // columns 2 (c / 2), + 1 of token e) as the B operand of a 16x16x32 MFMA
 // whose k = 2 e + p runs over the lane's tokens e and two planes p of the A
 // operand: dword e = the token's value twice.
-template <int C>
-__device__ __forceinline__ u32x4 bc_col2(const u32x4 (&m)[4]) {
-  constexpr uint32_t sel = (C & 1) ? 0x03020302u : 0x01000100u;
+__device__ __forceinline__ u32x4 bc_col2(const u32x4 (&m)[4], int C) {
+  const uint32_t sel = (C & 1) ? 0x03020302u : 0x01000100u;
   const int w = C >> 1;
   return u32x4{__builtin_amdgcn_perm(m[0][w], m[0][w], sel), __builtin_amdgcn_perm(m[1][w], m[1][w], sel),
                __builtin_amdgcn_perm(m[2][w], m[2][w], sel), __builtin_amdgcn_perm(m[3][w], m[3][w], sel)};
@@ -445,12 +383,10 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   auto issue_poll = [&](int u) {
 #pragma unroll
     for (int k = 0; k < npoll; ++k) {
-      // lane l: word l % 8 of member 8 k + l / 8 (words past kBcDataWords and
-      // members past G read zeros)
+      // lane l: word l % 8 of member 8 k + l / 8 (members past G read zeros)
       const int f = 64 * k + lane, i = f / kBcChunkWords;
-      const uint32_t off = i < G && (lane & (kBcChunkWords - 1)) < kBcDataWords
-                               ? (uint32_t)((((u & (kBcR - 1)) * 4 + wave) * G * kBcChunkWords + f) * 16)
-                               : kBufferOob;
+      const uint32_t off =
+          i < G ? (uint32_t)((((u & (kBcR - 1)) * 4 + wave) * G * kBcChunkWords + f) * 16) : kBufferOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ring, (lds_void_t*)(uintptr_t)(bc_opq(pb_l) + k * 1024), 16, off, 0, 0,
                                                kCoPolicySc1);
     }
@@ -525,7 +461,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           wait_vmcnt<0>();
         const uint32_t tag = (uint32_t)(u + 1);
         uint64_t deadline = 0;
-        float s0, s1, s2;
+        float s0, s1;
         // lane v < 16 of the chunk: token t = 4 wave + v / 4, stream v % 4
         const int t = 4 * wave + ((lane & 15) >> 2), nn = lane & 3;
         const uint32_t cf = gslot + kBcCoef + (uint32_t)(t * 64);
@@ -537,20 +473,17 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           bc_rd_poll(v, cz, mix, inv, sk, bc_opq(pb_l) + (uint32_t)(16 * lane), cf + 4 * nn, cf);
           uint32_t cur = 0;
 #pragma unroll
-          for (int k = 0; k < 4; ++k) cur += (uint32_t)__popcll(__ballot(v[k][3] == tag));
-          if (cur == (uint32_t)(kBcDataWords * G)) {
-            // members past G and words past kBcDataWords are zeros; the sum
-            // runs over k, then over the lanes of the same word (l ^ 8,
-            // l ^ 16, l ^ 32): a fixed order
+          for (int k = 0; k < 4; ++k) cur += (uint32_t)__popcll(__ballot(v[k][2] == tag));
+          if (cur == (uint32_t)(kBcChunkWords * G)) {
+            // members past G are zeros; the sum runs over k, then over the
+            // lanes of the same word (l ^ 8, l ^ 16, l ^ 32): a fixed order
             s0 = (__uint_as_float(v[0][0]) + __uint_as_float(v[1][0])) + (__uint_as_float(v[2][0]) + __uint_as_float(v[3][0]));
             s1 = (__uint_as_float(v[0][1]) + __uint_as_float(v[1][1])) + (__uint_as_float(v[2][1]) + __uint_as_float(v[3][1]));
-            s2 = (__uint_as_float(v[0][2]) + __uint_as_float(v[1][2])) + (__uint_as_float(v[2][2]) + __uint_as_float(v[3][2]));
             s0 = group_sum<56>(s0);
             s1 = group_sum<56>(s1);
-            s2 = group_sum<56>(s2);
             break;
           }
-          s0 = s1 = s2 = 0.f;
+          s0 = s1 = 0.f;
           if (deadline == 0) deadline = co_now() + to;
           if (co_lds_ld_u(bc_opq(c_ab))) break;
           if (co_now() > deadline) {
@@ -562,11 +495,9 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           issue_poll(u);
           wait_vmcnt<0>();
         }
-        // lane v < 16: value v of the chunk (token t = 4 wave + v / 4, stream v % 4),
-        // from lane v / 3 (word v / 3), component v % 3
-        const int src = (lane & 15) / 3, cmp = (lane & 15) % 3;
-        const float f0 = __shfl(s0, src, kWave), f1 = __shfl(s1, src, kWave), f2 = __shfl(s2, src, kWave);
-        const float gp = cmp == 0 ? f0 : (cmp == 1 ? f1 : f2);
+        // lane v < 16 holds word v % 8 of the chunk, whose components are
+        // values v % 8 and v % 8 + 8: value v is component v / 8
+        const float gp = (lane & 8) ? s1 : s0;
         const float gz = gp * cz;
         const float gmv = gz * a0;
         const float sd = group_sum<3>(gmv * mix);
@@ -647,29 +578,37 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         // (grad_mixes inv) @ phi in one 16x16 accumulator; every MFMA is
         // 16x16x32 (k over tokens x planes for the first three, over m for gs)
         uint32_t o[4][4];
-        auto col = [&](auto cc) -> floatx4 {
-          constexpr int c = decltype(cc)::value;
-          const u32x4 xd = bc_col2<c>(Xr[hh]), yd = bc_col2<c>(grh[hh]);
+        // four columns at a time, the MFMAs in step order so that four
+        // independent accumulations interleave (the gs products first: their
+        // operands are ready before the x / grad_y columns are formed)
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt) ph[hh][mt][c] = mfma16x16x32(as_bf16x8(gt[mt]), as_bf16x8(xd), ph[hh][mt][c]);
-          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = mfma16x16x32(as_bf16x8(dpre), as_bf16x8(yd), acc);
-          acc = mfma16x16x32(as_bf16x8(dsc), as_bf16x8(xd), acc);
-          acc = mfma16x16x32(as_bf16x8(gA0), as_bf16x8(pb[hh][c]), acc);
-          acc = mfma16x16x32(as_bf16x8(gA1), as_bf16x8(pb[hh][c]), acc);
-          return acc;
-        };
-        auto pair = [&](auto ww) {
-          constexpr int w = decltype(ww)::value;
-          const floatx4 c0 = col(std::integral_constant<int, 2 * w>{});
-          const floatx4 c1 = col(std::integral_constant<int, 2 * w + 1>{});
+        for (int k = 0; k < 2; ++k) {
+          u32x4 xd[4], yd[4];
+          floatx4 acc[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e][w] = pack_bf16x2(c0[e], c1[e]);
-        };
-        pair(std::integral_constant<int, 0>{});
-        pair(std::integral_constant<int, 1>{});
-        pair(std::integral_constant<int, 2>{});
-        pair(std::integral_constant<int, 3>{});
+          for (int i = 0; i < 4; ++i) {
+            xd[i] = bc_col2(Xr[hh], 4 * k + i);
+            yd[i] = bc_col2(grh[hh], 4 * k + i);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = mfma16x16x32(as_bf16x8(gA0), as_bf16x8(pb[hh][4 * k + i]), floatx4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+              ph[hh][mt][4 * k + i] = mfma16x16x32(as_bf16x8(gt[mt]), as_bf16x8(xd[i]), ph[hh][mt][4 * k + i]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = mfma16x16x32(as_bf16x8(gA1), as_bf16x8(pb[hh][4 * k + i]), acc[i]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = mfma16x16x32(as_bf16x8(dpre), as_bf16x8(yd[i]), acc[i]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = mfma16x16x32(as_bf16x8(dsc), as_bf16x8(xd[i]), acc[i]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e][2 * k] = pack_bf16x2(acc[0][e], acc[1][e]);
+            o[e][2 * k + 1] = pack_bf16x2(acc[2][e], acc[3][e]);
+          }
+        }
         const int colh = slice0 + 128 * hh + 8 * r;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -726,33 +665,28 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
       bc_sync();  // every wave's partials of tile j written
       // ---- (D) the record of tile j -----------------------------------------
       if (wave == ((j + 1) & 3)) {
-        // lane l < 24: chunk c = l / 6, word w = l % 6 holds values 3 w .. 3 w + 2
-        // of the chunk, value v = 4 (token - 4 c) + stream (v < 16)
-        const int ck = lane / kBcDataWords, wd = lane % kBcDataWords;
+        // lane l < 32: chunk c = l / 8, word w = l % 8 holds values w and w + 8
+        // of the chunk, value v = 4 (token - 4 c) + stream
+        const int ck = (lane >> 3) & 3, wd = lane & 7;
         u32x4 word;
         {
-          uint32_t ad[3];
-#pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            const int v = 3 * wd + k, vv = v < 16 ? v : 15;
-            ad[k] = bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + (vv & 3)) * kBcTT + 4 * (ck & 3) + (vv >> 2)) * 4);
-          }
-          uint32_t w0, w1, w2;
+          // value w: stream w % 4 of token 4 c + w / 4; value w + 8: the same
+          // stream, two tokens later
+          const uint32_t ad = bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + (wd & 3)) * kBcTT + 4 * ck + (wd >> 2)) * 4);
+          uint32_t w0, w1;
           asm volatile(
-              "ds_read_b32 %0, %3\n\t"
-              "ds_read_b32 %1, %4\n\t"
-              "ds_read_b32 %2, %5\n\t"
+              "ds_read_b32 %0, %2\n\t"
+              "ds_read_b32 %1, %2 offset:8\n\t"
               "s_waitcnt lgkmcnt(0)"
-              : "=&v"(w0), "=&v"(w1), "=&v"(w2)
-              : "v"(ad[0]), "v"(ad[1]), "v"(ad[2])
+              : "=&v"(w0), "=&v"(w1)
+              : "v"(ad)
               : "memory");
-          word[0] = 3 * wd < 16 ? w0 : 0u;
-          word[1] = 3 * wd + 1 < 16 ? w1 : 0u;
-          word[2] = 3 * wd + 2 < 16 ? w2 : 0u;
+          word[0] = w0;
+          word[1] = w1;
         }
-        word[3] = (uint32_t)(j + 1);
+        word[2] = word[3] = (uint32_t)(j + 1);
         const uint32_t off =
-            lane < 4 * kBcDataWords
+            lane < 4 * kBcChunkWords
                 ? (uint32_t)(((((j & (kBcR - 1)) * 4 + ck) * G + member) * kBcChunkWords + wd) * 16)
                 : kBufferOob;
         // default policy: the line stays in this XCC's L2, where the readers' loads find it
