@@ -294,13 +294,11 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       aoff[s] = (uint32_t)((H * (r / 4) + c / 16) * 1024 + (16 * (r % 4) + ((c % 16) ^ r)) * 16);
     }
 
-    bool alive = true;
     for (int j = 0; j < (nq < A ? nq : A); ++j) issue(j);
-    for (int j = 0; j < nq && alive; ++j) {
+    for (int j = 0; j < nq; ++j) {
       if (j + A < nq) {
-        alive = co_wait_ge(c_copied + 4 * (uint32_t)((j + A) & (S - 1)), (uint32_t)(YW * ((j + A) / S)), c_abort,
-                           status, kStLCopied, to);
-        if (!alive) break;
+        co_wait_ge(c_copied + 4 * (uint32_t)((j + A) & (S - 1)), (uint32_t)(YW * ((j + A) / S)), c_abort, status,
+                   kStLCopied, to);
         issue(j + A);
       }
       const int after = nq - 1 - j < A ? nq - 1 - j : A;
@@ -331,8 +329,7 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
 
       // partial -> pbuf[j % 2][w]; the buffer's previous tile must be published
       const int pb = j & 1;
-      alive = co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j >> 1), c_abort, status, kStLPread, to);
-      if (!alive) break;
+      co_wait_ge(c_pread + 4 * (uint32_t)pb, (uint32_t)(j >> 1), c_abort, status, kStLPread, to);
       const uint32_t pw = lds_addr(&pbuf[pb][w][0]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
@@ -413,14 +410,13 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     };
     const int sl = pw;
     for (int u = pw; u < nq; u += kCoPW) {
-      if (!co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to)) break;
+      co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to);
       // every member's words in one round of loads (one L2 round trip),
       // retried until every tag is this tile's; the sums run in member order
       // over members 0..15 and 16.., then the two partial sums are added
       const uint32_t tag = (uint32_t)(u + 1);
       const auto rr = rec_rsrc(u);
       float s0 = 0.f, s1 = 0.f;
-      bool alive = true;
       uint64_t deadline = 0;
       for (;;) {
         // the lane's word offset, opaque here so that the 32 member offsets
@@ -455,22 +451,16 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
           break;
         }
         if (deadline == 0) deadline = co_now() + to;
-        if (co_lds_ld_u(c_abort)) {
-          alive = false;
-          break;
-        }
+        if (co_lds_ld_u(c_abort)) break;
         if (co_now() > deadline) {
           co_lds_inc(c_abort);
           co_fail(status, kStPPoll);
-          alive = false;
           break;
         }
         __builtin_amdgcn_s_sleep(1);
       }
-      if (!alive) break;
       // the slot's previous tile must be read by every Y-wave
-      if (!co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot, to))
-        break;
+      co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot, to);
       if (pact) {
         tot[sl][2 * lane] = s0;
         tot[sl][2 * lane + 1] = s1;
@@ -517,10 +507,9 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   auto tok_of = [&](int l, int b) -> int { return 4 * ((v + YW * b) / H) + (l >> 4); };
 
   // tile j into Xc
-  auto copy = [&](int j, u32x4 (&Xc)[YB][4]) -> bool {
-    if (!co_wait_ge(c_landed + 4 * (uint32_t)(j & (S - 1)), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status,
-                    kStYLanded, to))
-      return false;
+  auto copy = [&](int j, u32x4 (&Xc)[YB][4]) {
+    co_wait_ge(c_landed + 4 * (uint32_t)(j & (S - 1)), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status, kStYLanded,
+               to);
 #pragma unroll
     for (int b = 0; b < YB; ++b) {
       if constexpr (XS) {
@@ -536,7 +525,6 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       }
     }
     co_lds_inc(c_copied + 4 * (uint32_t)(j & (S - 1)));
-    return true;
   };
 
   // y (and x_scaled) of tile u from Xt with this lane's p / inv: buffer
@@ -602,13 +590,12 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   // loop body is three steps, so the ring never moves between registers.
   static_assert(kCoLag == 2, "three register buffers: tiles j - 2 .. j");
   int own = 0;  // (tile t) % G: the member designated for tile t's totals
-  auto step = [&](int j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) -> bool {
+  auto step = [&](int j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) {
     const int t = j - kCoLag;
-    if (j < nq && !copy(j, Xc)) return false;
+    if (j < nq) copy(j, Xc);
     if (t >= 0 && t < nq) {
       const int sl = t & (kCoPSlots - 1);
-      if (!co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums, to))
-        return false;
+      co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums, to);
 #pragma unroll
       for (int b = 0; b < YB; ++b) {
 #pragma unroll
@@ -642,13 +629,12 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         }
       }
     }
-    return true;
   };
   u32x4 XA[YB][4], XB[YB][4], XC[YB][4];
   for (int j = 0; j < nq + kCoLag; j += 3) {
-    if (!step(j, XA, XB)) break;
-    if (!step(j + 1, XB, XC)) break;
-    if (!step(j + 2, XC, XA)) break;
+    step(j, XA, XB);
+    step(j + 1, XB, XC);
+    step(j + 2, XC, XA);
   }
 }
 
