@@ -64,7 +64,9 @@ def build(verbose: bool = False) -> str:
                 if rc:
                     raise RuntimeError(f"hipcc failed on {src}")
         tmp_so = OUT + ".tmp"
-        rc, out = _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_so])
+        # --no-undefined: a kernel whose host stub the compiler did not emit
+        # fails here rather than when the library is loaded
+        rc, out = _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *objs, "-o", tmp_so])
         if rc:
             print(out, file=sys.stderr)
             raise RuntimeError("link of libmhc_amd.so failed")

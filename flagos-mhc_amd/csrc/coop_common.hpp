@@ -93,20 +93,26 @@ __device__ __forceinline__ void co_fail(uint32_t* status, uint32_t code) {
 }
 // Wait until the LDS counter at `a` reaches `target` (or the block aborts /
 // `timeout` ticks pass without it: then false, with the abort flag and
-// status set).
+// status set).  A waiting wave shares its SIMD's issue slots with the waves
+// doing the work, so the loop is short: it sleeps SLEEP x 64 clocks between
+// reads of the counter and looks at the abort flag and the clock every
+// eighth read only.
+template <int SLEEP = 1>
 __device__ __forceinline__ bool co_wait_ge(uint32_t a, uint32_t target, uint32_t abort_a, uint32_t* status,
                                            uint32_t code, uint64_t timeout) {
   if (co_lds_ld_u(a) >= target) return true;
   const uint64_t deadline = co_now() + timeout;
-  for (;;) {
+  for (uint32_t i = 1;; ++i) {
+    __builtin_amdgcn_s_sleep(SLEEP);
     if (co_lds_ld_u(a) >= target) return true;
-    if (co_lds_ld_u(abort_a)) return false;
-    if (co_now() > deadline) {
-      co_lds_inc(abort_a);
-      co_fail(status, code);
-      return false;
+    if ((i & 7u) == 0u) {
+      if (co_lds_ld_u(abort_a)) return false;
+      if (co_now() > deadline) {
+        co_lds_inc(abort_a);
+        co_fail(status, code);
+        return false;
+      }
     }
-    __builtin_amdgcn_s_sleep(1);
   }
 }
 

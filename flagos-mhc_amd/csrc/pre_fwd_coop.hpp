@@ -103,7 +103,13 @@ struct CoCfg {
   static constexpr int SLOT = 4 * STREAM;           // bytes of a slot (one tile slice)
   static constexpr int S = 131072 / SLOT;           // LDS slots: 4 or 8 (128 KB)
   static_assert((S & (S - 1)) == 0, "slot indices are masks");
-  static constexpr int A = S - 2;                   // tiles of loads issued ahead (the Y-waves may lag one more)
+  // tiles of loads issued ahead: at most S - 2 (the Y-waves may lag one
+  // more).  The P-waves' exchange reads share the CU's vector memory path
+  // with the direct-to-LDS loads, and with loads two tiles ahead one round
+  // of them measured 1.4 - 2.5 us although the records sat in L2.  Without
+  // x_scaled one tile ahead measured 3-5% faster than two at the same HBM
+  // read rate; with x_scaled's larger stores two stay slightly faster.
+  static constexpr int A_MAX = S - 2;
   static constexpr int DMA = STREAM / 1024;         // direct-to-LDS loads per stream and tile
   static constexpr int STEPS = NCH / 4;             // 32-column MFMA steps per stream
   static constexpr int RB = NCH / 4;                // 1 KB row blocks per stream slot (4 tokens x 256 bytes)
@@ -210,7 +216,8 @@ __device__ __forceinline__ void co_lds_rd4x2(u32x4 (&v)[4], uint32_t a0, uint32_
 template <int NCH, bool XS>
 __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopArgs ca) {
   using C = CoCfg<NCH>;
-  constexpr int S = C::S, A = C::A, H = C::H, DMA = C::DMA, STEPS = C::STEPS, CS = C::CS, YW = C::YW, YB = C::YB;
+  constexpr int A = XS ? C::A_MAX : 1;
+  constexpr int S = C::S, H = C::H, DMA = C::DMA, STEPS = C::STEPS, CS = C::CS, YW = C::YW, YB = C::YB;
   constexpr int M = 24;
   __shared__ __align__(1024) u32x4 slots[S * C::SLOT / 16];
   __shared__ __align__(16) float pbuf[2][kCoLW][kCoTT * kCoVals];   // L-wave partials of a tile (two tiles)
@@ -270,18 +277,29 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     // direct-to-LDS loads of tile sequence qi, stream w: instruction i moves
     // tokens 4 (i / H) + rho (rho = lane / 16), 256 bytes each; lane rho*16 +
     // kp lands chunk 16 (i % H) + (kp ^ token) of its row (XOR swizzle: the
-    // MFMA reads of 16 tokens x one chunk hit 16 different bank groups)
+    // MFMA reads of 16 tokens x one chunk hit 16 different bank groups).
+    // Tiles are issued in sequence order, so the tile's first row is a
+    // running pointer.  The range ends with the slice of the tile's last
+    // token: rows past T (offsets >= nv K 2 > (nv - 1) K 2 + 2 CS) read zeros.
+    int iss_t0 = group * kCoTT;  // first token of the next tile issued
+    const bf16_t* iss_x = x + ((int64_t)iss_t0 * 4 + w) * D + slice0;
+    const int64_t iss_step = (int64_t)ngroups * kCoTT * K;  // elements between a group's tiles
+    uint32_t ioff[DMA];
+#pragma unroll
+    for (int i = 0; i < DMA; ++i) {
+      const int tok = 4 * (i / H) + (lane >> 4);
+      ioff[i] = (uint32_t)((tok * K + 8 * (16 * (i % H) + ((lane & 15) ^ tok))) * 2);
+    }
     auto issue = [&](int qi) {
-      const int64_t t0 = t0_of(qi);
-      const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
-      const auto rs = rows_rsrc(x + (t0 * 4 + w) * D + slice0, ((int64_t)(nv - 1) * K + CS) * 2);
+      const int64_t left = T - iss_t0;
+      const int nv = left < kCoTT ? (int)left : kCoTT;
+      const auto rs = rows_rsrc(iss_x, ((int64_t)(nv - 1) * K + CS) * 2);
+      iss_t0 += ngroups * kCoTT;
+      iss_x += iss_step;
       const uint32_t slot = sbase + (uint32_t)((qi & (S - 1)) * C::SLOT + w * C::STREAM);
-      const int rho = lane >> 4, kp = lane & 15;
 #pragma unroll
       for (int i = 0; i < DMA; ++i) {
-        const int tok = 4 * (i / H) + rho;
-        const int c = 16 * (i % H) + (kp ^ tok);
-        const uint32_t off = tok < nv ? (uint32_t)(((int64_t)tok * K + 8 * c) * 2) : kBufferOob;
+        const uint32_t off = ioff[i];
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(uintptr_t)(slot + i * 1024), 16, off, 0, 0,
                                                  2 /* nt */);
       }
@@ -324,8 +342,8 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         }
       }
       // token r's sum of squares: row r of column r, element r % 4 of lane (r, r / 4)
-      const int e4 = r & 3;
-      const float ssq = e4 == 0 ? gram[0] : e4 == 1 ? gram[1] : e4 == 2 ? gram[2] : gram[3];
+      const float g01 = (r & 1) ? gram[1] : gram[0], g23 = (r & 1) ? gram[3] : gram[2];
+      const float ssq = (r & 2) ? g23 : g01;
 
       // partial -> pbuf[j % 2][w]; the buffer's previous tile must be published
       const int pb = j & 1;
@@ -410,14 +428,16 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     };
     const int sl = pw;
     for (int u = pw; u < nq; u += kCoPW) {
-      co_wait_ge(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to);
+      // this CU's own record comes a few tiles after the previous tile this
+      // wave took (a wait of 2 - 3 us measured): fewer, longer sleeps
+      co_wait_ge<4>(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to);
+      const uint32_t tag = (uint32_t)(u + 1);
+      const auto rr = rec_rsrc(u);
+      uint64_t deadline = 0;
       // every member's words in one round of loads (one L2 round trip),
       // retried until every tag is this tile's; the sums run in member order
       // over members 0..15 and 16.., then the two partial sums are added
-      const uint32_t tag = (uint32_t)(u + 1);
-      const auto rr = rec_rsrc(u);
       float s0 = 0.f, s1 = 0.f;
-      uint64_t deadline = 0;
       for (;;) {
         // the lane's word offset, opaque here so that the 32 member offsets
         // are formed at each load, not held in registers across the retries
