@@ -14,36 +14,42 @@
 // y of those columns is written.  A block (one per CU) has three kinds of
 // waves:
 //   L-waves (one per stream) land the slice in an LDS slot by direct-to-LDS
-//     loads (two tiles ahead), contract it with their phi columns on MFMA
-//     (16 tokens x 32 m x 256 k) and form the sums of squares; the last of
-//     the four adds the four partials in stream order and publishes the
-//     member's record (16 tokens x 25 sums) to the group's exchange ring;
-//   P-waves (four, tiles taken round robin) read, once this CU has published
-//     a tile, the words y needs (four pre mixes and the sum of squares per
-//     token) and this member's share of the heads' mixes from every member's
-//     record, add them in member order, and leave the totals and each
-//     token's pre / inv_rms (rms_inv / pre_gate, as the finalize kernel) in
-//     LDS;
+//     loads (one tile ahead, two with x_scaled), contract it with their phi
+//     columns on MFMA (16 tokens x 32 m x 256 k) and form the sums of
+//     squares; the last of the four adds the four partials in stream order
+//     and publishes the member's record (16 tokens x 25 sums) to the group's
+//     exchange ring;
+//   P-waves (four, tiles taken round robin) total the group's records in two
+//     steps once this CU has published a tile: a reduce-scatter (member c
+//     reads its share [200 c / G, 200 (c + 1) / G) of the record words from
+//     every member, adds them over the members and publishes the totals to
+//     the group's totals ring) and a gather (the 40 words y needs, the four
+//     pre mixes and the sum of squares of each token, read from their
+//     owners' totals); they leave those totals, this member's share and
+//     each token's pre / inv_rms (rms_inv / pre_gate, as the finalize
+//     kernel) in LDS;
 //   Y-waves copy each landed slice into a ring of three tiles of registers
 //     (freeing the LDS slot) and, two tiles later, write y (and the optional
-//     fp32 x_scaled) of their columns with the P-waves' pre / inv_rms, this
-//     member's share of the heads' totals, and (for the tile's designated
-//     member, tile sequence % G) the y values' totals to the [T][M] / [T]
-//     buffers that pre_fwd_finalize_kernel turns into mixes, inv_rms, the
-//     heads and Sinkhorn afterwards.
-// Loads and stores live in different waves (P-waves only load, Y-waves only
-// store): with both in flight the compiler waits for the memory counter to
-// reach zero wherever one load is needed, which puts a store round trip into
+//     fp32 x_scaled) of their columns with the P-waves' pre / inv_rms and
+//     this member's share of the totals to the [T][M] / [T] buffers that
+//     pre_fwd_finalize_kernel turns into mixes, inv_rms, the heads and
+//     Sinkhorn afterwards.
+// Loads and stores live in different waves (P-waves load and store one
+// totals word a lane per tile, Y-waves only store): with loads and stores
+// in flight together the compiler waits for the memory counter to reach
+// zero wherever one load is needed, which puts a store round trip into
 // every tile.  x is read from HBM once; only the 3.2 KB records per member
-// and tile cross CUs, and they stay in the XCC's L2.
+// and tile and the group's 3.2 KB of totals cross CUs, and they stay in the
+// XCC's L2.
 //
 // Exchange.  A record is 200 16-byte words, each two (value, tag) pairs; the
 // tag is the tile's sequence number in its group plus one, so a reader knows
 // a value has arrived from its tag alone, with no flags, counters or fences
 // (one word is written by one store and read by one load, so it never
-// tears).  The ring (kCoR tiles per group) and the control words are zeroed
-// before every launch.  Records are stored with the default policy (the
-// lines stay in the writer's XCC L2) and read with device-scope (sc1) loads,
+// tears); the totals ring uses the same words.  The rings (kCoR tiles per
+// group) and the control words are zeroed before every launch.  Records and
+// totals are stored with the default policy (the lines stay in the writer's
+// XCC L2) and read with device-scope (sc1) loads,
 // which skip the reader's CU L1 (it may hold stale copies of the ring) and
 // find them in that L2: every member of a group sits on one XCC.
 // Membership comes from the XCC_ID hardware register at the start of the
@@ -58,9 +64,11 @@
 // turn a long delay into a reported failure.
 //
 // Progress.  L-waves reuse an LDS slot once the Y-waves copied it; P-waves
-// reuse their LDS slot once the Y-waves read it; records of tile q are
-// overwritten by tile q + kCoR only after every member's P-waves are past
-// tile q (kCoR >= 2 S + 2 kCoLag + 2 tiles, see CoCfg).  Every wait is
+// reuse their LDS slot once the Y-waves read it; records and totals of
+// tile q are overwritten by tile q + kCoR only after every member's P-waves
+// are past tile q (kCoR >= 2 S + 2 kCoLag + 2 tiles, see CoCfg: a member
+// publishes tile q + kCoR only after its Y-waves used the totals of a later
+// tile than q, which every member's P-waves produced after q's).  Every wait is
 // bounded: after kCoTimeout of s_memrealtime without progress a wave sets the
 // block's abort flag and the status word, and every wave leaves; the finalize
 // kernel then writes NaN to every output of the call and copies the status
@@ -82,12 +90,15 @@ constexpr int kCoR = 16;                           // exchange ring: tiles per g
 constexpr int kCoVals = 25;                        // sums per token: 24 mixes + sum(x^2)
 constexpr int kCoRecWords = kCoTT * kCoVals / 2;   // 16-byte words of a record (200)
 constexpr int kCoYWords = kCoTT * 5 / 2;           // words y needs: 4 pre mixes + sum(x^2) (40)
-constexpr int kCoMaxHW = (160 + kCoMinG - 1) / kCoMinG;  // head words a member totals, at most (10)
+constexpr int kCoMaxOW = (kCoRecWords + kCoMinG - 1) / kCoMinG;  // record words a member totals, at most (13)
+constexpr int kCoRsB = 16;                         // exchange lanes per member in a load (>= kCoMaxOW)
+static_assert(kCoMaxOW <= kCoRsB && kCoMaxG % (kWave / kCoRsB) == 0, "owned words fit a member's lanes");
 // forward status codes after the common ones (coop_common.hpp): the wait
 // that timed out: 3 L slot copied, 4 L partial buffer, 5 Y tile landed,
-// 6 P exchange poll, 7 Y sums, 8 P own publish, 9 P sums slot
+// 6 P exchange poll (the members' records), 7 Y sums, 8 P own publish, 9 P
+// sums slot, 10 P totals poll (the owners' totals)
 constexpr uint32_t kStLCopied = 3, kStLPread = 4, kStYLanded = 5, kStPPoll = 6, kStYSums = 7, kStPPub = 8,
-                   kStPSlot = 9;
+                   kStPSlot = 9, kStPTot = 10;
 
 // Value order inside a record: v * 16 + token, v = 0..3 the pre mixes
 // (m = 0..3), v = 4 the sum of squares, v = 5..24 the mixes m = 4..23, so
@@ -125,6 +136,7 @@ struct CoopArgs {
   PreFwdArgs a;     // inputs and outputs; part / part_ssq receive the designated sums
   uint32_t* ctl;    // kCoCtlWords control words, zeroed before the launch
   u32x4* rec;       // [maxg][kCoR][G][kCoRecWords], zeroed before the launch
+  u32x4* tot;       // [maxg][kCoR][kCoRecWords] group totals, zeroed before the launch
   int G;            // members per group (D / CS)
   int maxg;         // groups the ring has room for
   uint64_t timeout; // s_memrealtime ticks a wait may last without progress
@@ -221,7 +233,9 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   constexpr int M = 24;
   __shared__ __align__(1024) u32x4 slots[S * C::SLOT / 16];
   __shared__ __align__(16) float pbuf[2][kCoLW][kCoTT * kCoVals];   // L-wave partials of a tile (two tiles)
-  __shared__ float tot[kCoPSlots][2 * (kCoYWords + kCoMaxHW)];  // per tile: totals of the polled words (word w -> [2 w], [2 w + 1])
+  // per tile: the y words' totals (word w -> [2 w], [2 w + 1]), then this
+  // member's owned words' totals
+  __shared__ float tot[kCoPSlots][2 * (kCoYWords + kCoMaxOW)];
   __shared__ float pinv[kCoPSlots][kCoTT][5];  // per tile and token: pre (4) and inv_rms
   // counters: landed[S] at 0, copied[S] at 8, pcnt[2] at 16, pread[2] at 18,
   // abort at 21, pub (tiles published) at 22, pready[kCoPSlots] at 24,
@@ -395,8 +409,9 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   // of order), which would put a full store round trip into every tile.
   // P-waves only load (the group's records) and hand sums to the Y-waves
   // through LDS; Y-waves only store (y, x_scaled, part).
-  const int hw0 = kCoYWords + (kCoRecWords - kCoYWords) * member / G;
-  const int nhw = kCoYWords + (kCoRecWords - kCoYWords) * (member + 1) / G - hw0;  // <= kCoMaxHW
+  // the record words this member totals for the group: [ow0, ow0 + now)
+  const int ow0 = kCoRecWords * member / G;
+  const int now = kCoRecWords * (member + 1) / G - ow0;  // <= kCoMaxOW
   // uniform parameters moved to scalar registers up front: a vector register
   // still waiting on its load would make a loop wait on vmcnt(0) (every load
   // or store in flight) at its first use in each iteration
@@ -406,68 +421,72 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   if (wave >= kCoLW + YW) {
     // ======================= P-wave pw ======================================
     // P-wave pw takes the tiles u = pw (mod kCoPW) (so kCoPW tiles' polls are
-    // in flight at once, and each P-wave owns psum slot pw): once this CU has
-    // published tile u it reads, from every member, the 40 words y needs
-    // (lanes 0..39) and this member's share [hw0, hw0 + nhw) of the 160 words
-    // of the heads' values (lanes 40 ..), adds them in member order, and
-    // leaves the totals and each token's pre / inv_rms (rms_inv, pre_gate, as
-    // the finalize kernel) in LDS for the Y-waves.  Its loads are issued and
-    // consumed in the same iteration.
+    // in flight at once, and each P-wave owns psum slot pw).  The exchange is
+    // a reduce-scatter, then a gather of the words y needs: once this CU has
+    // published tile u, (1) it reads its own share [ow0, ow0 + now) of the
+    // record words from every member's record, adds them over the members
+    // and publishes the totals (same word format and tag) to the group's
+    // totals ring; (2) it reads the 40 words y needs from the totals ring
+    // (written by their owners) and leaves them, its own share and each
+    // token's pre / inv_rms (rms_inv, pre_gate, as the finalize kernel) in
+    // LDS for the Y-waves.  A CU so reads 16 bytes per member for each owned
+    // word and 640 bytes of totals per tile, instead of 50 words from every
+    // member.  Its loads are issued and consumed in the same iteration.
     const int pw = wave - kCoLW - YW;
     static_assert(kCoPSlots == kCoPW, "a psum slot per P-wave");
     const float a0 = uniform(a.alpha[0]);
     float base_n[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) base_n[n] = uniform(a.base[n]);
-    const bool pact = lane < kCoYWords + nhw;
-    const uint32_t poff = (uint32_t)((lane < kCoYWords ? lane : (pact ? hw0 + lane - kCoYWords : 0)) * 16);
-    // tile t's records: a range of exactly G members, so loads of members
-    // past G fall outside it and read zeros
+    // (1) lane l of load q: word ow0 + l % kCoRsB of member q kCoMB + l /
+    // kCoRsB.  Tile t's records are a range of exactly G members, so loads
+    // of members past G (and lanes past the share) fall outside it and read
+    // zeros, whose tag 0 never matches.
+    constexpr int kCoMB = kWave / kCoRsB;  // members a load covers (4)
+    constexpr int kCoNL = kCoMaxG / kCoMB;  // loads (8)
+    const int k1 = lane % kCoRsB;
+    const uint32_t roff = k1 < now ? (uint32_t)(((lane / kCoRsB) * kCoRecWords + ow0 + k1) * 16) : kBufferOob;
     auto rec_rsrc = [&](int t) {
       return rows_rsrc(recw + (size_t)(t & (kCoR - 1)) * G * kCoRecWords, (int64_t)G * kCoRecWords * 16);
     };
+    u32x4* totw = ca.tot + (size_t)group * kCoR * kCoRecWords;  // this group's totals ring
+    auto tot_rsrc = [&](int t) { return rows_rsrc(totw + (size_t)(t & (kCoR - 1)) * kCoRecWords, kCoRecWords * 16); };
     const int sl = pw;
     for (int u = pw; u < nq; u += kCoPW) {
       // this CU's own record comes a few tiles after the previous tile this
       // wave took (a wait of 2 - 3 us measured): fewer, longer sleeps
       co_wait_ge<4>(c_pub, (uint32_t)(u + 1), c_abort, status, kStPPub, to);
       const uint32_t tag = (uint32_t)(u + 1);
+      // ---- (1) this member's share from every record, retried until all
+      // G now words carry this tile's tag; the sum runs over the loads
+      // (members q kCoMB + l / kCoRsB in q order), then over the lanes of the
+      // same word (l ^ 16, l ^ 32): a fixed order
       const auto rr = rec_rsrc(u);
       uint64_t deadline = 0;
-      // every member's words in one round of loads (one L2 round trip),
-      // retried until every tag is this tile's; the sums run in member order
-      // over members 0..15 and 16.., then the two partial sums are added
       float s0 = 0.f, s1 = 0.f;
       for (;;) {
-        // the lane's word offset, opaque here so that the 32 member offsets
-        // are formed at each load, not held in registers across the retries
-        uint32_t vb = pact ? poff : kBufferOob;
+        uint32_t vb = roff;
         asm volatile("" : "+v"(vb));
-        u32x4 PV[kCoMaxG];
+        u32x4 PV[kCoNL];
 #pragma unroll
-        for (int i = 0; i < kCoMaxG; ++i)
-          PV[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, vb + (uint32_t)(i * kCoRecWords * 16), 0, kCoPolicySc1);
-        // members past G read zeros (their values add nothing, their tag 0
-        // never matches): the G members' words are all current when G tags
-        // match.  A word's two tags are written by one store and read by one
-        // load, so they are equal: one is checked.
-        uint32_t nok = 0;
-        float a0s = 0.f, a1s = 0.f, b0s = 0.f, b1s = 0.f;
+        for (int q = 0; q < kCoNL; ++q)
+          PV[q] = __builtin_amdgcn_raw_buffer_load_b128(rr, vb + (uint32_t)(q * kCoMB * kCoRecWords * 16), 0,
+                                                        kCoPolicySc1);
+        // a word's two tags are written by one store and read by one load,
+        // so they are equal: one is checked
+        uint32_t cur = 0;
 #pragma unroll
-        for (int i = 0; i < kCoMaxG; ++i) {
-          nok += PV[i][1] == tag ? 1u : 0u;
-          if (i < 16) {
-            a0s += __uint_as_float(PV[i][0]);
-            a1s += __uint_as_float(PV[i][2]);
-          } else {
-            b0s += __uint_as_float(PV[i][0]);
-            b1s += __uint_as_float(PV[i][2]);
+        for (int q = 0; q < kCoNL; ++q) cur += (uint32_t)__popcll(__ballot(PV[q][1] == tag));
+        if (cur == (uint32_t)(G * now)) {
+          s0 = __uint_as_float(PV[0][0]);
+          s1 = __uint_as_float(PV[0][2]);
+#pragma unroll
+          for (int q = 1; q < kCoNL; ++q) {
+            s0 += __uint_as_float(PV[q][0]);
+            s1 += __uint_as_float(PV[q][2]);
           }
-        }
-        const bool ok = !pact || nok == (uint32_t)G;
-        if (!__any(!ok)) {
-          s0 = a0s + b0s;
-          s1 = a1s + b1s;
+          s0 = group_sum<48>(s0);
+          s1 = group_sum<48>(s1);
           break;
         }
         if (deadline == 0) deadline = co_now() + to;
@@ -479,11 +498,43 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         }
         __builtin_amdgcn_s_sleep(1);
       }
+      // the share's totals to the totals ring (lanes k < now of the first
+      // row hold word ow0 + k); default policy: the lines stay in this XCC's
+      // L2, where the readers' device-scope loads find them
+      const auto tr = tot_rsrc(u);
+      if (lane < now)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(s0), tag, __float_as_uint(s1), tag}, tr,
+                                               (uint32_t)((ow0 + lane) * 16), 0, 0);
+      // ---- (2) the 40 words y needs, from their owners' totals
+      deadline = 0;
+      float y0 = 0.f, y1 = 0.f;
+      for (;;) {
+        uint32_t vb = lane < kCoYWords ? (uint32_t)(lane * 16) : kBufferOob;
+        asm volatile("" : "+v"(vb));
+        const u32x4 TV = __builtin_amdgcn_raw_buffer_load_b128(tr, vb, 0, kCoPolicySc1);
+        if (!__any(lane < kCoYWords && TV[1] != tag)) {
+          y0 = __uint_as_float(TV[0]);
+          y1 = __uint_as_float(TV[2]);
+          break;
+        }
+        if (deadline == 0) deadline = co_now() + to;
+        if (co_lds_ld_u(c_abort)) break;
+        if (co_now() > deadline) {
+          co_lds_inc(c_abort);
+          co_fail(status, kStPTot);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
       // the slot's previous tile must be read by every Y-wave
       co_wait_ge(c_ydone + 4 * (uint32_t)sl, (uint32_t)(YW * (u / kCoPW)), c_abort, status, kStPSlot, to);
-      if (pact) {
-        tot[sl][2 * lane] = s0;
-        tot[sl][2 * lane + 1] = s1;
+      if (lane < kCoYWords) {
+        tot[sl][2 * lane] = y0;
+        tot[sl][2 * lane + 1] = y1;
+      }
+      if (lane < now) {
+        tot[sl][2 * kCoYWords + 2 * lane] = s0;
+        tot[sl][2 * kCoYWords + 2 * lane + 1] = s1;
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (lane < kCoTT) {
@@ -605,11 +656,10 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   };
 
   // Step j: copy tile j into X[j % 3], then take tile t = j - 2 from
-  // X[t % 3]: pre / inv_rms and the part totals from the P-waves, y, the
-  // heads' share and (designated member) the y values' totals to part.  The
-  // loop body is three steps, so the ring never moves between registers.
+  // X[t % 3]: pre / inv_rms and this member's share of the totals from the
+  // P-waves, y, and (Y-wave 0) the share to part / part_ssq.  The loop body
+  // is three steps, so the ring never moves between registers.
   static_assert(kCoLag == 2, "three register buffers: tiles j - 2 .. j");
-  int own = 0;  // (tile t) % G: the member designated for tile t's totals
   auto step = [&](int j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) {
     const int t = j - kCoLag;
     if (j < nq) copy(j, Xc);
@@ -622,31 +672,30 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         for (int n = 0; n < 4; ++n) p[b][n] = pinv[sl][tok[b]][n];
         inv[b] = pinv[sl][tok[b]][4];
       }
-      const int pv = (v - 1) * kWave + lane;
-      const bool des = own == member && v >= 1 && pv < 5 * kCoTT;
-      own = own + 1 == G ? 0 : own + 1;
-      const bool hs = v == 0 && lane < 2 * nhw;
-      const float sh = hs ? tot[sl][2 * kCoYWords + lane] : 0.f;
-      const float dv = des ? tot[sl][pv] : 0.f;
+      // this member's share: record values 2 ow0 .. 2 (ow0 + now) - 1
+      // (value vv of token tk for value index 16 vv + tk), from an opaque
+      // copy of the lane index (addresses held across the loop would spill)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const bool hs = v == 0 && ln < 2 * now;
+      const float sh = hs ? tot[sl][2 * kCoYWords + ln] : 0.f;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       co_lds_inc(c_ydone + 4 * (uint32_t)sl);  // slot read
       write_y(t, Xt);
       const int64_t t0 = t0_of(t);
       const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
-      const auto ps = rows_rsrc(a.part + t0 * M, (int64_t)nv * M * 4);
-      if (hs) {  // this member's share of the heads' values
-        const int hv = 2 * hw0 + lane;  // value index in the record (>= 80)
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sh), ps, (uint32_t)((hv % kCoTT) * M + hv / kCoTT - 1) * 4,
+      const int vi = 2 * ow0 + ln, vv = vi / kCoTT, tk = vi % kCoTT;
+      // the mixes to part [T][M] (m = vv for vv < 4, vv - 1 past the sum of
+      // squares), the sum of squares to part_ssq [T]: two stores, each
+      // against one buffer
+      if (hs && vv != 4) {
+        const auto ps = rows_rsrc(a.part + t0 * M, (int64_t)nv * M * 4);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sh), ps, (uint32_t)(tk * M + (vv < 4 ? vv : vv - 1)) * 4,
                                               0, 0);
       }
-      if (des) {  // the designated member: the y values' totals to part / part_ssq
-        const int pl = (v - 1) * kWave + lane_at_use(), vt = pl / kCoTT, tk = pl % kCoTT;
-        if (vt == 4) {
-          const auto ss = rows_rsrc(a.part_ssq + t0, (int64_t)nv * 4);
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dv), ss, (uint32_t)tk * 4, 0, 0);
-        } else {
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dv), ps, (uint32_t)(tk * M + vt) * 4, 0, 0);
-        }
+      if (hs && vv == 4) {
+        const auto ss = rows_rsrc(a.part_ssq + t0, (int64_t)nv * 4);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sh), ss, (uint32_t)tk * 4, 0, 0);
       }
     }
   };
@@ -668,7 +717,8 @@ inline size_t coop_ws_bytes(int64_t T, int N, int D) {
   int G = 0;
   if (N != 4 || T < kCoopMinT || !coop_nch(D, &G)) return 0;
   return align256((size_t)kCoCtlWords * 4) + align256((size_t)coop_max_groups(G) * kCoR * G * kCoRecWords * 16) +
-         align256((size_t)T * 24 * 4) + align256((size_t)T * 4) + fwd_y_ws_bytes(T, 4);
+         align256((size_t)coop_max_groups(G) * kCoR * kCoRecWords * 16) + align256((size_t)T * 24 * 4) +
+         align256((size_t)T * 4) + fwd_y_ws_bytes(T, 4);
 }
 
 // Runs the single-pass form when it applies (N = 4 bf16 fast path, D with a
@@ -696,6 +746,9 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   ca.timeout = coop_wait_limit();
   const size_t rec_bytes = align256((size_t)ca.maxg * kCoR * G * kCoRecWords * 16);
   w += rec_bytes;
+  ca.tot = reinterpret_cast<u32x4*>(w);
+  const size_t tot_bytes = align256((size_t)ca.maxg * kCoR * kCoRecWords * 16);
+  w += tot_bytes;
   a.part = reinterpret_cast<float*>(w);
   w += align256((size_t)a.T * 24 * 4);
   a.part_ssq = reinterpret_cast<float*>(w);
@@ -705,7 +758,7 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   ca.a = a;
   ca.G = G;
   // zero the control words and the ring (contiguous)
-  const int64_t words = (int64_t)((align256((size_t)kCoCtlWords * 4) + rec_bytes) / 16);
+  const int64_t words = (int64_t)((align256((size_t)kCoCtlWords * 4) + rec_bytes + tot_bytes) / 16);
   hipLaunchKernelGGL(co_zero_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(ca.ctl), words);
   int rc = check_launch("pre_fwd_coop_zero");
   if (rc) return rc;
