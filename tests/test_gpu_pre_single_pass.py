@@ -82,10 +82,13 @@ def _run(mode, x, phi, alpha, base, xs, clamp=10.0, iters=20):
 
 CASES = [
     # (T, D, x_scaled)
-    (8192, 7168, False),
+    (8192, 7168, False),     # 28 members a group
     (8200, 7168, False),     # ragged last tile, groups with unequal tile counts
+    (8200, 7168, True),      # with fp32 x_scaled (loads two tiles ahead)
     (16384, 4096, False),    # two groups per XCC
     (16390, 4096, True),     # ragged, with fp32 x_scaled
+    (8192, 7680, False),     # 256-column slices, 30 members a group
+    (8192, 8192, True),      # 256-column slices, 32 members a group, x_scaled
     (65536, 7168, False),    # BASELINE config 5 width and length
 ]
 
