@@ -11,7 +11,10 @@
 //
 // Shape: N = 4, bf16 x / h_out / phi, D a multiple of 64 and >= 256; the C
 // entry point runs mhc_post then mhc_pre_clamp_sinkhorn for every other
-// shape.  (The tile's gates sit in one LDS buffer that wave 0 refills when it
+// shape, and also where the pre forward has its single pass (T >= 8192, D =
+// 4096 or 7168 .. 8192: it reads x_next once, so the two operators move
+// post's bytes plus one read of x_next, fewer than this kernel plus its y
+// pass).  (The tile's gates sit in one LDS buffer that wave 0 refills when it
 // issues the next tile's first stage, S - 1 stages ahead: a tile must span
 // at least S stages, D >= 64 * S, so that it has read its gates by then.)
 //
@@ -458,8 +461,13 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
   if (!x || !h_res || !h_out || !h_post || !phi || !alpha || !base || !x_next || !y || !post_out || !comb_frag)
     return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: null pointer");
   if (!post_pre_usable(x, h_out, phi, x_next, y, x_dtype, phi_dtype, N, D) || !workspace ||
-      workspace_bytes < fwd_y_ws_bytes(T, N)) {
-    // every other shape: the two operators one after the other
+      workspace_bytes < fwd_y_ws_bytes(T, N) ||
+      pre_fwd_single_pass_applies(x_next, x_dtype, phi, phi_dtype, y, workspace_bytes, T, N, D,
+                                  (hipStream_t)stream)) {
+    // every other shape, and where the pre forward reads x_next once (its
+    // single-pass form: then the post forward plus that move fewer bytes
+    // than this kernel plus the y pass): the two operators one after the
+    // other
     int rc = mhc_post_fwd(x, h_res, h_out, h_post, x_next, T, N, D, x_dtype, stream);
     if (rc) return rc;
     return mhc_pre_fwd(x_next, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,

@@ -1207,6 +1207,26 @@ extern "C" size_t mhc_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, in
   return coop && kPreFwdWsBase + coop > base ? kPreFwdWsBase + coop : base;
 }
 
+// Whether mhc_pre_fwd / mhc_pre_fwd_ex without x_scaled runs the single-pass
+// form on these arguments (the checks launch_pre_fwd_dma<4> and
+// launch_pre_fwd_coop make, in the same order).  The fused post + pre
+// forward defers to the two operators where it does.
+namespace mhc {
+bool pre_fwd_single_pass_applies(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype, const void* y,
+                                 size_t workspace_bytes, int64_t T, int32_t N, int32_t D, hipStream_t st) {
+  if (N != 4 || x_dtype != MHC_DTYPE_BF16 || phi_dtype != MHC_DTYPE_BF16 || D <= 0 || T <= 0) return false;
+  const int64_t K = (int64_t)N * D;
+  if (K % 8 || !aligned16(phi) || D % 8 || !aligned16(x) || !aligned16(y)) return false;
+  if ((int64_t)kFwdTile * N * D * 4 >= ((int64_t)1 << 31)) return false;
+  const size_t y_ws = fwd_y_ws_bytes(T, N), ha_ws = heads_apart_bytes(T, N);
+  if (workspace_bytes < kPreFwdWsBase + (ha_ws > y_ws ? ha_ws : y_ws)) return false;
+  int G = 0;
+  const size_t need = coop_ws_bytes(T, 4, D);
+  if (!coop_nch(D, &G) || !need || workspace_bytes < kPreFwdWsBase + need || stream_capturing(st)) return false;
+  return coop_fits((const void*)pre_fwd_coop_kernel<32, false>, CoCfg<32>::THREADS, 0);
+}
+}  // namespace mhc
+
 extern "C" int mhc_pre_fwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,
                               const float* alpha, const float* base, float norm_eps, float hc_eps,
                               float clamp_min, float clamp_max, int32_t iter_times, void* y,

@@ -36,6 +36,12 @@ inline size_t phiT_planes_bytes(int32_t phi_dtype, int M, int64_t K) {
 // x_next.
 int launch_pre_y_pass(const void* x, const float* pre, void* y, int64_t T, int N, int D, hipStream_t st);
 
+// Whether mhc_pre_fwd without x_scaled runs its single-pass form (x read
+// from HBM once) on these arguments: N = 4, bf16 x and phi, a slice
+// geometry for D, T large enough, workspace for it, no stream capture.
+bool pre_fwd_single_pass_applies(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype, const void* y,
+                                 size_t workspace_bytes, int64_t T, int32_t N, int32_t D, hipStream_t st);
+
 // Bytes the pre forward (and the fused post + pre forward) keep per call for
 // pre (T, N) and inv_rms (T,) between their contraction and y kernels.
 inline size_t fwd_y_ws_bytes(int64_t T, int N) { return align256((size_t)T * N * 4) + align256((size_t)T * 4); }
