@@ -460,6 +460,15 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
   if (T == 0) return MHC_OK;
   if (!x || !h_res || !h_out || !h_post || !phi || !alpha || !base || !x_next || !y || !post_out || !comb_frag)
     return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: null pointer");
+  if (N == 4 && x_dtype == MHC_DTYPE_BF16 && phi_dtype == MHC_DTYPE_BF16 && workspace) {
+    // one pass: x_next formed in the single-pass pre kernel and written once
+    bool used = false;
+    const int rc = post_pre_fwd_single_pass(x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
+                                            clamp_max, iter_times, x_next, y, post_out, comb_frag, inv_rms, mixes,
+                                            h_res_logits, pre, workspace, workspace_bytes, T, D,
+                                            (hipStream_t)stream, &used);
+    if (rc || used) return rc;
+  }
   if (!post_pre_usable(x, h_out, phi, x_next, y, x_dtype, phi_dtype, N, D) || !workspace ||
       workspace_bytes < fwd_y_ws_bytes(T, N) ||
       pre_fwd_single_pass_applies(x_next, x_dtype, phi, phi_dtype, y, workspace_bytes, T, N, D,

@@ -1225,6 +1225,53 @@ bool pre_fwd_single_pass_applies(const void* x, int32_t x_dtype, const void* phi
   if (!coop_nch(D, &G) || !need || workspace_bytes < kPreFwdWsBase + need || stream_capturing(st)) return false;
   return coop_fits((const void*)pre_fwd_coop_kernel<32, false>, CoCfg<32>::THREADS, 0);
 }
+
+// The fused post + pre forward in one pass (pre_fwd_coop_kernel with POST):
+// where the single-pass pre forward applies to x_next's shape, and x,
+// h_out, x_next and y are 16-byte aligned, x_next is formed in the kernel
+// and written once; *used says whether it ran.
+int post_pre_fwd_single_pass(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                             const void* phi, const float* alpha, const float* base, float norm_eps, float hc_eps,
+                             float clamp_min, float clamp_max, int32_t iter_times, void* x_next, void* y,
+                             float* post_out, float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
+                             float* pre, void* workspace, size_t workspace_bytes, int64_t T, int32_t D,
+                             hipStream_t st, bool* used) {
+  *used = false;
+  constexpr int N = 4;
+  if (!pre_fwd_single_pass_applies(x, MHC_DTYPE_BF16, phi, MHC_DTYPE_BF16, y, workspace_bytes, T, N, D, st) ||
+      !aligned16(h_out) || !aligned16(x_next))
+    return MHC_OK;
+  const int M = 2 * N + N * N;
+  const int64_t K = (int64_t)N * D;
+  PreFwdArgs a{};
+  a.x = x;
+  int rc = prepare_phi_planes(phi, MHC_DTYPE_BF16, M, K, workspace, workspace_bytes, &a.phi, &a.phi_ld,
+                              &a.phi_plane_stride, &a.phi_planes, st);
+  if (rc) return rc;
+  a.alpha = alpha;
+  a.base = base;
+  a.norm_eps = norm_eps;
+  a.hc_eps = hc_eps;
+  a.cmin = clamp_min;
+  a.cmax = clamp_max;
+  a.apply_clamp = (clamp_min != 0.0f || clamp_max != 0.0f) ? 1 : 0;
+  a.iters = iter_times;
+  a.y = y;
+  a.post_out = post_out;
+  a.comb = comb_frag;
+  a.inv_rms = inv_rms;
+  a.mixes = mixes;
+  a.logits = h_res_logits;
+  a.pre = pre;
+  a.T = T;
+  a.D = D;
+  CoopArgs post{};
+  post.h_out = static_cast<const bf16_t*>(h_out);
+  post.h_res = h_res;
+  post.h_post = h_post;
+  post.x_next = static_cast<bf16_t*>(x_next);
+  return launch_pre_fwd_coop_x<false, true>(a, workspace, workspace_bytes, st, used, &post);
+}
 }  // namespace mhc
 
 extern "C" int mhc_pre_fwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype,

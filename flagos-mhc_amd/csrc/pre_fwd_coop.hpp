@@ -96,9 +96,10 @@ static_assert(kCoMaxOW <= kCoRsB && kCoMaxG % (kWave / kCoRsB) == 0, "owned word
 // forward status codes after the common ones (coop_common.hpp): the wait
 // that timed out: 3 L slot copied, 4 L partial buffer, 5 Y tile landed,
 // 6 P exchange poll (the members' records), 7 Y sums, 8 P own publish, 9 P
-// sums slot, 10 P totals poll (the owners' totals)
+// sums slot, 10 P totals poll (the owners' totals), 11 L x_next formed
+// (fused post + pre form)
 constexpr uint32_t kStLCopied = 3, kStLPread = 4, kStYLanded = 5, kStPPoll = 6, kStYSums = 7, kStPPub = 8,
-                   kStPSlot = 9, kStPTot = 10;
+                   kStPSlot = 9, kStPTot = 10, kStLXnext = 11;
 
 // Value order inside a record: v * 16 + token, v = 0..3 the pre mixes
 // (m = 0..3), v = 4 the sum of squares, v = 5..24 the mixes m = 4..23, so
@@ -140,6 +141,12 @@ struct CoopArgs {
   int G;            // members per group (D / CS)
   int maxg;         // groups the ring has room for
   uint64_t timeout; // s_memrealtime ticks a wait may last without progress
+  // fused post + pre form (POST): a.x is the post's input x (T, 4, D); the
+  // kernel forms x_next = h_res^T x + h_post h_out and writes it once
+  const bf16_t* h_out;  // (T, D)
+  const float* h_res;   // (T, 4, 4)
+  const float* h_post;  // (T, 4)
+  bf16_t* x_next;       // (T, 4, D)
 };
 
 // The 200 value pairs of a record from the four L-waves' partials (1600
@@ -202,6 +209,59 @@ __device__ __forceinline__ void co_lds_rd4(u32x4 (&v)[4], uint32_t a0, uint32_t 
       : "memory");
 }
 
+// h_out's chunk (at a + 32768, the slot's fifth region) and a token's
+// h_res row (16 floats at c) and h_post row (4 floats at p) in one batch
+__device__ __forceinline__ void co_lds_rd_post(u32x4& h, float (&hr)[16], float (&hp)[4], uint32_t a, uint32_t c,
+                                               uint32_t p) {
+  u32x4 r[5];
+  asm volatile(
+      "ds_read_b128 %0, %6 offset:32768\n\t"
+      "ds_read_b128 %1, %7\n\t"
+      "ds_read_b128 %2, %7 offset:16\n\t"
+      "ds_read_b128 %3, %7 offset:32\n\t"
+      "ds_read_b128 %4, %7 offset:48\n\t"
+      "ds_read_b128 %5, %8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(h), "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4])
+      : "v"(a), "v"(c), "v"(p)
+      : "memory");
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) hr[4 * k + e] = __uint_as_float(r[k][e]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hp[e] = __uint_as_float(r[4][e]);
+}
+
+// x_next of one 16-byte chunk (8 columns) of the four streams: x_next[i] =
+// h_post[i] h_out + sum_j h_res[j][i] x[j] in mhc_post's order (the h_post
+// product first, then an FMA per input stream in stream order), rounded to
+// bf16 (round to nearest even), as the post kernels form it.  In place:
+// each word's four inputs are read before its four outputs are written.
+__device__ __forceinline__ void co_post_chunk(u32x4 (&X)[4], const u32x4& Hh, const float (&hr)[16],
+                                              const float (&hp)[4]) {
+#pragma unroll
+  for (int wd = 0; wd < 4; ++wd) {
+    const float h0 = __uint_as_float(Hh[wd] << 16), h1 = __uint_as_float(Hh[wd] & 0xffff0000u);
+    float x0[4], x1[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      x0[jj] = __uint_as_float(X[jj][wd] << 16);
+      x1[jj] = __uint_as_float(X[jj][wd] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v0 = hp[i] * h0, v1 = hp[i] * h1;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        v0 = fmaf(hr[4 * jj + i], x0[jj], v0);
+        v1 = fmaf(hr[4 * jj + i], x1[jj], v1);
+      }
+      X[i][wd] = pack_bf16x2(v0, v1);
+    }
+  }
+}
+
 // Two 8-byte reads per stream, four streams STRIDE bytes apart: stream n's
 // reads at a0 + n STRIDE and a1 + n STRIDE land in v[n][0..1] and v[n][2..3].
 template <int STRIDE>
@@ -225,13 +285,24 @@ __device__ __forceinline__ void co_lds_rd4x2(u32x4 (&v)[4], uint32_t a0, uint32_
   for (int n = 0; n < 4; ++n) v[n] = u32x4{h[2 * n][0], h[2 * n][1], h[2 * n + 1][0], h[2 * n + 1][1]};
 }
 
-template <int NCH, bool XS>
+// POST: the fused post + pre forward.  A slot then also holds h_out's slice
+// (a fifth 8 KB region, the streams' layout) and the tile's h_res / h_post
+// (coefs), so 3 slots of 40 KB fit; the Y-waves form x_next from each landed
+// slot (mhc_post's FMA order and rounding), write it back into the slot for
+// the L-waves' contraction and to HBM, and keep it for y.
+template <int NCH, bool XS, bool POST = false>
 __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopArgs ca) {
   using C = CoCfg<NCH>;
-  constexpr int A = XS ? C::A_MAX : 1;
-  constexpr int S = C::S, H = C::H, DMA = C::DMA, STEPS = C::STEPS, CS = C::CS, YW = C::YW, YB = C::YB;
+  static_assert(!(XS && POST), "the fused form writes no x_scaled");
+  constexpr int S = POST ? 3 : C::S;                            // LDS slots
+  constexpr int SLOT = POST ? C::SLOT + C::STREAM : C::SLOT;     // bytes of a slot
+  constexpr int A = POST ? 1 : (XS ? C::A_MAX : 1);
+  static_assert(A <= S - 2 && kCoR >= 2 * S + 2 * kCoLag + 2, "slot and ring depths");
+  constexpr int H = C::H, DMA = C::DMA, STEPS = C::STEPS, CS = C::CS, YW = C::YW, YB = C::YB;
   constexpr int M = 24;
-  __shared__ __align__(1024) u32x4 slots[S * C::SLOT / 16];
+  constexpr int kCoef = kCoTT * 20;  // floats of a tile's h_res (16 a token) and h_post (4 a token)
+  __shared__ __align__(1024) u32x4 slots[S * SLOT / 16];
+  __shared__ __align__(16) float coefs[POST ? S : 1][kCoef];
   __shared__ __align__(16) float pbuf[2][kCoLW][kCoTT * kCoVals];   // L-wave partials of a tile (two tiles)
   // per tile: the y words' totals (word w -> [2 w], [2 w + 1]), then this
   // member's owned words' totals
@@ -267,6 +338,10 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   u32x4* recw = ca.rec + (size_t)group * kCoR * G * kCoRecWords;  // this group's ring
   const auto ring = rows_rsrc(recw, (int64_t)kCoR * G * kCoRecWords * 16);
   const uint32_t sbase = lds_addr(slots);
+  const uint32_t cbase = lds_addr(&coefs[0][0]);
+  // the LDS slot of tile sequence j, and how many tiles used it before j
+  auto slot_of = [](int j) -> uint32_t { return (uint32_t)j % (uint32_t)S; };
+  auto round_of = [](int j) -> uint32_t { return (uint32_t)j / (uint32_t)S; };
   const uint32_t c_landed = lds_addr(cnt), c_copied = c_landed + 32, c_pcnt = c_landed + 64,
                  c_pread = c_landed + 72, c_abort = c_landed + 84, c_pub = c_landed + 88, c_pready = c_landed + 96,
                  c_ydone = c_pready + 4 * kCoPSlots, c_pfinal = c_ydone + 4 * kCoPSlots;
@@ -304,19 +379,53 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       const int tok = 4 * (i / H) + (lane >> 4);
       ioff[i] = (uint32_t)((tok * K + 8 * (16 * (i % H) + ((lane & 15) ^ tok))) * 2);
     }
+    // POST: L-wave w also loads instructions 2w, 2w + 1 of h_out's slice
+    // (rows of D elements, the streams' layout: tokens 4w + rho, half rows
+    // 0 and 1), wave 0 the tile's h_res rows (1 KB) and wave 1 its h_post
+    // rows (256 bytes) into the slot's coefs
+    static_assert(!POST || (H == 2 && DMA == 8), "h_out's eight loads split two a wave");
+    const bf16_t* iss_h = POST ? ca.h_out + (int64_t)iss_t0 * D + slice0 : nullptr;
+    uint32_t hoff[2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int tok = 4 * w + (lane >> 4);
+      hoff[ii] = (uint32_t)((tok * D + 8 * (16 * ii + ((lane & 15) ^ tok))) * 2);
+    }
     auto issue = [&](int qi) {
       const int64_t left = T - iss_t0;
       const int nv = left < kCoTT ? (int)left : kCoTT;
       const auto rs = rows_rsrc(iss_x, ((int64_t)(nv - 1) * K + CS) * 2);
-      iss_t0 += ngroups * kCoTT;
-      iss_x += iss_step;
-      const uint32_t slot = sbase + (uint32_t)((qi & (S - 1)) * C::SLOT + w * C::STREAM);
+      const uint32_t sb = sbase + slot_of(qi) * SLOT;
+      const uint32_t slot = sb + (uint32_t)(w * C::STREAM);
 #pragma unroll
       for (int i = 0; i < DMA; ++i) {
         const uint32_t off = ioff[i];
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(uintptr_t)(slot + i * 1024), 16, off, 0, 0,
                                                  2 /* nt */);
       }
+      if constexpr (POST) {
+        const auto rh = rows_rsrc(iss_h, ((int64_t)(nv - 1) * D + CS) * 2);
+        const uint32_t hsl = sb + (uint32_t)(4 * C::STREAM + 2 * w * 1024);
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const uint32_t off = hoff[ii];
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (lds_void_t*)(uintptr_t)(hsl + ii * 1024), 16, off, 0, 0,
+                                                   2 /* nt */);
+        }
+        const uint32_t cs = cbase + slot_of(qi) * (uint32_t)(kCoef * 4);
+        if (w == 0) {
+          const auto rr = rows_rsrc(ca.h_res + (int64_t)iss_t0 * 16, (int64_t)nv * 64);
+          const uint32_t off = (uint32_t)(lane * 16);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t*)(uintptr_t)cs, 16, off, 0, 0, 0);
+        } else if (w == 1) {
+          const auto rp = rows_rsrc(ca.h_post + (int64_t)iss_t0 * 4, (int64_t)nv * 16);
+          const uint32_t off = (uint32_t)(lane * 4);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_void_t*)(uintptr_t)(cs + 1024), 4, off, 0, 0, 0);
+        }
+        iss_h += (int64_t)ngroups * kCoTT * D;
+      }
+      iss_t0 += ngroups * kCoTT;
+      iss_x += iss_step;
     };
     // LDS address of lane (r, q)'s A operand of step s in a stream slot
     uint32_t aoff[STEPS];
@@ -329,16 +438,26 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
     for (int j = 0; j < (nq < A ? nq : A); ++j) issue(j);
     for (int j = 0; j < nq; ++j) {
       if (j + A < nq) {
-        co_wait_ge(c_copied + 4 * (uint32_t)((j + A) & (S - 1)), (uint32_t)(YW * ((j + A) / S)), c_abort, status,
-                   kStLCopied, to);
+        co_wait_ge(c_copied + 4 * slot_of(j + A), (uint32_t)YW * round_of(j + A), c_abort, status, kStLCopied, to);
         issue(j + A);
       }
       const int after = nq - 1 - j < A ? nq - 1 - j : A;
-      co_wait_tiles<DMA, A>(after);
-      co_lds_inc(c_landed + 4 * (uint32_t)(j & (S - 1)));
+      if constexpr (POST) {  // loads a tile: 8 + 2, and h_res (wave 0) or h_post (wave 1)
+        if (w < 2)
+          co_wait_tiles<DMA + 3, A>(after);
+        else
+          co_wait_tiles<DMA + 2, A>(after);
+      } else {
+        co_wait_tiles<DMA, A>(after);
+      }
+      co_lds_inc(c_landed + 4 * slot_of(j));
+      // POST: the Y-waves replace the slot's x by x_next (and count it as
+      // copied) before the contraction reads it
+      if constexpr (POST)
+        co_wait_ge(c_copied + 4 * slot_of(j), (uint32_t)YW * (round_of(j) + 1), c_abort, status, kStLXnext, to);
 
       // contraction of this stream's 16 x CS slice: fresh MFMA chain
-      const uint32_t sl = sbase + (uint32_t)((j & (S - 1)) * C::SLOT + w * C::STREAM);
+      const uint32_t sl = sbase + slot_of(j) * SLOT + (uint32_t)(w * C::STREAM);
       // sum(x^2) on the matrix cores too: the A operand is also the B operand
       // of x x^T (the register layouts coincide), whose diagonal holds each
       // token's sum of squares
@@ -577,10 +696,10 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   };
   auto tok_of = [&](int l, int b) -> int { return 4 * ((v + YW * b) / H) + (l >> 4); };
 
-  // tile j into Xc
+  // tile j into Xc (POST: x_next, formed from the slot's x, h_out and
+  // coefs, also written back into the slot for the contraction)
   auto copy = [&](int j, u32x4 (&Xc)[YB][4]) {
-    co_wait_ge(c_landed + 4 * (uint32_t)(j & (S - 1)), (uint32_t)(kCoLW * (j / S + 1)), c_abort, status, kStYLanded,
-               to);
+    co_wait_ge(c_landed + 4 * slot_of(j), (uint32_t)kCoLW * (round_of(j) + 1), c_abort, status, kStYLanded, to);
 #pragma unroll
     for (int b = 0; b < YB; ++b) {
       if constexpr (XS) {
@@ -588,14 +707,46 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         // kp / 2 and 8 + kp / 2, half kp % 2, each at the lane position
         // chunk ^ token where the direct-to-LDS load put it
         const int l = lane_at_use(), k2 = (l & 15) >> 1, tk = tok_of(l, b);
-        const uint32_t o = sbase + (uint32_t)((j & (S - 1)) * C::SLOT + (v + YW * b) * 1024 + (l >> 4) * 256 + 8 * (l & 1));
+        const uint32_t o = sbase + slot_of(j) * SLOT + (uint32_t)((v + YW * b) * 1024 + (l >> 4) * 256 + 8 * (l & 1));
         co_lds_rd4x2<C::STREAM>(Xc[b], o + (uint32_t)((k2 ^ tk) * 16), o + (uint32_t)(((8 + k2) ^ tk) * 16));
       } else {
-        const uint32_t o = sbase + (uint32_t)((j & (S - 1)) * C::SLOT + (v + YW * b) * 1024 + lane * 16);
+        const uint32_t o = sbase + slot_of(j) * SLOT + (uint32_t)((v + YW * b) * 1024 + lane * 16);
         co_lds_rd4(Xc[b], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
+        if constexpr (POST) {
+          static_assert(4 * C::STREAM == 32768, "h_out's region at offset 32768 of a slot");
+          u32x4 Hh;
+          float hr[16], hp[4];
+          // the token's coefs addresses from an opaque copy of the lane index
+          // (held across the loop they would be spilled, and a scratch reload
+          // in this store-only wave waits for every store in flight)
+          int l = lane;
+          asm volatile("" : "+v"(l));
+          const uint32_t tk = (uint32_t)tok_of(l, b);
+          const uint32_t cs = cbase + slot_of(j) * (uint32_t)(kCoef * 4);
+          co_lds_rd_post(Hh, hr, hp, o, cs + tk * 64u, cs + 1024u + tk * 16u);
+          co_post_chunk(Xc[b], Hh, hr, hp);
+#pragma unroll
+          for (int n = 0; n < 4; ++n) co_lds_st4(o + (uint32_t)(n * C::STREAM), __builtin_bit_cast(floatx4, Xc[b][n]));
+        }
       }
     }
-    co_lds_inc(c_copied + 4 * (uint32_t)(j & (S - 1)));
+    // (POST: the count is raised after the x_next writes: a wave's LDS
+    // operations are performed in order)
+    co_lds_inc(c_copied + 4 * slot_of(j));
+  };
+  // POST: x_next of tile j's slice to HBM (rows past T fall outside the
+  // range and are dropped)
+  auto store_xnext = [&](int j, const u32x4 (&Xc)[YB][4]) {
+    const int64_t t0 = t0_of(j);
+    const int nv = (int)(T - t0 < kCoTT ? T - t0 : kCoTT);
+    const auto xn = rows_rsrc(ca.x_next + t0 * 4 * D, (int64_t)nv * 4 * D * 2);
+#pragma unroll
+    for (int b = 0; b < YB; ++b)
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        __builtin_amdgcn_raw_buffer_store_b128(Xc[b][n], xn,
+                                               (((uint32_t)tok[b] * 4 + n) * D + (uint32_t)(slice0 + 8 * chunk[b])) * 2,
+                                               0, 2 /* nt */);
   };
 
   // y (and x_scaled) of tile u from Xt with this lane's p / inv: buffer
@@ -662,7 +813,10 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   static_assert(kCoLag == 2, "three register buffers: tiles j - 2 .. j");
   auto step = [&](int j, u32x4 (&Xc)[YB][4], const u32x4 (&Xt)[YB][4]) {
     const int t = j - kCoLag;
-    if (j < nq) copy(j, Xc);
+    if (j < nq) {
+      copy(j, Xc);
+      if constexpr (POST) store_xnext(j, Xc);
+    }
     if (t >= 0 && t < nq) {
       const int sl = t & (kCoPSlots - 1);
       co_wait_ge(c_pfinal + 4 * (uint32_t)sl, (uint32_t)(t / kCoPSlots + 1), c_abort, status, kStYSums, to);
@@ -725,20 +879,28 @@ inline size_t coop_ws_bytes(int64_t T, int N, int D) {
 // slice geometry, T >= kCoopMinT, enough workspace, not under stream capture,
 // a block fits a CU); *used says whether it ran.  The finalize kernel copies
 // the status word to a.status_out (when set).
-template <bool XS>
+// POST (the fused post + pre forward): `post` carries h_out, h_res, h_post
+// and x_next, and a.x is the post's input x.
+template <bool XS, bool POST = false>
 static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace_bytes, hipStream_t st,
-                                  bool* used) {
+                                  bool* used, const CoopArgs* post = nullptr) {
   *used = false;
   int G = 0;
   const int nch = coop_nch(a.D, &G);
   const size_t need = coop_ws_bytes(a.T, 4, a.D);
   if (!nch || !need || !workspace || workspace_bytes < kPreFwdWsBase + need) return MHC_OK;
   if (stream_capturing(st)) return MHC_OK;
-  const void* kfn = (const void*)pre_fwd_coop_kernel<32, XS>;
+  const void* kfn = (const void*)pre_fwd_coop_kernel<32, XS, POST>;
   const int threads = CoCfg<32>::THREADS;
-  if (!coop_fits(kfn, threads, 0)) return MHC_OK;
+  if (!coop_fits(kfn, threads, POST ? 2 : 0)) return MHC_OK;
   char* w = static_cast<char*>(workspace) + kPreFwdWsBase;
-  CoopArgs ca;
+  CoopArgs ca{};
+  if constexpr (POST) {
+    ca.h_out = post->h_out;
+    ca.h_res = post->h_res;
+    ca.h_post = post->h_post;
+    ca.x_next = post->x_next;
+  }
   ca.ctl = reinterpret_cast<uint32_t*>(w);
   w += align256((size_t)kCoCtlWords * 4);
   ca.rec = reinterpret_cast<u32x4*>(w);
@@ -762,7 +924,7 @@ static int launch_pre_fwd_coop_x(PreFwdArgs a, void* workspace, size_t workspace
   hipLaunchKernelGGL(co_zero_kernel, dim3(1024), dim3(256), 0, st, reinterpret_cast<u32x4*>(ca.ctl), words);
   int rc = check_launch("pre_fwd_coop_zero");
   if (rc) return rc;
-  hipLaunchKernelGGL((pre_fwd_coop_kernel<32, XS>), dim3((unsigned)device_cu_count()), dim3(threads), 0, st, ca);
+  hipLaunchKernelGGL((pre_fwd_coop_kernel<32, XS, POST>), dim3((unsigned)device_cu_count()), dim3(threads), 0, st, ca);
   if ((rc = check_launch("pre_fwd_coop"))) return rc;
   *used = true;
   a.co_status = ca.ctl + kCtlStatus;  // a timed-out wait turns every output of the call into NaN

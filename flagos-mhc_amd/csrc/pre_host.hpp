@@ -42,6 +42,16 @@ int launch_pre_y_pass(const void* x, const float* pre, void* y, int64_t T, int N
 bool pre_fwd_single_pass_applies(const void* x, int32_t x_dtype, const void* phi, int32_t phi_dtype, const void* y,
                                  size_t workspace_bytes, int64_t T, int32_t N, int32_t D, hipStream_t st);
 
+// The fused post + pre forward in one pass (N = 4, bf16): x_next formed in
+// the single-pass pre kernel and written once.  *used is false (and nothing
+// ran) where that form does not apply.
+int post_pre_fwd_single_pass(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                             const void* phi, const float* alpha, const float* base, float norm_eps, float hc_eps,
+                             float clamp_min, float clamp_max, int32_t iter_times, void* x_next, void* y,
+                             float* post_out, float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
+                             float* pre, void* workspace, size_t workspace_bytes, int64_t T, int32_t D,
+                             hipStream_t st, bool* used);
+
 // Bytes the pre forward (and the fused post + pre forward) keep per call for
 // pre (T, N) and inv_rms (T,) between their contraction and y kernels.
 inline size_t fwd_y_ws_bytes(int64_t T, int N) { return align256((size_t)T * N * 4) + align256((size_t)T * 4); }

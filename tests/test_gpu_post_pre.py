@@ -6,10 +6,10 @@ The pre outputs are checked against the float64 oracle applied to that
 x_next on a token subset (bf16 y rtol/atol 2e-2, fp32 outputs rtol 1e-4 /
 atol 1e-5, as for mhc_pre_clamp_sinkhorn) and against the two operators run
 in turn over every token.  Shapes outside the fused kernel (N = 8, fp32,
-D % 64 != 0, D < 256, and the pre forward's single-pass shapes, where the
-two operators move fewer bytes) run the two kernels in turn and must match
-them bit for bit; the autograd form must give the gradients of the unfused
-chain."""
+D % 64 != 0, D < 256) run the two kernels in turn, and the pre forward's
+single-pass shapes form x_next inside the single-pass pre kernel; both must
+match the two operators bit for bit.  The autograd form must give the
+gradients of the unfused chain."""
 
 from __future__ import annotations
 
@@ -47,7 +47,8 @@ def _close_gpu(got, want, rtol, atol, what):
 def _fused_kernel(T, N, D, dtype):
     """The fused kernel runs for N = 4 bf16, D % 64 == 0 and D >= 256, except
     where the pre forward reads x once (its single pass: T >= 8192, D = 4096
-    or 7168 .. 8192 in steps of 256); there the two operators run in turn."""
+    or 7168 .. 8192 in steps of 256): there the single-pass pre kernel forms
+    x_next itself and computes exactly what the two operators compute."""
     single = (N == 4 and dtype == torch.bfloat16 and T >= 8192
               and (D == 4096 or (D % 256 == 0 and 7168 <= D <= 8192)))
     return N == 4 and dtype == torch.bfloat16 and D % 64 == 0 and D >= 256 and not single
@@ -60,7 +61,9 @@ CASES = [
     (200, 4, 3584, torch.bfloat16),     # fused
     (4133, 4, 7168, torch.bfloat16),    # fused, D = 7168, several tiles per block
     (31, 4, 7168, torch.bfloat16),      # fused, one partial tile
-    (65536, 4, 7168, torch.bfloat16),   # two operators (the pre forward's single pass), config 5
+    (65536, 4, 7168, torch.bfloat16),   # one pass (x_next formed in the single-pass pre kernel), config 5
+    (8200, 4, 7168, torch.bfloat16),    # one pass, ragged last tile
+    (16390, 4, 4096, torch.bfloat16),   # one pass, two groups per XCC, ragged
     (8192, 4, 6144, torch.bfloat16),    # fused, T in the single-pass range but no slice geometry for D
     (2000, 4, 3072, torch.bfloat16),    # fused
     (77, 4, 256, torch.bfloat16),       # fused, smallest D: a tile spans 4 stages
