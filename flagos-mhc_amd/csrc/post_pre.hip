@@ -11,10 +11,10 @@
 //
 // Shape: N = 4, bf16 x / h_out / phi, D a multiple of 64 and >= 256; the C
 // entry point runs mhc_post then mhc_pre_clamp_sinkhorn for every other
-// shape, and also where the pre forward has its single pass (T >= 8192, D =
-// 4096 or 7168 .. 8192: it reads x_next once, so the two operators move
-// post's bytes plus one read of x_next, fewer than this kernel plus its y
-// pass).  (The tile's gates sit in one LDS buffer that wave 0 refills when it
+// shape.  Where the pre forward has its single pass (T >= 8192, D = 4096 or
+// 7168 .. 8192) the single-pass pre kernel runs with a post front end
+// instead (post_pre_fwd_single_pass: x_next formed in the kernel, written
+// once, never read back), or, if that form cannot run, post then pre.  (The tile's gates sit in one LDS buffer that wave 0 refills when it
 // issues the next tile's first stage, S - 1 stages ahead: a tile must span
 // at least S stages, D >= 64 * S, so that it has read its gates by then.)
 //

@@ -2,7 +2,9 @@
 // phi, D = 256 G with G = 16 or 28 <= G <= 32 (coop_nch; D = 7168: G = 28).
 // Included by pre_fwd.hip.
 //
-// Semantics: mhc_pre_clamp_sinkhorn_ref, src/mhc_pre_clamp_sinkhorn.py:974-1022.
+// Semantics: mhc_pre_clamp_sinkhorn_ref, src/mhc_pre_clamp_sinkhorn.py:974-1022;
+// with POST also mhc_post_ref before it (src/mhc_post.py:344-352), x_next
+// formed in the kernel (the fused post + pre forward).
 // The passes it replaces are the reference's RMS / contraction passes over x
 // (:897-916) and its y pass (:956), which read x three times.
 //
