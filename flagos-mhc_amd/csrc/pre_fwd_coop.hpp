@@ -289,9 +289,10 @@ __device__ __forceinline__ void co_lds_rd4x2(u32x4 (&v)[4], uint32_t a0, uint32_
 
 // POST: the fused post + pre forward.  A slot then also holds h_out's slice
 // (a fifth 8 KB region, the streams' layout) and the tile's h_res / h_post
-// (coefs), so 3 slots of 40 KB fit; the Y-waves form x_next from each landed
-// slot (mhc_post's FMA order and rounding), write it back into the slot for
-// the L-waves' contraction and to HBM, and keep it for y.
+// (coefs), so 3 slots of 40 KB fit.  Once a slot has landed, L-wave w and
+// Y-wave w form x_next of row blocks w and w + 4 (mhc_post's FMA order and
+// rounding) in place; the contraction and the Y-waves' copy wait for all
+// eight; the Y-waves write x_next to HBM and keep it for y.
 template <int NCH, bool XS, bool POST = false>
 __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopArgs ca) {
   using C = CoCfg<NCH>;
@@ -344,7 +345,8 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   // the LDS slot of tile sequence j, and how many tiles used it before j
   auto slot_of = [](int j) -> uint32_t { return (uint32_t)j % (uint32_t)S; };
   auto round_of = [](int j) -> uint32_t { return (uint32_t)j / (uint32_t)S; };
-  const uint32_t c_landed = lds_addr(cnt), c_copied = c_landed + 32, c_pcnt = c_landed + 64,
+  // (POST: conv[S] at 4, the L-waves' x_next conversions of a slot)
+  const uint32_t c_landed = lds_addr(cnt), c_conv = c_landed + 16, c_copied = c_landed + 32, c_pcnt = c_landed + 64,
                  c_pread = c_landed + 72, c_abort = c_landed + 84, c_pub = c_landed + 88, c_pready = c_landed + 96,
                  c_ydone = c_pready + 4 * kCoPSlots, c_pfinal = c_ydone + 4 * kCoPSlots;
   const bf16_t* __restrict__ x = static_cast<const bf16_t*>(a.x);
@@ -453,10 +455,29 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
         co_wait_tiles<DMA, A>(after);
       }
       co_lds_inc(c_landed + 4 * slot_of(j));
-      // POST: the Y-waves replace the slot's x by x_next (and count it as
-      // copied) before the contraction reads it
-      if constexpr (POST)
-        co_wait_ge(c_copied + 4 * slot_of(j), (uint32_t)YW * (round_of(j) + 1), c_abort, status, kStLXnext, to);
+      if constexpr (POST) {
+        // x_next in place of x: once every L-wave's loads of the tile have
+        // landed (x of all streams, h_out, the gates), L-wave w converts row
+        // block w of the slot (all four streams of those chunks) and Y-wave
+        // w row block w + 4; the contraction waits for all eight
+        const uint32_t sc = slot_of(j), rc = round_of(j) + 1;
+        co_wait_ge(c_landed + 4 * sc, (uint32_t)kCoLW * rc, c_abort, status, kStLXnext, to);
+        const uint32_t cs = cbase + sc * (uint32_t)(kCoef * 4);
+        {
+          const int rb = w;
+          const uint32_t o = sbase + sc * SLOT + (uint32_t)(rb * 1024 + lane * 16);
+          const uint32_t tk = (uint32_t)(4 * (rb / H) + (lane >> 4));
+          u32x4 X[4], Hh;
+          float hr[16], hp[4];
+          co_lds_rd4(X, o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
+          co_lds_rd_post(Hh, hr, hp, o, cs + tk * 64u, cs + 1024u + tk * 16u);
+          co_post_chunk(X, Hh, hr, hp);
+#pragma unroll
+          for (int n = 0; n < 4; ++n) co_lds_st4(o + (uint32_t)(n * C::STREAM), __builtin_bit_cast(floatx4, X[n]));
+        }
+        co_lds_inc(c_conv + 4 * sc);  // after the writes (a wave's LDS operations stay in order)
+        co_wait_ge(c_conv + 4 * sc, (uint32_t)(kCoLW + YW) * rc, c_abort, status, kStLXnext, to);
+      }
 
       // contraction of this stream's 16 x CS slice: fresh MFMA chain
       const uint32_t sl = sbase + slot_of(j) * SLOT + (uint32_t)(w * C::STREAM);
@@ -698,10 +719,32 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
   };
   auto tok_of = [&](int l, int b) -> int { return 4 * ((v + YW * b) / H) + (l >> 4); };
 
-  // tile j into Xc (POST: x_next, formed from the slot's x, h_out and
-  // coefs, also written back into the slot for the contraction)
+  // tile j into Xc (POST: x_next; this wave forms row block v + 4 in the
+  // slot, the L-waves row blocks 0..3)
   auto copy = [&](int j, u32x4 (&Xc)[YB][4]) {
     co_wait_ge(c_landed + 4 * slot_of(j), (uint32_t)kCoLW * (round_of(j) + 1), c_abort, status, kStYLanded, to);
+    if constexpr (POST) {
+      static_assert(YB == 2 && 4 * C::STREAM == 32768, "row blocks v and v + 4; h_out at offset 32768");
+      const uint32_t sc = slot_of(j);
+      const uint32_t o = sbase + sc * SLOT + (uint32_t)((v + YW) * 1024 + lane * 16);
+      const uint32_t cs = cbase + sc * (uint32_t)(kCoef * 4);
+      int l = lane;  // an opaque lane index: addresses held across the loop would spill
+      asm volatile("" : "+v"(l));
+      const uint32_t tk = (uint32_t)tok_of(l, 1);
+      u32x4 Hh;
+      float hr[16], hp[4];
+      co_lds_rd4(Xc[1], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
+      co_lds_rd_post(Hh, hr, hp, o, cs + tk * 64u, cs + 1024u + tk * 16u);
+      co_post_chunk(Xc[1], Hh, hr, hp);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) co_lds_st4(o + (uint32_t)(n * C::STREAM), __builtin_bit_cast(floatx4, Xc[1][n]));
+      co_lds_inc(c_conv + 4 * sc);  // after the writes (a wave's LDS operations stay in order)
+      co_wait_ge(c_conv + 4 * sc, (uint32_t)(kCoLW + YW) * (round_of(j) + 1), c_abort, status, kStYLanded, to);
+      const uint32_t o0 = sbase + sc * SLOT + (uint32_t)(v * 1024 + lane * 16);
+      co_lds_rd4(Xc[0], o0, o0 + C::STREAM, o0 + 2 * C::STREAM, o0 + 3 * C::STREAM);
+      co_lds_inc(c_copied + 4 * sc);
+      return;
+    }
 #pragma unroll
     for (int b = 0; b < YB; ++b) {
       if constexpr (XS) {
@@ -714,26 +757,8 @@ __global__ __launch_bounds__(CoCfg<NCH>::THREADS) void pre_fwd_coop_kernel(CoopA
       } else {
         const uint32_t o = sbase + slot_of(j) * SLOT + (uint32_t)((v + YW * b) * 1024 + lane * 16);
         co_lds_rd4(Xc[b], o, o + C::STREAM, o + 2 * C::STREAM, o + 3 * C::STREAM);
-        if constexpr (POST) {
-          static_assert(4 * C::STREAM == 32768, "h_out's region at offset 32768 of a slot");
-          u32x4 Hh;
-          float hr[16], hp[4];
-          // the token's coefs addresses from an opaque copy of the lane index
-          // (held across the loop they would be spilled, and a scratch reload
-          // in this store-only wave waits for every store in flight)
-          int l = lane;
-          asm volatile("" : "+v"(l));
-          const uint32_t tk = (uint32_t)tok_of(l, b);
-          const uint32_t cs = cbase + slot_of(j) * (uint32_t)(kCoef * 4);
-          co_lds_rd_post(Hh, hr, hp, o, cs + tk * 64u, cs + 1024u + tk * 16u);
-          co_post_chunk(Xc[b], Hh, hr, hp);
-#pragma unroll
-          for (int n = 0; n < 4; ++n) co_lds_st4(o + (uint32_t)(n * C::STREAM), __builtin_bit_cast(floatx4, Xc[b][n]));
-        }
       }
     }
-    // (POST: the count is raised after the x_next writes: a wave's LDS
-    // operations are performed in order)
     co_lds_inc(c_copied + 4 * slot_of(j));
   };
   // POST: x_next of tile j's slice to HBM (rows past T fall outside the
