@@ -90,7 +90,7 @@ KERNEL_SUMMARY = os.path.join("profiles", "c5_chain_kernel_stats.json")
 # each operator's main kernel at the headline shape (the rest of an operator's
 # launches are zero fills, the per-token kernel A and fixed-order sums)
 MAIN_KERNEL = {
-    "pre_fwd": "pre_fwd_coop_kernel<32, false>",
+    "pre_fwd": "pre_fwd_coop_kernel<32, false, false>",
     "post_fwd": "post_fwd_block_kernel<4, bf16_t, true>",
     "post_bwd": "post_bwd_block_kernel<4, bf16_t, true, false, 1>",
     "pre_bwd": "pre_bwd_coop_kernel",
