@@ -54,6 +54,9 @@ _SIGNATURES = {
     "mhc_post_pre_fwd": (_c.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
                                     _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                     _i64, _i32, _i32, _vp]),
+    "mhc_post_pre_fwd_ex": (_c.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _vp, _f32, _f32, _f32,
+                                       _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp,
+                                       _i64, _i32, _i32, _vp]),
     "mhc_pre_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "mhc_pre_bwd": (_c.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _f32, _f32, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _sz,

@@ -445,12 +445,13 @@ extern "C" size_t mhc_post_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t 
   return mhc_pre_fwd_workspace_size(T, N, D, phi_dtype);
 }
 
-extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,
-                                int32_t x_dtype, const void* phi, int32_t phi_dtype, const float* alpha,
-                                const float* base, float norm_eps, float hc_eps, float clamp_min, float clamp_max,
-                                int32_t iter_times, void* x_next, void* y, float* post_out, float* comb_frag,
-                                float* inv_rms, float* mixes, float* h_res_logits, float* pre, void* workspace,
-                                size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream) {
+extern "C" int mhc_post_pre_fwd_ex(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                                   int32_t x_dtype, const void* phi, int32_t phi_dtype, const float* alpha,
+                                   const float* base, float norm_eps, float hc_eps, float clamp_min,
+                                   float clamp_max, int32_t iter_times, void* x_next, void* y, float* post_out,
+                                   float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits, float* pre,
+                                   void* workspace, size_t workspace_bytes, int32_t* status, int64_t T, int32_t N,
+                                   int32_t D, void* stream) {
   clear_error();
   if (T < 0 || D <= 0 || N <= 0)
     return set_error(MHC_ERR_INVALID, "mhc_post_pre_fwd: bad shape T=%lld N=%d D=%d", (long long)T, N, D);
@@ -465,7 +466,7 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
     bool used = false;
     const int rc = post_pre_fwd_single_pass(x, h_res, h_out, h_post, phi, alpha, base, norm_eps, hc_eps, clamp_min,
                                             clamp_max, iter_times, x_next, y, post_out, comb_frag, inv_rms, mixes,
-                                            h_res_logits, pre, workspace, workspace_bytes, T, D,
+                                            h_res_logits, pre, workspace, workspace_bytes, status, T, D,
                                             (hipStream_t)stream, &used);
     if (rc || used) return rc;
   }
@@ -479,9 +480,9 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
     // other
     int rc = mhc_post_fwd(x, h_res, h_out, h_post, x_next, T, N, D, x_dtype, stream);
     if (rc) return rc;
-    return mhc_pre_fwd(x_next, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
-                       iter_times, y, post_out, comb_frag, inv_rms, mixes, h_res_logits, pre, nullptr, workspace,
-                       workspace_bytes, T, N, D, stream);
+    return mhc_pre_fwd_ex(x_next, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps, clamp_min, clamp_max,
+                          iter_times, y, post_out, comb_frag, inv_rms, mixes, h_res_logits, pre, nullptr, workspace,
+                          workspace_bytes, status, T, N, D, stream);
   }
   PostPreArgs a{};
   a.x = static_cast<const bf16_t*>(x);
@@ -514,4 +515,15 @@ extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h
   hipLaunchKernelGGL(post_pre_fwd_kernel, dim3((unsigned)grid), dim3(kPPThreads), 0, (hipStream_t)stream, a);
   if (int rc = check_launch("post_pre_fwd")) return rc;
   return launch_pre_y_pass(x_next, a.pre_ws, y, T, N, D, (hipStream_t)stream);
+}
+
+extern "C" int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                                int32_t x_dtype, const void* phi, int32_t phi_dtype, const float* alpha,
+                                const float* base, float norm_eps, float hc_eps, float clamp_min, float clamp_max,
+                                int32_t iter_times, void* x_next, void* y, float* post_out, float* comb_frag,
+                                float* inv_rms, float* mixes, float* h_res_logits, float* pre, void* workspace,
+                                size_t workspace_bytes, int64_t T, int32_t N, int32_t D, void* stream) {
+  return mhc_post_pre_fwd_ex(x, h_res, h_out, h_post, x_dtype, phi, phi_dtype, alpha, base, norm_eps, hc_eps,
+                             clamp_min, clamp_max, iter_times, x_next, y, post_out, comb_frag, inv_rms, mixes,
+                             h_res_logits, pre, workspace, workspace_bytes, nullptr, T, N, D, stream);
 }

@@ -65,6 +65,8 @@ struct PreFwdArgs {
   // and copies the word to status_out (the caller's, may be null)
   const uint32_t* co_status;
   int32_t* status_out;
+  // fused post + pre form: x_next (T, N, D) bf16, also set to NaN on failure
+  void* x_next_nan;
 };
 
 template <int N, typename S, bool VEC, int P>
@@ -893,6 +895,10 @@ __global__ __launch_bounds__(kFwdThreads) void pre_fwd_finalize_kernel(PreFwdArg
     for (int64_t i = tid; i < nt * a.D; i += kFwdThreads) y[t0 * a.D + i] = 0x7FC0u;  // bf16 NaN
     if (a.x_scaled)
       for (int64_t i = tid; i < nt * N * a.D; i += kFwdThreads) a.x_scaled[t0 * N * a.D + i] = __builtin_nanf("");
+    if (a.x_next_nan) {
+      uint16_t* xn = static_cast<uint16_t*>(a.x_next_nan);
+      for (int64_t i = tid; i < nt * N * a.D; i += kFwdThreads) xn[t0 * N * a.D + i] = 0x7FC0u;
+    }
   }
   if (ok) {
     if (a.mixes) {
@@ -1234,8 +1240,8 @@ int post_pre_fwd_single_pass(const void* x, const float* h_res, const void* h_ou
                              const void* phi, const float* alpha, const float* base, float norm_eps, float hc_eps,
                              float clamp_min, float clamp_max, int32_t iter_times, void* x_next, void* y,
                              float* post_out, float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
-                             float* pre, void* workspace, size_t workspace_bytes, int64_t T, int32_t D,
-                             hipStream_t st, bool* used) {
+                             float* pre, void* workspace, size_t workspace_bytes, int32_t* status, int64_t T,
+                             int32_t D, hipStream_t st, bool* used) {
   *used = false;
   constexpr int N = 4;
   if (!pre_fwd_single_pass_applies(x, MHC_DTYPE_BF16, phi, MHC_DTYPE_BF16, y, workspace_bytes, T, N, D, st) ||
@@ -1265,6 +1271,8 @@ int post_pre_fwd_single_pass(const void* x, const float* h_res, const void* h_ou
   a.pre = pre;
   a.T = T;
   a.D = D;
+  a.status_out = status;
+  a.x_next_nan = x_next;
   CoopArgs post{};
   post.h_out = static_cast<const bf16_t*>(h_out);
   post.h_res = h_res;

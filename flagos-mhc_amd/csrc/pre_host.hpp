@@ -44,13 +44,14 @@ bool pre_fwd_single_pass_applies(const void* x, int32_t x_dtype, const void* phi
 
 // The fused post + pre forward in one pass (N = 4, bf16): x_next formed in
 // the single-pass pre kernel and written once.  *used is false (and nothing
-// ran) where that form does not apply.
+// ran) where that form does not apply.  `status` (may be null) receives the
+// single pass's status word, as mhc_pre_fwd_ex's.
 int post_pre_fwd_single_pass(const void* x, const float* h_res, const void* h_out, const float* h_post,
                              const void* phi, const float* alpha, const float* base, float norm_eps, float hc_eps,
                              float clamp_min, float clamp_max, int32_t iter_times, void* x_next, void* y,
                              float* post_out, float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
-                             float* pre, void* workspace, size_t workspace_bytes, int64_t T, int32_t D,
-                             hipStream_t st, bool* used);
+                             float* pre, void* workspace, size_t workspace_bytes, int32_t* status, int64_t T,
+                             int32_t D, hipStream_t st, bool* used);
 
 // Bytes the pre forward (and the fused post + pre forward) keep per call for
 // pre (T, N) and inv_rms (T,) between their contraction and y kernels.

@@ -264,9 +264,13 @@ int mhc_pre_bwd_ex(const void* x, int32_t x_dtype, const void* phi, int32_t phi_
  * Outputs: x_next = mhc_post(x, h_res, h_out, h_post) (T,N,D) `x_dtype`,
  * bit-identical to mhc_post_fwd; y, post_out, comb_frag and the optional
  * inv_rms, mixes, h_res_logits, pre of mhc_pre_fwd applied to x_next (no
- * x_scaled).  N = 4 with bf16 x, h_out and phi, D % 64 == 0, D >= 256 and
- * 16-byte aligned rows reads x once and writes x_next once (then reads
- * x_next back for y); every other shape runs mhc_post_fwd then mhc_pre_fwd.
+ * x_scaled).  N = 4 with bf16 x, h_out and phi and 16-byte aligned rows:
+ * where mhc_pre_fwd has its single pass (T >= 8192, D = 4096 or 7168..8192,
+ * the workspace from mhc_post_pre_fwd_workspace_size, no stream capture)
+ * that kernel forms x_next itself (x and h_out read once, x_next written
+ * once; outputs bit-identical to the two operators); other shapes with
+ * D % 64 == 0 and D >= 256 read x once and write x_next once, then read
+ * x_next back for y; every other shape runs mhc_post_fwd then mhc_pre_fwd.
  */
 size_t mhc_post_pre_fwd_workspace_size(int64_t T, int32_t N, int32_t D, int32_t phi_dtype);
 int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const float* h_post,
@@ -276,6 +280,22 @@ int mhc_post_pre_fwd(const void* x, const float* h_res, const void* h_out, const
                      float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
                      float* pre, void* workspace, size_t workspace_bytes, int64_t T, int32_t N,
                      int32_t D, void* stream);
+/*
+ * mhc_post_pre_fwd with a status word, as mhc_pre_fwd_ex: where the single
+ * pass runs (the one-pass fused form, or mhc_pre_fwd's single pass after
+ * mhc_post_fwd) a bounded wait that gives up makes every output of the call
+ * NaN (x_next included) and writes its failure code (> 0) to *status, 0 when
+ * every wait was satisfied; other forms leave *status untouched.
+ * mhc_post_pre_fwd is this call with status == NULL.  No counterpart in the
+ * reference.  Other arguments as in mhc_post_pre_fwd.
+ */
+int mhc_post_pre_fwd_ex(const void* x, const float* h_res, const void* h_out, const float* h_post,
+                        int32_t x_dtype, const void* phi, int32_t phi_dtype, const float* alpha,
+                        const float* base, float norm_eps, float hc_eps, float clamp_min,
+                        float clamp_max, int32_t iter_times, void* x_next, void* y, float* post_out,
+                        float* comb_frag, float* inv_rms, float* mixes, float* h_res_logits,
+                        float* pre, void* workspace, size_t workspace_bytes, int32_t* status, int64_t T,
+                        int32_t N, int32_t D, void* stream);
 
 #ifdef __cplusplus
 }

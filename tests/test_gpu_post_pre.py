@@ -159,3 +159,41 @@ def test_post_pre_autograd(T, D):
         w = _np(tb.grad)
         atol = (1e-2 if name in ("h_res", "h_post") else 2e-3) * np.abs(w).max()
         assert_close(ta.grad.float(), w, 2e-2, 2e-2 + atol, name + ".grad")
+
+
+def test_post_pre_one_pass_failure_is_loud():
+    """With the waits' limit forced to zero ticks from the host (the
+    mhc_debug_set_wait_limit test hook), the one-pass fused forward gives up
+    at its first unsatisfied wait and every kernel still exits: x_next, y and
+    the pre outputs are NaN, the status word reaches the package, and
+    check_errors raises RuntimeError.  With the normal limit restored the
+    next call equals the two operators again."""
+    from FlagOS_mhc import _lib
+
+    T, N, D = 8192, 4, 7168
+    x, h_res, h_out, h_post, phi, alpha, base = _inputs(T, N, D, torch.bfloat16, seed=5)
+    lib = _lib.load()
+    m.check_errors()  # nothing pending that failed
+    try:
+        lib.mhc_debug_set_wait_limit(0)
+        x_next, out = m.mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post, phi, alpha, base,
+                                                    need_backward=True, **KW)
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(x_next.float()).all()), "x_next"
+        for k in ("y",) + FWD_KEYS:
+            assert bool(torch.isnan(out[k].float()).all()), k
+        with pytest.raises(RuntimeError, match="bounded wait"):
+            m.check_errors()
+    finally:
+        lib.mhc_debug_set_wait_limit(-1)
+        torch.cuda.synchronize()
+    m.check_errors()
+    x_next, out = m.mhc_post_pre_clamp_sinkhorn(x, h_res, h_out, h_post, phi, alpha, base,
+                                                need_backward=True, **KW)
+    x_ref = m.mhc_post(x, h_res, h_out, h_post)
+    ref = m.mhc_pre_clamp_sinkhorn(x_ref, phi, alpha, base, need_backward=True, **KW)
+    torch.cuda.synchronize()
+    assert torch.equal(x_next, x_ref)
+    for k in ("y",) + FWD_KEYS:
+        assert torch.equal(out[k], ref[k]), k
+    m.check_errors()
