@@ -31,7 +31,7 @@
 // pre_bwd_dma_kernel).  Per iteration j (tile j landing, tile u = j - 2 in
 // phase 2):
 //   * direct-to-LDS loads of tile j + 2: x into 3 slots of 32 KB, grad_y,
-//     kernel A's grad_mixes rows and records into 4 slots of 11 KB;
+//     kernel A's grad_mixes rows and records into 4 slots of 10.5 KB;
 //   * phase 1 of tile j: copy its x into a ring of two tiles of registers
 //     (freeing the slot) and sum grad_y . x per token over the wave's
 //     columns (v_dot2_f32_bf16), then over the 16 lanes of a row (DPP); the
@@ -41,8 +41,10 @@
 //     the group's ring;
 //   * exchange of tile u: wave w polls chunk w of every member's record (4
 //     direct-to-LDS loads, lane = (member, word)), adds over members in a
-//     fixed order and forms each token's grad_mixes[0..3], g = grad_mixes
-//     inv and scale in LDS;
+//     fixed order, forms its four tokens' grad_mixes[0..3] and scale, and
+//     writes its share of the tile's phase-2 operands that all four waves
+//     use (g = grad_mixes inv in both bf16 planes as MFMA A operands, the
+//     diagonal words of pre and scale) to LDS, once for the block;
 //   * phase 2 of tile u: grad_phi partial += g^T @ x and grad_x = diag(pre)
 //     grad_y + diag(scale) x + (grad_mixes inv) @ phi on the matrix cores
 //     (16x16x32 MFMAs, both bf16 planes of each fp32 factor), grad_x stored
@@ -70,11 +72,17 @@ constexpr int kBcTT = 16;                 // tokens per tile
 constexpr int kBcWaves = 4;               // one per stream
 constexpr int kBcLag = 2;                 // phase 2 of tile j - 2 while tile j lands
 constexpr int kBcSx = 3;                  // x slots of 32 KB
-constexpr int kBcSg = 4;                  // grad_y / per-token slots of 11 KB
-constexpr int kBcGSlot = 11 * 1024;       // grad_y (8 KB) + coefX (1 KB) + grad_mixes rows (1.5 KB) + pad
+constexpr int kBcSg = 4;                  // grad_y / per-token slots of 10.5 KB
+constexpr int kBcGSlot = 10752;           // grad_y (8 KB) + coefX (1 KB) + grad_mixes rows (1.5 KB)
 constexpr int kBcCoef = 8 * 1024;         // offset of coefX in a grad_y slot
 constexpr int kBcGm = 9 * 1024;           // offset of the grad_mixes rows [16][24] fp32
-constexpr int kBcRS = 2;                  // ready slots (per-token results of the exchange)
+// The shared phase-2 operands of a tile (opw, bytes): the A operands of the
+// grad_mixes @ phi product (hi / lo planes, lane (r, q): token r, m = 8 q ..
+// 8 q + 7), of the grad_phi products (rows m = 16 mt + r, lane (r, q): tokens
+// 4 q .. 4 q + 3, both planes), and the diagonal words (hi | lo << 16) of
+// pre[16][4] and scale[16]; entries no wave writes (m >= 24) stay zero.
+constexpr int kBcOpA0 = 0, kBcOpA1 = 1024, kBcOpT0 = 2048, kBcOpT1 = 3072, kBcOpPre = 4096, kBcOpSc = 4352;
+constexpr int kBcOpBytes = 4416;
 constexpr int kBcR = 16;                  // exchange ring: tiles per group
 constexpr int kBcChunkWords = 8;          // a record chunk: 16 sums (4 tokens x 4 streams), word w = (v_w, v_{w+8}, tag, tag)
 constexpr int kBcRecWords = 4 * kBcChunkWords;  // a member's record of a tile: 4 chunks
@@ -171,51 +179,52 @@ __device__ __forceinline__ void bc_rd_phase1(u32x4 (&x)[2][4], u32x4 (&g)[2][4],
       : "memory");
 }
 
-// Phase 2, first batch: grad_mixes of token r (m = 8 q ..: two reads at ga),
-// the exchange's pre-head grad_mixes of token r (gg), the inv_rms of tokens
-// 4 q .. 4 q + 3 (ia + 64 i), pre[r][n], inv_rms[r] and scale[r] of token r
-// (pr, ir, sr), and the half-1 grad_y units (g1, 1 KB apart); one wait.
-__device__ __forceinline__ void bc_rd_phase2a(u32x4& gl, u32x4& gh, u32x4& g4, float (&inv)[4], float& pre_r,
-                                              float& inv_r, float& sc_r, u32x4 (&gr)[4], uint32_t ga, uint32_t gg,
-                                              uint32_t ia, uint32_t pr, uint32_t ir, uint32_t sr, uint32_t g1) {
-  uint32_t iv[4], p, i, c;
+// Phase 2's operands in one batch of reads: the shared A operands at oa
+// (kBcOpA0 / A1 / T0 / T1 from the tile's opw), the diagonal words of pre[r][n]
+// and scale[r] (pa, sa), and the lane's grad_y units of both halves (g1:
+// half 1, g0: half 0, 1 KB apart); one wait.
+__device__ __forceinline__ void bc_rd_ops(u32x4& a0, u32x4& a1, u32x4& t0, u32x4& t1, uint32_t& pw, uint32_t& sw,
+                                          u32x4 (&g1)[4], u32x4 (&g0)[4], uint32_t oa, uint32_t pa, uint32_t sa,
+                                          uint32_t ga1, uint32_t ga0) {
+  static_assert(kBcOpA0 == 0 && kBcOpA1 == 1024 && kBcOpT0 == 2048 && kBcOpT1 == 3072, "offsets below");
   asm volatile(
       "ds_read_b128 %0, %14\n\t"
-      "ds_read_b128 %1, %14 offset:16\n\t"
-      "ds_read_b128 %2, %15\n\t"
-      "ds_read_b32 %3, %16\n\t"
-      "ds_read_b32 %4, %16 offset:64\n\t"
-      "ds_read_b32 %5, %16 offset:128\n\t"
-      "ds_read_b32 %6, %16 offset:192\n\t"
-      "ds_read_b32 %7, %17\n\t"
-      "ds_read_b32 %8, %18\n\t"
-      "ds_read_b32 %9, %19\n\t"
-      "ds_read_b128 %10, %20\n\t"
-      "ds_read_b128 %11, %20 offset:1024\n\t"
-      "ds_read_b128 %12, %20 offset:2048\n\t"
-      "ds_read_b128 %13, %20 offset:3072\n\t"
+      "ds_read_b128 %1, %14 offset:1024\n\t"
+      "ds_read_b128 %2, %14 offset:2048\n\t"
+      "ds_read_b128 %3, %14 offset:3072\n\t"
+      "ds_read_b32 %4, %15\n\t"
+      "ds_read_b32 %5, %16\n\t"
+      "ds_read_b128 %6, %17\n\t"
+      "ds_read_b128 %7, %17 offset:1024\n\t"
+      "ds_read_b128 %8, %17 offset:2048\n\t"
+      "ds_read_b128 %9, %17 offset:3072\n\t"
+      "ds_read_b128 %10, %18\n\t"
+      "ds_read_b128 %11, %18 offset:1024\n\t"
+      "ds_read_b128 %12, %18 offset:2048\n\t"
+      "ds_read_b128 %13, %18 offset:3072\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(gl), "=&v"(gh), "=&v"(g4), "=&v"(iv[0]), "=&v"(iv[1]), "=&v"(iv[2]), "=&v"(iv[3]), "=&v"(p),
-        "=&v"(i), "=&v"(c), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]), "=&v"(gr[3])
-      : "v"(ga), "v"(gg), "v"(ia), "v"(pr), "v"(ir), "v"(sr), "v"(g1)
+      : "=&v"(a0), "=&v"(a1), "=&v"(t0), "=&v"(t1), "=&v"(pw), "=&v"(sw), "=&v"(g1[0]), "=&v"(g1[1]), "=&v"(g1[2]),
+        "=&v"(g1[3]), "=&v"(g0[0]), "=&v"(g0[1]), "=&v"(g0[2]), "=&v"(g0[3])
+      : "v"(oa), "v"(pa), "v"(sa), "v"(ga1), "v"(ga0)
       : "memory");
-#pragma unroll
-  for (int k = 0; k < 4; ++k) inv[k] = __uint_as_float(iv[k]);
-  pre_r = __uint_as_float(p);
-  inv_r = __uint_as_float(i);
-  sc_r = __uint_as_float(c);
 }
 
 // The A operand of a 16x16x32 MFMA holding diag(v) over a tile's 16 tokens in
 // both bf16 planes (k = 8 q + 2 e + p: token 4 q + e, plane p; paired with a
-// bc_col2 B operand): lane (r, q) holds row r, so only the lane with
-// q == r / 4 has a nonzero dword, e = r % 4, the planes' bits hi | lo << 16.
-__device__ __forceinline__ u32x4 bc_diag2(float v, int r, int q) {
-  uint32_t hi, lo;
-  split2_bf16(v, hi, lo);
-  const uint32_t d = q == (r >> 2) ? (hi | (lo << 16)) : 0u;
+// bc_col2 B operand) from v's word w = hi | lo << 16: lane (r, q) holds row r,
+// so only the lane with q == r / 4 has a nonzero dword, e = r % 4.
+__device__ __forceinline__ u32x4 bc_diagw(uint32_t w, int r, int q) {
+  const uint32_t d = q == (r >> 2) ? w : 0u;
   const int e = r & 3;
   return u32x4{e == 0 ? d : 0u, e == 1 ? d : 0u, e == 2 ? d : 0u, e == 3 ? d : 0u};
+}
+
+// v's two bf16 planes as one word, hi | lo << 16 (the dword of a diagonal or
+// grad_phi A operand)
+__device__ __forceinline__ uint32_t bc_word2(float v) {
+  uint32_t hi, lo;
+  split2_bf16(v, hi, lo);
+  return hi | (lo << 16);
 }
 
 // Column c of a lane's 4-token x 8-column block of bf16 (m[e][c / 2] holds
@@ -229,73 +238,57 @@ __device__ __forceinline__ u32x4 bc_col2(const u32x4 (&m)[4], int C) {
                __builtin_amdgcn_perm(m[2][w], m[2][w], sel), __builtin_amdgcn_perm(m[3][w], m[3][w], sel)};
 }
 
-// Phase 2, second batch: for tokens 4 q + i, the exchange's g of row r (ra +
-// 16 i), grad_mixes rows r (ma + 96 i) and 16 + r % 8 (mb + 96 i), and the
-// half-0 grad_y units (g0, 1 KB apart); one wait.
-__device__ __forceinline__ void bc_rd_phase2b(float (&ge)[4], float (&m0)[4], float (&m1)[4], u32x4 (&gr)[4],
-                                              uint32_t ra, uint32_t ma, uint32_t mb, uint32_t g0) {
-  uint32_t a[4], b[4], c[4];
-  asm volatile(
-      "ds_read_b32 %0, %16\n\t"
-      "ds_read_b32 %1, %16 offset:16\n\t"
-      "ds_read_b32 %2, %16 offset:32\n\t"
-      "ds_read_b32 %3, %16 offset:48\n\t"
-      "ds_read_b32 %4, %17\n\t"
-      "ds_read_b32 %5, %17 offset:96\n\t"
-      "ds_read_b32 %6, %17 offset:192\n\t"
-      "ds_read_b32 %7, %17 offset:288\n\t"
-      "ds_read_b32 %8, %18\n\t"
-      "ds_read_b32 %9, %18 offset:96\n\t"
-      "ds_read_b32 %10, %18 offset:192\n\t"
-      "ds_read_b32 %11, %18 offset:288\n\t"
-      "ds_read_b128 %12, %19\n\t"
-      "ds_read_b128 %13, %19 offset:1024\n\t"
-      "ds_read_b128 %14, %19 offset:2048\n\t"
-      "ds_read_b128 %15, %19 offset:3072\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]),
-        "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]), "=&v"(gr[0]), "=&v"(gr[1]), "=&v"(gr[2]),
-        "=&v"(gr[3])
-      : "v"(ra), "v"(ma), "v"(mb), "v"(g0)
-      : "memory");
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    ge[i] = __uint_as_float(a[i]);
-    m0[i] = __uint_as_float(b[i]);
-    m1[i] = __uint_as_float(c[i]);
-  }
-}
-
 // The poll buffer's four 1 KB units (the lane's 16 bytes of each, at pa)
-// and four 4-byte reads (cz, mix, inv, scale without the pre head), one wait
-__device__ __forceinline__ void bc_rd_poll(u32x4 (&p)[4], float& cz, float& mix, float& inv, float& sk, uint32_t pa,
-                                           uint32_t ca, uint32_t cb) {
-  uint32_t v[4];
+// and five 4-byte reads (pre, cz, mix, inv, scale without the pre head), one
+// wait
+__device__ __forceinline__ void bc_rd_poll(u32x4 (&p)[4], float& pre, float& cz, float& mix, float& inv, float& sk,
+                                           uint32_t pa, uint32_t ca, uint32_t cb) {
+  uint32_t v[5];
   asm volatile(
-      "ds_read_b128 %0, %8\n\t"
-      "ds_read_b128 %1, %8 offset:1024\n\t"
-      "ds_read_b128 %2, %8 offset:2048\n\t"
-      "ds_read_b128 %3, %8 offset:3072\n\t"
-      "ds_read_b32 %4, %9 offset:16\n\t"
-      "ds_read_b32 %5, %9 offset:32\n\t"
-      "ds_read_b32 %6, %10 offset:48\n\t"
-      "ds_read_b32 %7, %10 offset:52\n\t"
+      "ds_read_b128 %0, %9\n\t"
+      "ds_read_b128 %1, %9 offset:1024\n\t"
+      "ds_read_b128 %2, %9 offset:2048\n\t"
+      "ds_read_b128 %3, %9 offset:3072\n\t"
+      "ds_read_b32 %4, %10\n\t"
+      "ds_read_b32 %5, %10 offset:16\n\t"
+      "ds_read_b32 %6, %10 offset:32\n\t"
+      "ds_read_b32 %7, %11 offset:48\n\t"
+      "ds_read_b32 %8, %11 offset:52\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(p[0]), "=&v"(p[1]), "=&v"(p[2]), "=&v"(p[3]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "=&v"(p[0]), "=&v"(p[1]), "=&v"(p[2]), "=&v"(p[3]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]),
+        "=&v"(v[4])
       : "v"(pa), "v"(ca), "v"(cb)
       : "memory");
-  cz = __uint_as_float(v[0]);
-  mix = __uint_as_float(v[1]);
-  inv = __uint_as_float(v[2]);
-  sk = __uint_as_float(v[3]);
+  pre = __uint_as_float(v[0]);
+  cz = __uint_as_float(v[1]);
+  mix = __uint_as_float(v[2]);
+  inv = __uint_as_float(v[3]);
+  sk = __uint_as_float(v[4]);
+}
+
+// Two 4-byte reads, one wait: the grad_mixes rows' pair at a (8-byte
+// aligned) and the word at b
+__device__ __forceinline__ void bc_rd_pair(float& x0, float& x1, float& y, uint32_t a, uint32_t b) {
+  u32x2 v;
+  uint32_t w;
+  asm volatile(
+      "ds_read_b64 %0, %2\n\t"
+      "ds_read_b32 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v), "=&v"(w)
+      : "v"(a), "v"(b)
+      : "memory");
+  x0 = __uint_as_float(v[0]);
+  x1 = __uint_as_float(v[1]);
+  y = __uint_as_float(w);
 }
 
 __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a) {
   constexpr int M = 24, C = 3 + M;
   __shared__ __align__(1024) u32x4 xs[kBcSx * 32 * kWave];           // 96 KB: [slot][stream][h][e] 1 KB units
-  __shared__ __align__(1024) u32x4 gsl[kBcSg * kBcGSlot / 16];       // 44 KB
+  __shared__ __align__(1024) u32x4 gsl[kBcSg * kBcGSlot / 16];       // 42 KB
   __shared__ __align__(1024) u32x4 pbuf[kBcWaves * kBcPollKB * kWave];  // 16 KB: each wave's poll
-  __shared__ __align__(16) float rdy[kBcRS][144];                    // gm[16][4], g[16][4], scale[16]
+  __shared__ __align__(16) uint32_t opw[kBcOpBytes / 4];             // the shared phase-2 operands
   __shared__ __align__(16) float pp[2][kBcWaves][kBcTT];             // phase-1 partials
   __shared__ __align__(16) float red[kBcWaves][8];                   // end: the waves' contributions
   // counters: abort at 22
@@ -313,6 +306,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   uint32_t* status = a.ctl + kCtlStatus;
 
   if (tid < 32) cnt[tid] = 0u;
+  for (int i = tid; i < kBcOpBytes / 4; i += kBcThreads) opw[i] = 0u;
   if (tid == 0) co_register(a.ctl, G, a.maxg, to, info);
   __syncthreads();
   const int group = info[0], ngroups = info[1], member = info[2];
@@ -326,7 +320,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   u32x4* recw = a.rec + (size_t)group * kBcR * G * kBcRecWords;
   const auto ring = rows_rsrc(recw, (int64_t)kBcR * G * kBcRecWords * 16);
   const uint32_t xs_l = lds_addr(xs), gs_l = lds_addr(gsl), pb_l = lds_addr(pbuf) + wave * kBcPollKB * 1024;
-  const uint32_t rdy_l = lds_addr(&rdy[0][0]), pp_l = lds_addr(&pp[0][0][0]);
+  const uint32_t opw_l = lds_addr(opw), pp_l = lds_addr(&pp[0][0][0]);
   const uint32_t c_ab = lds_addr(cnt) + 88;
   const int kg = wave < 3 ? 3 : 2;  // grad_y / per-token loads this wave issues per tile
   constexpr int npoll = kBcPollKB;  // poll loads a wave issues per tile
@@ -369,9 +363,12 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
                                                off, 0, 0, 2 /* nt */);
     }
     if (wave < 2) {
+      // wave 1: the 512 bytes past the first 1 KB, from lanes 0..31 (the
+      // others are masked off and write nothing)
       const auto rm = rows_rsrc(a.gm + t0 * M, (int64_t)nv * M * 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void_t*)(uintptr_t)(slot + kBcGm + wave * 1024), 16,
-                                               (uint32_t)(wave * 1024 + 16 * lane), 0, 0, 0);
+      if (wave == 0 || lane < 32)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_void_t*)(uintptr_t)(slot + kBcGm + wave * 1024), 16,
+                                                 (uint32_t)(wave * 1024 + 16 * lane), 0, 0, 0);
     } else if (wave == 2) {
       const auto rc = rows_rsrc(a.coefX + t0 * 16, (int64_t)nv * 64);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_void_t*)(uintptr_t)(slot + kBcCoef), 16,
@@ -437,8 +434,8 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   // returns at once, and the loads and stores stay in range); the sum
   // kernel then replaces the outputs with NaN.  Block barriers order
   // the waves ((F): the exchange results ready; (I): phase 2 of tile u done,
-  // which frees its grad_y slot and, for tile u + 1, the ready slot of tile
-  // u - 1; (A): tile j landed, which also frees every buffer iteration j - 1
+  // which frees its grad_y slot and, for tile u + 1, the operands' buffer;
+  // (A): tile j landed, which also frees every buffer iteration j - 1
   // read); every wave runs the same iterations, so each barrier is reached
   // by all four (the bounded waits end, failed or not); a fourth after
   // (B) gives the publisher every wave's partials of tile j.
@@ -446,8 +443,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
     const int u = j - kBcLag;
     const bool pub_prev = (j & 3) == wave;  // this wave published tile j - 1's record
     if (u >= 0 && u < nq) {
-      const int rs = u & 1;
-      const uint32_t rslot = bc_opq(rdy_l) + (uint32_t)(rs * 144 * 4);
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
       // ---- (E) this wave's share of the exchange of tile u -------------------
       {
@@ -465,12 +460,12 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         // lane v < 16 of the chunk: token t = 4 wave + v / 4, stream v % 4
         const int t = 4 * wave + ((lane & 15) >> 2), nn = lane & 3;
         const uint32_t cf = gslot + kBcCoef + (uint32_t)(t * 64);
-        float cz, mix, inv, sk;
+        float pre, cz, mix, inv, sk;
         for (;;) {
           // lane l: word w = l % 8 of members l / 8 + 8 k, k = 0..3; every
           // valid word of the G members must carry this tile's tag
           u32x4 v[4];
-          bc_rd_poll(v, cz, mix, inv, sk, bc_opq(pb_l) + (uint32_t)(16 * lane), cf + 4 * nn, cf);
+          bc_rd_poll(v, pre, cz, mix, inv, sk, bc_opq(pb_l) + (uint32_t)(16 * lane), cf + 4 * nn, cf);
           uint32_t cur = 0;
 #pragma unroll
           for (int k = 0; k < 4; ++k) cur += (uint32_t)__popcll(__ballot(v[k][2] == tag));
@@ -502,15 +497,53 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         const float gmv = gz * a0;
         const float sd = group_sum<3>(gmv * mix);
         const float sc = sk - inv * inv * sd * invK;
-        // ready slot rs held tile u - 2's results: every wave finished phase 2
-        // of tile u - 1 (the barrier before (I) of the last iteration), so of
-        // u - 2
-        const bool owner = own == member;  // the tile's owner adds its grad_alpha[0] / grad_base terms
-        if (lane < 16) {
-          co_lds_st(rslot + (uint32_t)(4 * (4 * t + nn)), gmv);
-          co_lds_st(rslot + (uint32_t)(256 + 4 * (4 * t + nn)), gmv * inv);
-          if (nn == 0) co_lds_st(rslot + (uint32_t)(512 + 4 * t), sc);
+        // The tile's shared phase-2 operands for this wave's tokens 4 wave ..
+        // 4 wave + 3 (opw held tile u - 1's: every wave finished phase 2 of
+        // it before the barrier of (I) in the last iteration).  Lane l forms
+        // g = grad_mixes * inv of token rt = 4 wave + l / 16 at m0 = 8 fq +
+        // 2 fp and m0 + 1 (fq = l / 4 % 4, fp = l % 4; m < 4 from the
+        // exchange, whose value (token rt, m) every 16 lanes hold at lane
+        // 4 (l / 16) + m), and writes both planes into the A operands of the
+        // grad_mixes @ phi product (lane (rt, fq)) and of the grad_phi
+        // product (rows m: lane (m % 16, wave), dword l / 16)
+        {
+          const uint32_t ob = bc_opq(opw_l);
+          const int tl = lane >> 4, fq = (lane >> 2) & 3, fp = lane & 3;
+          const int m0 = 8 * fq + 2 * fp, rt = 4 * wave + tl;
+          const float e0 = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * tl + (m0 & 3)), __float_as_int(gmv)));
+          const float e1 = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * tl + (m0 & 3) + 1), __float_as_int(gmv)));
+          float g0, g1, ir;
+          bc_rd_pair(g0, g1, ir, gslot + kBcGm + (uint32_t)((rt * M + (m0 < M ? m0 : 0)) * 4),
+                     gslot + kBcCoef + (uint32_t)(rt * 64 + 48));
+          const float s0 = m0 < 4 ? e0 : g0, s1 = m0 < 4 ? e1 : g1;
+          float f0 = s0 * ir, f1 = s1 * ir;
+          const uint32_t h0 = f32_to_bf16_bits(f0), h1 = f32_to_bf16_bits(f1);
+          if (fq < 3) {
+            // lo plane of the gs operand: the residual of the exact product
+            // (one fma)
+            const uint32_t l0 = f32_to_bf16_bits(fmaf(s0, ir, -bf16_bits_to_f32(h0)));
+            const uint32_t l1 = f32_to_bf16_bits(fmaf(s1, ir, -bf16_bits_to_f32(h1)));
+            const uint32_t aa = ob + (uint32_t)(16 * (16 * fq + rt) + 4 * fp);
+            co_lds_st(aa + kBcOpA0, __uint_as_float(h0 | (h1 << 16)));
+            co_lds_st(aa + kBcOpA1, __uint_as_float(l0 | (l1 << 16)));
+          }
+          if (m0 < M) {
+            // lo plane of the grad_phi operand: the residual of the rounded
+            // product (kept opaque, so no fma forms)
+            asm volatile("" : "+v"(f0), "+v"(f1));
+            const uint32_t l0 = f32_to_bf16_bits(f0 - bf16_bits_to_f32(h0));
+            const uint32_t l1 = f32_to_bf16_bits(f1 - bf16_bits_to_f32(h1));
+            // m0 and m0 + 1 share a row block (m0 is even): lanes m0 % 16 and + 1
+            const uint32_t ta = ob + kBcOpT0 + (uint32_t)((m0 >> 4) * 1024 + 16 * ((m0 & 15) + 16 * wave) + 4 * tl);
+            co_lds_st(ta, __uint_as_float(h0 | (l0 << 16)));
+            co_lds_st(ta + 16, __uint_as_float(h1 | (l1 << 16)));
+          }
+          if (lane < 16) {
+            co_lds_st(ob + kBcOpPre + (uint32_t)(4 * (4 * t + nn)), __uint_as_float(bc_word2(pre)));
+            if (nn == 0) co_lds_st(ob + kBcOpSc + (uint32_t)(4 * t), __uint_as_float(bc_word2(sc)));
+          }
         }
+        const bool owner = own == member;  // the tile's owner adds its grad_alpha[0] / grad_base terms
         if (owner && lane < 16) {
           acc_c0 = fmaf(gz, mix, acc_c0);
           acc_b += gz;
@@ -524,49 +557,21 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
     if (u + 1 >= 0 && u + 1 < nq) issue_poll(u + 1);
     if (u >= 0 && u < nq) {
       // ---- (H) phase 2 of tile u --------------------------------------------
-      const int rs = u & 1;
-      const uint32_t rslot = bc_opq(rdy_l) + (uint32_t)(rs * 144 * 4);
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
-      const uint32_t gmb = gslot + kBcGm, cfb = gslot + kBcCoef;
-      // operands from the slot and the exchange, in two batches of reads:
-      // gA = grad_mixes * inv of token r, m = 8 q .. 8 q + 7 (hi / lo planes;
-      // m < 4 from the exchange, m >= 24 zero); gt[mt] = g = grad_mixes * inv
-      // of row m = 16 mt + r for tokens 4 q .. 4 q + 3 (dword e: token e's hi
-      // and lo planes; m < 4 from the exchange); diag(pre[., n]) and
-      // diag(scale) over the tile's tokens; grad_y of both halves
+      // operands: gA = grad_mixes * inv of token r, m = 8 q .. 8 q + 7 (hi /
+      // lo planes); gt[mt] = g = grad_mixes * inv of row m = 16 mt + r for
+      // tokens 4 q .. 4 q + 3 (dword e: token e's hi and lo planes);
+      // diag(pre[., n]) and diag(scale) over the tile's tokens; grad_y of
+      // both halves
       u32x4 gA0, gA1, gt[2], grh[2][4], dpre, dsc;
       {
-        u32x4 gl, gh, g4;
-        float inv_e[4], pre_r, inv_r, sc_r;
-        bc_rd_phase2a(gl, gh, g4, inv_e, pre_r, inv_r, sc_r, grh[1],
-                      gmb + (uint32_t)((r * M + 8 * (q < 3 ? q : 2)) * 4), rslot + (uint32_t)(16 * r),
-                      cfb + (uint32_t)(256 * q + 48), cfb + (uint32_t)(64 * r + 4 * n), cfb + (uint32_t)(64 * r + 48),
-                      rslot + (uint32_t)(512 + 4 * r), gslot + (uint32_t)(4096 + 16 * lane));
-        float ge[4], m0[4], m1[4];
-        bc_rd_phase2b(ge, m0, m1, grh[0], rslot + (uint32_t)(256 + 64 * q + 4 * (r & 3)),
-                      gmb + (uint32_t)((96 * 4 * q) + 4 * r), gmb + (uint32_t)((96 * 4 * q) + 64 + 4 * (r & 7)),
-                      gslot + (uint32_t)(16 * lane));
-        float f[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f[i] = (q == 0 ? __uint_as_float(g4[i]) : (q < 3 ? __uint_as_float(gl[i]) : 0.f)) * inv_r;
-          f[4 + i] = (q < 3 ? __uint_as_float(gh[i]) : 0.f) * inv_r;
-        }
-        split8(f, gA0, gA1);
-        uint32_t hi[2][4], lo[2][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float g0 = r < 4 ? ge[i] : m0[i] * inv_e[i];
-          const float g1 = r < 8 ? m1[i] * inv_e[i] : 0.f;
-          split2_bf16(g0, hi[0][i], lo[0][i]);
-          split2_bf16(g1, hi[1][i], lo[1][i]);
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-          gt[mt] = u32x4{hi[mt][0] | (lo[mt][0] << 16), hi[mt][1] | (lo[mt][1] << 16), hi[mt][2] | (lo[mt][2] << 16),
-                         hi[mt][3] | (lo[mt][3] << 16)};
-        dpre = bc_diag2(pre_r, r, q);
-        dsc = bc_diag2(sc_r, r, q);
+        const uint32_t ob = bc_opq(opw_l);
+        uint32_t pw, sw;
+        bc_rd_ops(gA0, gA1, gt[0], gt[1], pw, sw, grh[1], grh[0], ob + (uint32_t)(16 * lane),
+                  ob + kBcOpPre + (uint32_t)(4 * (4 * r + n)), ob + kBcOpSc + (uint32_t)(4 * r),
+                  gslot + (uint32_t)(4096 + 16 * lane), gslot + (uint32_t)(16 * lane));
+        dpre = bc_diagw(pw, r, q);
+        dsc = bc_diagw(sw, r, q);
       }
       const int64_t t0 = t0_of(u);
       const int nv = nv_of(t0);
@@ -617,7 +622,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           __builtin_amdgcn_raw_buffer_store_b128(u32x4{o[e][0], o[e][1], o[e][2], o[e][3]}, rgx, off, 0, 2 /* nt */);
         }
       }
-      // ---- (I) every wave done with tile u (its grad_y slot and ready slot),
+      // ---- (I) every wave done with tile u (its grad_y slot and operands),
       // then grad_y / per-token data of tile j + 2 into the slot ---------------
       bc_sync();
       if (j + 2 < nq) issue_g(j + 2);
@@ -706,14 +711,14 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
     const int iters = nq + kBcLag;
     for (int j = 0; j < iters; ++j) {
       step(j, XP);
+      // v_swap_b32 exchanges the two registers in place (a swap written in C++
+      // becomes three moves a register)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const u32x4 t = XP[hh][e];
-          XP[hh][e] = XQ[hh][e];
-          XQ[hh][e] = t;
-        }
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) asm volatile("v_swap_b32 %0, %1" : "+v"(XP[hh][e][w]), "+v"(XQ[hh][e][w]));
     }
   }
   wait_vmcnt<0>();  // no direct-to-LDS load may outlive the block
