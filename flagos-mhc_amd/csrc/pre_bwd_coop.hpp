@@ -633,11 +633,12 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
     if (j < nq) {
       // ---- (A) tile j landed ---------------------------------------------
       // operations this wave issued after tile j's x loads (iteration j - 1:
-      // poll (3), stores (8), grad_y loads (kg), record (its publisher), x
-      // loads (8); iteration j: poll (3), stores (8), grad_y loads (kg));
-      // away from the steady state all of them
+      // poll (npoll = 4), stores (8), grad_y loads (kg), record (its
+      // publisher), x loads (8); iteration j: poll (4), stores (8), grad_y
+      // loads (kg)); away from the steady state all of them
+      static_assert(npoll == 4, "the wait below counts four poll loads an iteration");
       if (j >= 3 && j + 2 < nq)
-        bc_wait_steady<30, 2>(kg, pub_prev);
+        bc_wait_steady<32, 2>(kg, pub_prev);
       else
         wait_vmcnt<0>();
       // Every wave past this point: tile j's x and grad_y slots landed (each
