@@ -266,8 +266,8 @@ __device__ __forceinline__ void bc_rd_poll(u32x4 (&p)[4], float& pre, float& cz,
   sk = __uint_as_float(v[4]);
 }
 
-// Two 4-byte reads, one wait: the grad_mixes rows' pair at a (8-byte
-// aligned) and the word at b
+// One 8-byte read (the grad_mixes rows' pair at a, 8-byte aligned) and one
+// 4-byte read (the word at b), one wait
 __device__ __forceinline__ void bc_rd_pair(float& x0, float& x1, float& y, uint32_t a, uint32_t b) {
   u32x2 v;
   uint32_t w;
@@ -306,6 +306,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   uint32_t* status = a.ctl + kCtlStatus;
 
   if (tid < 32) cnt[tid] = 0u;
+  // the operand entries of m >= 24 are never written: zero for every tile
   for (int i = tid; i < kBcOpBytes / 4; i += kBcThreads) opw[i] = 0u;
   if (tid == 0) co_register(a.ctl, G, a.maxg, to, info);
   __syncthreads();
