@@ -423,10 +423,11 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   //   (E) this wave's share of the exchange of tile u (chunk `wave`: tokens
   //       4 wave .. 4 wave + 3), (F) wait for all four shares, (G) this
   //       wave's poll of tile u + 1, (H) phase 2 of tile u from Xr with its
-  //       stores, (I) tile j + 2's grad_y loads into tile u's slot,
-  //   (A) tile j landed, (B) phase 1 of tile j into Xr (the registers phase
-  //       2 just released), (D) the record of tile j (its publisher), (C)
-  //       tile j + 2's x loads.
+  //       stores,
+  //   (A) tile j landed, then tile j + 2's grad_y loads into tile u's slot,
+  //       (B) phase 1 of tile j into Xr (the registers phase 2 just
+  //       released), (D) the record of tile j (its publisher), (C) tile
+  //       j + 2's x loads.
   // So only two tiles of x sit in registers at a time.  The poll is issued
   // before this iteration's stores and loads, so it completes after older
   // work only.  Every index is a 32-bit scalar; every wait on a counter is a
@@ -434,12 +435,12 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   // the loop run to its end on whatever the buffers hold (every later wait
   // returns at once, and the loads and stores stay in range); the sum
   // kernel then replaces the outputs with NaN.  Block barriers order
-  // the waves ((F): the exchange results ready; (I): phase 2 of tile u done,
-  // which frees its grad_y slot and, for tile u + 1, the operands' buffer;
-  // (A): tile j landed, which also frees every buffer iteration j - 1
-  // read); every wave runs the same iterations, so each barrier is reached
-  // by all four (the bounded waits end, failed or not); a fourth after
-  // (B) gives the publisher every wave's partials of tile j.
+  // the waves ((F): the exchange results ready; (A): tile j landed and
+  // every wave done with phase 2 of tile u, which frees its grad_y slot
+  // and, for tile u + 1, the operands' buffer, and with every buffer
+  // iteration j - 1 read); every wave runs the same iterations, so each
+  // barrier is reached by all four (the bounded waits end, failed or not);
+  // a third after (B) gives the publisher every wave's partials of tile j.
   auto step = [&](int j, u32x4 (&Xr)[2][4]) {
     const int u = j - kBcLag;
     const bool pub_prev = (j & 3) == wave;  // this wave published tile j - 1's record
@@ -500,7 +501,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         const float sc = sk - inv * inv * sd * invK;
         // The tile's shared phase-2 operands for this wave's tokens 4 wave ..
         // 4 wave + 3 (opw held tile u - 1's: every wave finished phase 2 of
-        // it before the barrier of (I) in the last iteration).  Lane l forms
+        // it before the barrier of (A) in the last iteration).  Lane l forms
         // g = grad_mixes * inv of token rt = 4 wave + l / 16 at m0 = 8 fq +
         // 2 fp and m0 + 1 (fq = l / 4 % 4, fp = l % 4; m < 4 from the
         // exchange, whose value (token rt, m) every 16 lanes hold at lane
@@ -623,32 +624,28 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
           __builtin_amdgcn_raw_buffer_store_b128(u32x4{o[e][0], o[e][1], o[e][2], o[e][3]}, rgx, off, 0, 2 /* nt */);
         }
       }
-      // ---- (I) every wave done with tile u (its grad_y slot and operands),
-      // then grad_y / per-token data of tile j + 2 into the slot ---------------
-      bc_sync();
-      if (j + 2 < nq) issue_g(j + 2);
       own = own + 1 == G ? 0 : own + 1;
-    } else if (j + 2 < nq) {
-      issue_g(j + 2);  // (I) a slot not used before
     }
     if (j < nq) {
       // ---- (A) tile j landed ---------------------------------------------
       // operations this wave issued after tile j's x loads (iteration j - 1:
       // poll (npoll = 4), stores (8), grad_y loads (kg), record (its
-      // publisher), x loads (8); iteration j: poll (4), stores (8), grad_y
-      // loads (kg)); away from the steady state all of them
+      // publisher), x loads (8); iteration j: poll (4), stores (8)); away
+      // from the steady state all of them
       static_assert(npoll == 4, "the wait below counts four poll loads an iteration");
       if (j >= 3 && j + 2 < nq)
-        bc_wait_steady<32, 2>(kg, pub_prev);
+        bc_wait_steady<32, 1>(kg, pub_prev);
       else
         wait_vmcnt<0>();
       // Every wave past this point: tile j's x and grad_y slots landed (each
       // wave's own loads, the grad_y ones issued first), and every wave is
-      // done with iteration j - 1, so with tile j - 1's x slot (refilled in
-      // (C) below) and with the publisher's reads of the partial buffer of
-      // tile j - 2 (overwritten in (B)).
+      // done with phase 2 of tile u (its grad_y slot, refilled now, and the
+      // shared operands) and with iteration j - 1, so with tile j - 1's x
+      // slot (refilled in (C) below) and with the publisher's reads of the
+      // partial buffer of tile j - 2 (overwritten in (B)).
       const uint32_t jm3 = (uint32_t)j % 3u;
       bc_sync();
+      if (j + 2 < nq) issue_g(j + 2);
       // ---- (B) phase 1: copy x, grad_pre partial -------------------------
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(j & (kBcSg - 1)) * kBcGSlot;
       const uint32_t xslot = bc_opq(xs_l) + jm3 * 32 * 1024 + (uint32_t)(n * 8192 + 16 * lane);
