@@ -35,10 +35,10 @@
 //   * phase 1 of tile j: copy its x into a ring of two tiles of registers
 //     (freeing the slot) and sum grad_y . x per token over the wave's
 //     columns (v_dot2_f32_bf16), then over the 16 lanes of a row (DPP); the
-//     tile's publisher wave gathers the four streams' partials into the
-//     member's record (16 tokens x 4 streams as 4 chunks of 8 16-byte words,
-//     word w of a chunk (value w, value w + 8, tag, tag)) and stores it to
-//     the group's ring;
+//     member's record of the tile (16 tokens x 4 streams as 4 chunks of 8
+//     16-byte words, word w of a chunk (value w, value w + 8, tag, tag))
+//     goes to the group's ring, each wave storing the 8 words that hold its
+//     stream's sums;
 //   * exchange of tile u: wave w polls chunk w of every member's record (4
 //     direct-to-LDS loads, lane = (member, word)), adds over members in a
 //     fixed order, forms its four tokens' grad_mixes[0..3] and scale, and
@@ -113,22 +113,15 @@ struct BwdCoopArgs {
   uint64_t timeout;
 };
 
-// s_waitcnt vmcnt(BASE + KG * kg + pub) for wave-uniform kg in {2, 3} and
-// pub in {0, 1}: the steady-state counts of the main loop's two waits
-template <int BASE, int KG>
-__device__ __forceinline__ void bc_wait_steady(int kg, bool pub) {
-  static_assert(BASE + 3 * KG + 1 < 64, "vmcnt range");
-  if (kg == 3) {
-    if (pub)
-      wait_vmcnt<BASE + 3 * KG + 1>();
-    else
-      wait_vmcnt<BASE + 3 * KG>();
-  } else {
-    if (pub)
-      wait_vmcnt<BASE + 2 * KG + 1>();
-    else
-      wait_vmcnt<BASE + 2 * KG>();
-  }
+// s_waitcnt vmcnt(BASE + kg) for wave-uniform kg in {2, 3}: the
+// steady-state counts of the main loop's two waits
+template <int BASE>
+__device__ __forceinline__ void bc_wait_steady(int kg) {
+  static_assert(BASE + 3 < 64, "vmcnt range");
+  if (kg == 3)
+    wait_vmcnt<BASE + 3>();
+  else
+    wait_vmcnt<BASE + 2>();
 }
 
 // An opaque copy of a wave-uniform value: what derives from it (LDS slot and
@@ -289,7 +282,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   __shared__ __align__(1024) u32x4 gsl[kBcSg * kBcGSlot / 16];       // 42 KB
   __shared__ __align__(1024) u32x4 pbuf[kBcWaves * kBcPollKB * kWave];  // 16 KB: each wave's poll
   __shared__ __align__(16) uint32_t opw[kBcOpBytes / 4];             // the shared phase-2 operands
-  __shared__ __align__(16) float pp[2][kBcWaves][kBcTT];             // phase-1 partials
   __shared__ __align__(16) float red[kBcWaves][8];                   // end: the waves' contributions
   // counters: abort at 22
   __shared__ uint32_t cnt[32];
@@ -321,7 +313,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   u32x4* recw = a.rec + (size_t)group * kBcR * G * kBcRecWords;
   const auto ring = rows_rsrc(recw, (int64_t)kBcR * G * kBcRecWords * 16);
   const uint32_t xs_l = lds_addr(xs), gs_l = lds_addr(gsl), pb_l = lds_addr(pbuf) + wave * kBcPollKB * 1024;
-  const uint32_t opw_l = lds_addr(opw), pp_l = lds_addr(&pp[0][0][0]);
+  const uint32_t opw_l = lds_addr(opw);
   const uint32_t c_ab = lds_addr(cnt) + 88;
   const int kg = wave < 3 ? 3 : 2;  // grad_y / per-token loads this wave issues per tile
   constexpr int npoll = kBcPollKB;  // poll loads a wave issues per tile
@@ -329,9 +321,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   const float invK = 1.0f / (float)K;
   auto t0_of = [&](int qi) { return (int64_t)(group + qi * ngroups) * kBcTT; };
   auto nv_of = [&](int64_t t0) { return (int)(T - t0 < kBcTT ? T - t0 : kBcTT); };
-  // the publisher of tile j's record (wave w polls and totals chunk w of every
-  // tile): wave (j + 1) % 4
-
   // ---- loads: tile qi's x units of this stream (8), its grad_y units (h, e =
   // wave) and (waves 0..2) a third of the per-token data: wave 0 grad_mixes
   // bytes [0, 1024), wave 1 [1024, 1536) (lanes past 1536 read zeros into the
@@ -426,7 +415,7 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   //       stores,
   //   (A) tile j landed, then tile j + 2's grad_y loads into tile u's slot,
   //       (B) phase 1 of tile j into Xr (the registers phase 2 just
-  //       released), (D) the record of tile j (its publisher), (C) tile
+  //       released), (D) this wave's words of the record of tile j, (C) tile
   //       j + 2's x loads.
   // So only two tiles of x sit in registers at a time.  The poll is issued
   // before this iteration's stores and loads, so it completes after older
@@ -439,21 +428,19 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   // every wave done with phase 2 of tile u, which frees its grad_y slot
   // and, for tile u + 1, the operands' buffer, and with every buffer
   // iteration j - 1 read); every wave runs the same iterations, so each
-  // barrier is reached by all four (the bounded waits end, failed or not);
-  // a third after (B) gives the publisher every wave's partials of tile j.
+  // barrier is reached by all four (the bounded waits end, failed or not).
   auto step = [&](int j, u32x4 (&Xr)[2][4]) {
     const int u = j - kBcLag;
-    const bool pub_prev = (j & 3) == wave;  // this wave published tile j - 1's record
     if (u >= 0 && u < nq) {
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
       // ---- (E) this wave's share of the exchange of tile u -------------------
       {
         // operations issued after the poll (iteration j - 1: stores of tile
-        // u - 1 (8), grad_y loads of tile j + 1 (kg), the record of tile j - 1
-        // (its publisher), x loads of tile j + 1 (8)); away from the steady
-        // state all of them
+        // u - 1 (8), grad_y loads of tile j + 1 (kg), this wave's words of
+        // the record of tile j - 1 (1), x loads of tile j + 1 (8)); away from
+        // the steady state all of them
         if (j >= 3 && j + 1 < nq)
-          bc_wait_steady<16, 1>(kg, pub_prev);
+          bc_wait_steady<17>(kg);
         else
           wait_vmcnt<0>();
         const uint32_t tag = (uint32_t)(u + 1);
@@ -629,20 +616,19 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
     if (j < nq) {
       // ---- (A) tile j landed ---------------------------------------------
       // operations this wave issued after tile j's x loads (iteration j - 1:
-      // poll (npoll = 4), stores (8), grad_y loads (kg), record (its
-      // publisher), x loads (8); iteration j: poll (4), stores (8)); away
-      // from the steady state all of them
+      // poll (npoll = 4), stores (8), grad_y loads (kg), record words (1), x
+      // loads (8); iteration j: poll (4), stores (8)); away from the steady
+      // state all of them
       static_assert(npoll == 4, "the wait below counts four poll loads an iteration");
       if (j >= 3 && j + 2 < nq)
-        bc_wait_steady<32, 1>(kg, pub_prev);
+        bc_wait_steady<33>(kg);
       else
         wait_vmcnt<0>();
       // Every wave past this point: tile j's x and grad_y slots landed (each
       // wave's own loads, the grad_y ones issued first), and every wave is
       // done with phase 2 of tile u (its grad_y slot, refilled now, and the
       // shared operands) and with iteration j - 1, so with tile j - 1's x
-      // slot (refilled in (C) below) and with the publisher's reads of the
-      // partial buffer of tile j - 2 (overwritten in (B)).
+      // slot (refilled in (C) below).
       const uint32_t jm3 = (uint32_t)j % 3u;
       bc_sync();
       if (j + 2 < nq) issue_g(j + 2);
@@ -664,34 +650,21 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) pe[e] = group_sum<15>(pe[e]);  // the 16 lanes of row q: token 4 q + e
-      const int pbi = j & 1;
-      if (r == 0) co_lds_st4(bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + n) * kBcTT + 4 * q) * 4), floatx4{pe[0], pe[1], pe[2], pe[3]});
-      bc_sync();  // every wave's partials of tile j written
-      // ---- (D) the record of tile j -----------------------------------------
-      if (wave == ((j + 1) & 3)) {
-        // lane l < 32: chunk c = l / 8, word w = l % 8 holds values w and w + 8
-        // of the chunk, value v = 4 (token - 4 c) + stream
-        const int ck = (lane >> 3) & 3, wd = lane & 7;
+      // ---- (D) this wave's words of the record of tile j -------------------
+      {
+        // word w of chunk c holds values w and w + 8 of the chunk (value v =
+        // 4 (token - 4 c) + stream), so the words w = n and n + 4 hold this
+        // stream's sums only: lane 16 c + h (row c, whose 16 lanes hold
+        // tokens 4 c .. 4 c + 3 in pe[0..3]) stores word n + 4 h of chunk c,
+        // tokens 4 c + h and 4 c + h + 2
+        const int ck = lane >> 4, h = lane & 1;
         u32x4 word;
-        {
-          // value w: stream w % 4 of token 4 c + w / 4; value w + 8: the same
-          // stream, two tokens later
-          const uint32_t ad = bc_opq(pp_l) + (uint32_t)(((pbi * kBcWaves + (wd & 3)) * kBcTT + 4 * ck + (wd >> 2)) * 4);
-          uint32_t w0, w1;
-          asm volatile(
-              "ds_read_b32 %0, %2\n\t"
-              "ds_read_b32 %1, %2 offset:8\n\t"
-              "s_waitcnt lgkmcnt(0)"
-              : "=&v"(w0), "=&v"(w1)
-              : "v"(ad)
-              : "memory");
-          word[0] = w0;
-          word[1] = w1;
-        }
+        word[0] = __float_as_uint(h ? pe[1] : pe[0]);
+        word[1] = __float_as_uint(h ? pe[3] : pe[2]);
         word[2] = word[3] = (uint32_t)(j + 1);
         const uint32_t off =
-            lane < 4 * kBcChunkWords
-                ? (uint32_t)(((((j & (kBcR - 1)) * 4 + ck) * G + member) * kBcChunkWords + wd) * 16)
+            (lane & 14) == 0
+                ? (uint32_t)(((((j & (kBcR - 1)) * 4 + ck) * G + member) * kBcChunkWords + n + 4 * h) * 16)
                 : kBufferOob;
         // default policy: the line stays in this XCC's L2, where the readers' loads find it
         __builtin_amdgcn_raw_buffer_store_b128(word, ring, off, 0, 0);
