@@ -410,16 +410,15 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   int own = 0;  // (tile u) % G: the member that owns tile u's grad_alpha / grad_base terms
   // Iteration j, with u = j - 2:
   //   (E) this wave's share of the exchange of tile u (chunk `wave`: tokens
-  //       4 wave .. 4 wave + 3), (F) wait for all four shares, (G) this
-  //       wave's poll of tile u + 1, (H) phase 2 of tile u from Xr with its
-  //       stores,
-  //   (A) tile j landed, then tile j + 2's grad_y loads into tile u's slot,
-  //       (B) phase 1 of tile j into Xr (the registers phase 2 just
-  //       released), (D) this wave's words of the record of tile j, (C) tile
-  //       j + 2's x loads.
+  //       4 wave .. 4 wave + 3), (F) wait for all four shares, (H) phase 2
+  //       of tile u from Xr with its stores, (G) this wave's poll of tile
+  //       u + 1,
+  //   (A) tile j landed, (B) phase 1 of tile j into Xr (the registers phase
+  //       2 just released), (D) this wave's words of the record of tile j,
+  //       (C) tile j + 2's grad_y loads into tile u's slot and its x loads.
   // So only two tiles of x sit in registers at a time.  The poll is issued
-  // before this iteration's stores and loads, so it completes after older
-  // work only.  Every index is a 32-bit scalar; every wait on a counter is a
+  // before this iteration's loads, so it completes after older work only.
+  // Every index is a 32-bit scalar; every wait on a counter is a
   // scalar branch.  A wait that gives up (abort flag and status set) lets
   // the loop run to its end on whatever the buffers hold (every later wait
   // returns at once, and the loads and stores stay in range); the sum
@@ -435,12 +434,12 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
       // ---- (E) this wave's share of the exchange of tile u -------------------
       {
-        // operations issued after the poll (iteration j - 1: stores of tile
-        // u - 1 (8), grad_y loads of tile j + 1 (kg), this wave's words of
-        // the record of tile j - 1 (1), x loads of tile j + 1 (8)); away from
-        // the steady state all of them
+        // operations issued after the poll (iteration j - 1: this wave's
+        // words of the record of tile j - 1 (1), grad_y loads of tile j + 1
+        // (kg), x loads of tile j + 1 (8)); away from the steady state all of
+        // them
         if (j >= 3 && j + 1 < nq)
-          bc_wait_steady<17>(kg);
+          bc_wait_steady<9>(kg);
         else
           wait_vmcnt<0>();
         const uint32_t tag = (uint32_t)(u + 1);
@@ -541,9 +540,6 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
       // ---- (F) wait for the four shares -------------------------------------
       bc_sync();
     }
-    // ---- (G) the next tile's poll (this wave's buffer is free once it has
-    // totalled tile u) ---------------------------------------------------------
-    if (u + 1 >= 0 && u + 1 < nq) issue_poll(u + 1);
     if (u >= 0 && u < nq) {
       // ---- (H) phase 2 of tile u --------------------------------------------
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(u & (kBcSg - 1)) * kBcGSlot;
@@ -613,11 +609,16 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
       }
       own = own + 1 == G ? 0 : own + 1;
     }
+    // ---- (G) the next tile's poll (this wave's buffer is free once it has
+    // totalled tile u).  Issued here, after the stores, a load issue that
+    // waits for the memory pipeline to take the stores overlaps the wait for
+    // tile j below, and the records have had most of an iteration to arrive.
+    if (u + 1 >= 0 && u + 1 < nq) issue_poll(u + 1);
     if (j < nq) {
       // ---- (A) tile j landed ---------------------------------------------
       // operations this wave issued after tile j's x loads (iteration j - 1:
-      // poll (npoll = 4), stores (8), grad_y loads (kg), record words (1), x
-      // loads (8); iteration j: poll (4), stores (8)); away from the steady
+      // stores (8), poll (npoll = 4), record words (1), grad_y loads (kg), x
+      // loads (8); iteration j: stores (8), poll (4)); away from the steady
       // state all of them
       static_assert(npoll == 4, "the wait below counts four poll loads an iteration");
       if (j >= 3 && j + 2 < nq)
@@ -626,12 +627,11 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         wait_vmcnt<0>();
       // Every wave past this point: tile j's x and grad_y slots landed (each
       // wave's own loads, the grad_y ones issued first), and every wave is
-      // done with phase 2 of tile u (its grad_y slot, refilled now, and the
-      // shared operands) and with iteration j - 1, so with tile j - 1's x
-      // slot (refilled in (C) below).
+      // done with phase 2 of tile u (its grad_y slot and the shared
+      // operands) and with iteration j - 1, so with tile j - 1's x slot
+      // (both refilled in (C) below).
       const uint32_t jm3 = (uint32_t)j % 3u;
       bc_sync();
-      if (j + 2 < nq) issue_g(j + 2);
       // ---- (B) phase 1: copy x, grad_pre partial -------------------------
       const uint32_t gslot = bc_opq(gs_l) + (uint32_t)(j & (kBcSg - 1)) * kBcGSlot;
       const uint32_t xslot = bc_opq(xs_l) + jm3 * 32 * 1024 + (uint32_t)(n * 8192 + 16 * lane);
@@ -669,7 +669,9 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
         // default policy: the line stays in this XCC's L2, where the readers' loads find it
         __builtin_amdgcn_raw_buffer_store_b128(word, ring, off, 0, 0);
       }
-      // ---- (C) x of tile j + 2 into the slot of tile j - 1 --------------------
+      // ---- (C) grad_y / per-token data of tile j + 2 into tile u's slot, x
+      // of tile j + 2 into the slot of tile j - 1 ------------------------------
+      if (j + 2 < nq) issue_g(j + 2);
       if (j + 2 < nq) {
         issue_x(j + 2);
       }
