@@ -679,20 +679,14 @@ __global__ __launch_bounds__(kBcThreads) void pre_bwd_coop_kernel(BwdCoopArgs a)
   };
 
   {
-    // two tiles of x in registers: XP holds tile j - 2 on entry to iteration
-    // j and tile j on exit, XQ tile j - 1; they swap after each iteration
+    // two tiles of x in registers: XP holds the even tiles and XQ the odd
+    // ones (phase 2 of tile j - 2 and phase 1 of tile j use the same set),
+    // so the loop runs two iterations a trip and the ring never moves
     u32x4 XP[2][4], XQ[2][4];
     const int iters = nq + kBcLag;
-    for (int j = 0; j < iters; ++j) {
+    for (int j = 0; j < iters; j += 2) {
       step(j, XP);
-      // v_swap_b32 exchanges the two registers in place (a swap written in C++
-      // becomes three moves a register)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) asm volatile("v_swap_b32 %0, %1" : "+v"(XP[hh][e][w]), "+v"(XQ[hh][e][w]));
+      if (j + 1 < iters) step(j + 1, XQ);
     }
   }
   wait_vmcnt<0>();  // no direct-to-LDS load may outlive the block
