@@ -202,7 +202,7 @@ inline int coop_max_groups(int G) {
 
 // Per device and kernel kind (`kind` < 4): does one block of the kernel fit a
 // CU (so a grid of one block per CU is resident at once on an otherwise idle
-// device)?
+// device), and does the kernel use no scratch memory?
 inline bool coop_fits(const void* kernel, int threads, int kind) {
   static std::atomic<int> cache[64][4];
   int dev = 0;
@@ -211,7 +211,12 @@ inline bool coop_fits(const void* kernel, int threads, int kind) {
   int v = slot.load(std::memory_order_relaxed);
   if (v) return v > 0;
   int nb = 0;
-  const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1;
+  // the single-pass kernels wait on their loads with exact memory-counter
+  // counts, which scratch (register spill) loads and stores issued by the
+  // compiler would upset: a build with private memory does not run them
+  hipFuncAttributes fa{};
+  const bool ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, 0) == hipSuccess && nb >= 1 &&
+                  hipFuncGetAttributes(&fa, kernel) == hipSuccess && fa.localSizeBytes == 0;
   (void)hipGetLastError();
   slot.store(ok ? 1 : -1, std::memory_order_relaxed);
   return ok;

@@ -61,7 +61,9 @@
 // Memory-counter accounting.  Vector memory operations complete in issue
 // order; each wave waits for a tile's loads and for its poll with s_waitcnt
 // vmcnt(n), n the exact number of operations it issued after them in the
-// steady state (vmcnt(0) near the ends of the loop).
+// steady state (vmcnt(0) near the ends of the loop).  That needs a build
+// without scratch memory (no spill loads or stores among them): the host
+// side runs the kernel only when its private segment is empty.
 #pragma once
 
 #include "coop_common.hpp"
