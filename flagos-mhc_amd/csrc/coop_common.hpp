@@ -166,14 +166,14 @@ __device__ __forceinline__ void co_register(uint32_t* ctl, int G, int maxg, uint
   info[2] = (int)(rank % (uint32_t)G);
 }
 
-// zero `n` 16-byte words (the control words and the exchange ring before a launch)
+// zero `n` 16-byte words (the control words and the exchange ring before a
+// launch) with streaming stores
 namespace {
 __global__ __launch_bounds__(256) void co_zero_kernel(u32x4* p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    u32x4 z;
-    z[0] = z[1] = z[2] = z[3] = 0u;
-    p[i] = z;
-  }
+  u32x4 z;
+  z[0] = z[1] = z[2] = z[3] = 0u;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    __builtin_nontemporal_store(z, p + i);
 }
 }  // namespace
 
